@@ -1,0 +1,363 @@
+// s2x_abi.cpp -- the extern "C" boundary (include/s2x.h): argument checks,
+// status codes, weight objects and the op-level entry points.
+#include "s2x.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "s2x_internal.h"
+#include "s2x_kernels.h"
+
+namespace s2x {
+
+static thread_local std::string g_last_error;
+
+int fail(int status, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(S2X_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+WeightView view_of(const s2x_weight *w) { return w->view; }
+
+}  // namespace s2x
+
+using namespace s2x;
+
+extern "C" {
+
+const char *s2x_status_string(int status) {
+    switch (status) {
+    case S2X_OK: return "ok";
+    case S2X_ERR_INVALID_ARG: return "invalid argument";
+    case S2X_ERR_UNSUPPORTED: return "unsupported";
+    case S2X_ERR_HIP: return "HIP runtime error";
+    case S2X_ERR_WORKSPACE: return "workspace too small";
+    case S2X_ERR_OOM: return "out of device memory";
+    case S2X_ERR_NOT_LOADED: return "encoder not loaded";
+    default: return "unknown status";
+    }
+}
+
+const char *s2x_last_error(void) { return g_last_error.c_str(); }
+
+const char *s2x_version(void) { return "s2x 0.1 gfx950"; }
+
+// ---------------------------------------------------------------------------
+// a1
+// ---------------------------------------------------------------------------
+int s2x_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
+                      void *qs, void *ds, void *stream) {
+    if (M < 0 || K < 0 || K_pad <= 0 || K_pad % QK_ != 0 || K > K_pad || ldx < K)
+        return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: bad shape K=%lld K_pad=%lld ldx=%lld M=%lld",
+                    (long long)K, (long long)K_pad, (long long)ldx, (long long)M);
+    if (M == 0) return S2X_OK;
+    if (!x || !qs || !ds) return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: null pointer");
+    if (!aligned(qs, 4) || !aligned(ds, 4) || !aligned(x, 4))
+        return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: qs/ds/x must be 4-byte aligned");
+    hipError_t e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)qs, (uint32_t *)ds,
+                                        (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize_q8_1 launch");
+}
+
+// ---------------------------------------------------------------------------
+// a2
+// ---------------------------------------------------------------------------
+size_t s2x_weight_bytes(int64_t K_pad, int64_t N) {
+    if (K_pad <= 0 || N <= 0 || K_pad % QK_ != 0) return 0;
+    return weight_planes_bytes(K_pad, N);
+}
+
+int s2x_weight_create_in(const void *raw_dev, int64_t K_pad, int64_t N, void *dev_buf,
+                         void *stream, s2x_weight **out) {
+    if (!out) return fail(S2X_ERR_INVALID_ARG, "weight_create_in: out is null");
+    *out = nullptr;
+    if (K_pad <= 0 || N <= 0 || K_pad % QK_ != 0)
+        return fail(S2X_ERR_INVALID_ARG, "weight_create_in: bad shape K_pad=%lld N=%lld",
+                    (long long)K_pad, (long long)N);
+    if (!raw_dev || !dev_buf || !aligned(raw_dev, 2) || !aligned(dev_buf, 256))
+        return fail(S2X_ERR_INVALID_ARG,
+                    "weight_create_in: raw must be 2-byte and dev_buf 256-byte aligned");
+    s2x_weight *w = new s2x_weight();
+    w->mem = dev_buf;
+    w->owns = false;
+    w->view = planes_view(dev_buf, K_pad, N);
+    hipError_t e = launch_repack_q8_0(raw_dev, K_pad, N, const_cast<int8_t *>(w->view.qs),
+                                      const_cast<float *>(w->view.d), (hipStream_t)stream);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(e, "repack launch");
+    }
+    *out = w;
+    return S2X_OK;
+}
+
+int s2x_weight_create(const void *raw, int raw_is_host, int64_t K_pad, int64_t N, void *stream,
+                      s2x_weight **out) {
+    if (!out) return fail(S2X_ERR_INVALID_ARG, "weight_create: out is null");
+    *out = nullptr;
+    if (K_pad <= 0 || N <= 0 || K_pad % QK_ != 0 || !raw)
+        return fail(S2X_ERR_INVALID_ARG, "weight_create: bad shape K_pad=%lld N=%lld",
+                    (long long)K_pad, (long long)N);
+    int st = weight_upload(raw, raw_is_host != 0, K_pad, N, (hipStream_t)stream, out);
+    if (st != S2X_OK) return st;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) {
+        s2x_weight_destroy(*out);
+        *out = nullptr;
+        return hip_fail(e, "weight_create sync");
+    }
+    return S2X_OK;
+}
+
+void s2x_weight_destroy(s2x_weight *w) {
+    if (!w) return;
+    if (w->owns && w->mem) (void)hipFree(w->mem);
+    delete w;
+}
+
+int64_t s2x_weight_k(const s2x_weight *w) { return w ? w->view.K_pad : 0; }
+int64_t s2x_weight_n(const s2x_weight *w) { return w ? w->view.N : 0; }
+
+// ---------------------------------------------------------------------------
+// a3
+// ---------------------------------------------------------------------------
+static int check_epi(const s2x_epilogue *epi, EpiParams &p) {
+    p = EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0};
+    if (!epi) return S2X_OK;
+    p.kind = epi->kind;
+    p.bias = epi->bias;
+    p.resid = epi->resid;
+    p.ld_resid = epi->ld_resid;
+    p.resid_rows = epi->resid_rows;
+    switch (epi->kind) {
+    case S2X_EPI_NONE: return S2X_OK;
+    case S2X_EPI_BIAS:
+    case S2X_EPI_BIAS_GELU:
+        if (!epi->bias) return fail(S2X_ERR_INVALID_ARG, "epilogue: bias is null");
+        return S2X_OK;
+    case S2X_EPI_BIAS_RESID:
+        if (!epi->bias || !epi->resid || epi->ld_resid <= 0 || epi->resid_rows < 0)
+            return fail(S2X_ERR_INVALID_ARG, "epilogue: bias/resid/ld_resid invalid");
+        return S2X_OK;
+    default: return fail(S2X_ERR_INVALID_ARG, "epilogue: unknown kind %d", epi->kind);
+    }
+}
+
+int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds, int64_t M,
+                          float *y, int64_t ldy, const s2x_epilogue *epi, void *stream) {
+    if (!w) return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: weight is null");
+    if (M < 0 || ldy < w->view.N)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: bad M=%lld or ldy=%lld < N=%lld",
+                    (long long)M, (long long)ldy, (long long)w->view.N);
+    if (M == 0) return S2X_OK;
+    if (M > INT32_MAX / 2) return fail(S2X_ERR_UNSUPPORTED, "mul_mat: M too large");
+    if (!qs || !ds || !y) return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: null pointer");
+    if (!aligned(qs, 16) || !aligned(ds, 4) || !aligned(y, 4))
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: qs must be 16-byte aligned");
+    EpiParams p;
+    int st = check_epi(epi, p);
+    if (st != S2X_OK) return st;
+    hipError_t e = launch_mmq(w->view, (const int8_t *)qs, (const uint32_t *)ds, M, y, ldy, p,
+                              (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
+}
+
+size_t s2x_mul_mat_workspace_size(int64_t K_pad, int64_t N, int64_t M) {
+    if (K_pad <= 0 || N <= 0 || M < 0 || K_pad % QK_ != 0) return 0;
+    return mul_mat_ws_layout(K_pad, N, M).total;
+}
+
+int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const float *x, int64_t K,
+                         int64_t ldx, int64_t M, float *y, void *workspace, size_t ws_bytes,
+                         void *stream) {
+    if (K_pad <= 0 || N <= 0 || K_pad % QK_ != 0 || K <= 0 || K > K_pad || ldx < K || M < 0)
+        return fail(S2X_ERR_INVALID_ARG,
+                    "mul_mat_q8_0_f32: bad shape K=%lld K_pad=%lld N=%lld M=%lld ldx=%lld",
+                    (long long)K, (long long)K_pad, (long long)N, (long long)M, (long long)ldx);
+    if (M == 0) return S2X_OK;
+    if (!w_raw || !x || !y || !workspace)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_f32: null pointer");
+    const MulMatWs L = mul_mat_ws_layout(K_pad, N, M);
+    if (ws_bytes < L.total)
+        return fail(S2X_ERR_WORKSPACE, "mul_mat_q8_0_f32: workspace %zu < %zu bytes", ws_bytes,
+                    L.total);
+    if (!aligned(workspace, 256) || !aligned(w_raw, 2) || !aligned(x, 4) || !aligned(y, 4))
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_f32: misaligned pointer");
+    uint8_t *ws = (uint8_t *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    const WeightView wv = planes_view(ws + L.w_off, K_pad, N);
+    hipError_t e = launch_repack_q8_0(w_raw, K_pad, N, const_cast<int8_t *>(wv.qs),
+                                      const_cast<float *>(wv.d), s);
+    if (e != hipSuccess) return hip_fail(e, "repack launch");
+    e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)(ws + L.qs_off),
+                             (uint32_t *)(ws + L.ds_off), s);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
+    e = launch_mmq(wv, (const int8_t *)(ws + L.qs_off), (const uint32_t *)(ws + L.ds_off), M, y, N,
+                   p, s);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
+}
+
+int s2x_block_dots(const s2x_weight *w, const void *qs, int64_t M, int64_t kb, int32_t *out,
+                   void *stream) {
+    if (!w || !qs || !out) return fail(S2X_ERR_INVALID_ARG, "block_dots: null pointer");
+    if (M <= 0 || kb < 0 || kb >= w->view.K_pad / QK_)
+        return fail(S2X_ERR_INVALID_ARG, "block_dots: bad M=%lld or kb=%lld", (long long)M,
+                    (long long)kb);
+    if (!aligned(qs, 16)) return fail(S2X_ERR_INVALID_ARG, "block_dots: qs must be 16-byte aligned");
+    // the integer stage reads no scales (the EPI_DUMP_I kernel skips them)
+    EpiParams p{EPI_DUMP_I, nullptr, nullptr, 0, 0, kb};
+    hipError_t e = launch_mmq(w->view, (const int8_t *)qs, nullptr, M, reinterpret_cast<float *>(out),
+                              w->view.N, p, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "block dots launch");
+}
+
+// ---------------------------------------------------------------------------
+// a4 / a5
+// ---------------------------------------------------------------------------
+static int check_ln(const float *x, int64_t H, int64_t M, int64_t ldx, const char *who) {
+    if (H <= 0 || H % QK_ != 0 || H > 2048 || M < 0 || ldx < H)
+        return fail(S2X_ERR_INVALID_ARG, "%s: bad shape H=%lld M=%lld ldx=%lld", who,
+                    (long long)H, (long long)M, (long long)ldx);
+    if (M > 0 && !x) return fail(S2X_ERR_INVALID_ARG, "%s: x is null", who);
+    return S2X_OK;
+}
+
+int s2x_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
+                  const float *b, float eps, float *y, int64_t ldy, void *stream) {
+    int st = check_ln(x, H, M, ldx, "layernorm");
+    if (st != S2X_OK) return st;
+    if (M == 0) return S2X_OK;
+    if (!y || ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm: y null or ldy < H");
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, nullptr, nullptr, y, ldy,
+                                    (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
+}
+
+int s2x_layernorm_quantize_q8_1(const float *x, int64_t H, int64_t M, int64_t ldx,
+                                const float *w, const float *b, float eps, void *qs, void *ds,
+                                float *y, int64_t ldy, void *stream) {
+    int st = check_ln(x, H, M, ldx, "layernorm_quantize");
+    if (st != S2X_OK) return st;
+    if (M == 0) return S2X_OK;
+    if (!qs || !ds || !aligned(qs, 4) || !aligned(ds, 4))
+        return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: qs/ds null or misaligned");
+    if (y && ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: ldy < H");
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, (int8_t *)qs, (uint32_t *)ds, y, ldy,
+                                    (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm_quantize launch");
+}
+
+int s2x_bias_residual(const float *mm, const float *bias, const float *resid, float *y,
+                      int64_t H, int64_t n_pos, void *stream) {
+    if (H <= 0 || n_pos < 0) return fail(S2X_ERR_INVALID_ARG, "bias_residual: bad shape");
+    if (n_pos == 0) return S2X_OK;
+    if (!mm || !bias || !resid || !y) return fail(S2X_ERR_INVALID_ARG, "bias_residual: null");
+    hipError_t e = launch_bias_residual(mm, bias, resid, y, H, n_pos, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "bias_residual launch");
+}
+
+int s2x_bias_gelu(const float *mm, const float *bias, float *y, int64_t H, int64_t n_pos,
+                  void *stream) {
+    if (H <= 0 || n_pos < 0) return fail(S2X_ERR_INVALID_ARG, "bias_gelu: bad shape");
+    if (n_pos == 0) return S2X_OK;
+    if (!mm || !bias || !y) return fail(S2X_ERR_INVALID_ARG, "bias_gelu: null");
+    hipError_t e = launch_bias_gelu(mm, bias, y, H, n_pos, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "bias_gelu launch");
+}
+
+// ---------------------------------------------------------------------------
+// a6 / a7
+// ---------------------------------------------------------------------------
+static int check_attn_shape(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head,
+                            const char *who) {
+    if (n_seg < 0 || max_len <= 0 || n_head <= 0 || d_head <= 0)
+        return fail(S2X_ERR_INVALID_ARG, "%s: bad shape", who);
+    const AttnLayout L = attn_layout(n_seg, max_len, n_head, d_head);
+    if (L.d_pad != 80 || L.dv_pad != 96 || d_head % 4 != 0)
+        return fail(S2X_ERR_UNSUPPORTED, "%s: d_head %lld not supported (needs 65..80, %%4)", who,
+                    (long long)d_head);
+    return S2X_OK;
+}
+
+size_t s2x_attn_workspace_size(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head) {
+    if (n_seg < 0 || max_len <= 0 || n_head <= 0 || d_head <= 0) return 0;
+    return attn_layout(n_seg, max_len, n_head, d_head).bytes;
+}
+
+int s2x_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                  const int32_t *seg_start_dev, const int32_t *seg_len_dev, int64_t n_seg,
+                  int64_t max_len, int64_t n_head, int64_t d_head, void *ws, size_t ws_bytes,
+                  void *stream) {
+    int st = check_attn_shape(n_seg, max_len, n_head, d_head, "attn_prep");
+    if (st != S2X_OK) return st;
+    if (n_seg == 0) return S2X_OK;
+    const AttnLayout L = attn_layout(n_seg, max_len, n_head, d_head);
+    if (!qkv || !qkv_bias || !seg_start_dev || !seg_len_dev || !ws)
+        return fail(S2X_ERR_INVALID_ARG, "attn_prep: null pointer");
+    if (ws_bytes < L.bytes) return fail(S2X_ERR_WORKSPACE, "attn_prep: workspace too small");
+    if (ld_qkv < 3 * n_head * d_head || !aligned(ws, 256))
+        return fail(S2X_ERR_INVALID_ARG, "attn_prep: ld_qkv < 3H or ws misaligned");
+    hipError_t e = launch_attn_prep(qkv, ld_qkv, qkv_bias, seg_start_dev, seg_len_dev, L, ws,
+                                    (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "attn_prep launch");
+}
+
+int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
+                 const int32_t *seg_len_dev, const uint8_t *key_valid, int64_t n_seg,
+                 int64_t max_len, int64_t n_head, int64_t d_head, float scale, float *out,
+                 int64_t ld_out, void *stream) {
+    int st = check_attn_shape(n_seg, max_len, n_head, d_head, "attn_run");
+    if (st != S2X_OK) return st;
+    if (n_seg == 0) return S2X_OK;
+    const AttnLayout L = attn_layout(n_seg, max_len, n_head, d_head);
+    if (!ws || !seg_start_dev || !seg_len_dev || !out)
+        return fail(S2X_ERR_INVALID_ARG, "attn_run: null pointer");
+    if (ws_bytes < L.bytes) return fail(S2X_ERR_WORKSPACE, "attn_run: workspace too small");
+    if (ld_out < n_head * d_head || ld_out % 4 != 0 || !aligned(out, 16))
+        return fail(S2X_ERR_INVALID_ARG, "attn_run: out must be 16-byte aligned, ld_out %% 4 == 0");
+    hipError_t e = launch_attn(ws, seg_start_dev, seg_len_dev, key_valid, L, scale, out, ld_out,
+                               (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "attn launch");
+}
+
+// ---------------------------------------------------------------------------
+// a8 / a11
+// ---------------------------------------------------------------------------
+int s2x_resize_pos_embed(const float *pos, int64_t n_side, int64_t H, int64_t out_h,
+                         int64_t out_w, float *out, void *stream) {
+    if (n_side <= 0 || H <= 0 || out_h <= 0 || out_w <= 0 || !pos || !out)
+        return fail(S2X_ERR_INVALID_ARG, "resize_pos_embed: bad arguments");
+    if (2 * n_side > out_h * 32 || 2 * n_side > out_w * 32)
+        return fail(S2X_ERR_UNSUPPORTED, "resize_pos_embed: downscale factor too large");
+    hipError_t e = launch_resize_pos_embed(pos, n_side, H, out_h, out_w, out, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "resize launch");
+}
+
+int s2x_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows_table, const int32_t *ids,
+                      int64_t n_ids, const float *add, int64_t add_rows, float *out,
+                      void *stream) {
+    if (K <= 0 || K % QK_ != 0 || n_rows_table <= 0 || n_ids < 0 || (add && add_rows <= 0))
+        return fail(S2X_ERR_INVALID_ARG, "get_rows_q8_0: bad shape");
+    if (n_ids == 0) return S2X_OK;
+    if (!table_raw || !ids || !out) return fail(S2X_ERR_INVALID_ARG, "get_rows_q8_0: null");
+    hipError_t e = launch_get_rows_q8_0(table_raw, K, n_rows_table, ids, n_ids, add, add_rows, out,
+                                        (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "get_rows launch");
+}
+
+}  // extern "C"

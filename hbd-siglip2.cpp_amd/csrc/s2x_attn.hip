@@ -1,0 +1,374 @@
+// s2x_attn.hip -- bidirectional multi-head attention for SigLIP2 (d_head 72)
+// on gfx950 f16 MFMA, over packed variable-length segments.
+//
+// Staging (k_attn_prep) replaces the reference's QKV bias + split + pad +
+// f16 cast (src/cuda/siglip2_megakernel.cu:160-267): from the QKV GEMM rows
+// [q | k | v] (+ bias) it writes, per segment and head,
+//   Q  [len_pad][d_pad]  f16   (d zero-padded 72 -> 80)
+//   K  [len_pad][d_pad]  f16
+//   Vt [dv_pad][len_pad] f16   (V transposed, d zero-padded 72 -> 96)
+// (len_pad = segment length rounded up to 128)
+// with every padding slot an exact zero.
+//
+// Flash attention (k_attn) computes S^T = K Q^T with v_mfma_f32_32x32x16_f16
+// so that the result layout puts one query per lane (column l & 31) and 16
+// keys per lane in registers: the online-softmax max / sum are lane-local
+// plus one exchange with lane l ^ 32, and the P values are already in the
+// B-operand layout of the next product O^T = V^T P^T, whose result again
+// holds one query per lane -- no shuffles of P or of the output rescale.
+//
+// k-index convention for an f16 32x32x16 MFMA operand: lane l, slot s <-> k
+// = 8*(s/4) + 4*(l/32) + s%4 for the P V product (the layout P has as an S^T
+// result) and k = 8*(l/32) + s for Q K^T.  A and B use the same convention,
+// so the contraction is complete whatever the hardware's own k order is.
+#include "s2x_device.h"
+#include "s2x_kernels.h"
+
+namespace s2x {
+
+static inline int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+
+AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head) {
+    AttnLayout L;
+    L.n_seg = n_seg;
+    L.max_len = max_len;
+    L.n_head = n_head;
+    L.d_head = d_head;
+    L.d_pad = round_up(d_head, 16);
+    L.dv_pad = round_up(d_head, 32);
+    L.len_pad = round_up(max_len, 128);  // whole 128-query tiles stay in bounds
+    const size_t qk = (size_t)(n_seg * n_head * L.len_pad * L.d_pad) * 2;
+    const size_t vt = (size_t)(n_seg * n_head * L.dv_pad * L.len_pad) * 2;
+    L.q_off = 0;
+    L.k_off = round_up((int64_t)qk, 256);
+    L.vt_off = L.k_off + round_up((int64_t)qk, 256);
+    L.bytes = L.vt_off + round_up((int64_t)vt, 256);
+    return L;
+}
+
+// ---------------------------------------------------------------------------
+// staging: one workgroup per (64-position tile, head, segment)
+// ---------------------------------------------------------------------------
+constexpr int PREP_T = 64;
+
+__global__ __launch_bounds__(256) void k_attn_prep(
+    const float *__restrict__ qkv, int64_t ld, const float *__restrict__ bias,
+    const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len, int n_head,
+    int d_head, int d_pad, int dv_pad, int len_pad, _Float16 *__restrict__ Q,
+    _Float16 *__restrict__ K, _Float16 *__restrict__ Vt) {
+    __shared__ _Float16 vs[PREP_T][97];  // one tile of V, d <= 96
+    const int tile = blockIdx.x, h = blockIdx.y, sg = blockIdx.z;
+    const int p0 = tile * PREP_T;
+    const int len = seg_len[sg];
+    const int64_t row0 = seg_start[sg];
+    const int H = n_head * d_head;
+    const int64_t head_qk = ((int64_t)sg * n_head + h) * len_pad * d_pad;
+    const int64_t head_vt = ((int64_t)sg * n_head + h) * dv_pad * len_pad;
+
+    // Q and K rows: element (p, d) of the tile, d fastest
+    for (int i = threadIdx.x; i < PREP_T * d_pad; i += blockDim.x) {
+        const int p = i / d_pad, d = i % d_pad;
+        const int pos = p0 + p;
+        float q = 0.0f, k = 0.0f;
+        if (pos < len && d < d_head) {
+            const float *r = qkv + (row0 + pos) * ld + h * d_head + d;
+            q = r[0] + bias[h * d_head + d];
+            k = r[H] + bias[H + h * d_head + d];
+        }
+        Q[head_qk + (int64_t)pos * d_pad + d] = (_Float16)q;
+        K[head_qk + (int64_t)pos * d_pad + d] = (_Float16)k;
+    }
+    // V tile into LDS (d fastest reads), then transposed out (p fastest writes)
+    for (int i = threadIdx.x; i < PREP_T * dv_pad; i += blockDim.x) {
+        const int p = i / dv_pad, d = i % dv_pad;
+        const int pos = p0 + p;
+        float v = 0.0f;
+        if (pos < len && d < d_head)
+            v = qkv[(row0 + pos) * ld + 2 * H + h * d_head + d] + bias[2 * H + h * d_head + d];
+        vs[p][d] = (_Float16)v;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < PREP_T * dv_pad; i += blockDim.x) {
+        const int d = i / PREP_T, p = i % PREP_T;
+        Vt[head_vt + (int64_t)d * len_pad + p0 + p] = vs[p][d];
+    }
+}
+
+hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                            const int32_t *seg_start, const int32_t *seg_len,
+                            const AttnLayout &L, void *ws, hipStream_t stream) {
+    if (L.n_seg == 0) return hipSuccess;
+    uint8_t *base = reinterpret_cast<uint8_t *>(ws);
+    const dim3 grid((unsigned)(L.len_pad / PREP_T), (unsigned)L.n_head, (unsigned)L.n_seg);
+    hipLaunchKernelGGL(k_attn_prep, grid, dim3(256), 0, stream, qkv, ld_qkv, qkv_bias,
+                       seg_start, seg_len, (int)L.n_head, (int)L.d_head, (int)L.d_pad,
+                       (int)L.dv_pad, (int)L.len_pad,
+                       reinterpret_cast<_Float16 *>(base + L.q_off),
+                       reinterpret_cast<_Float16 *>(base + L.k_off),
+                       reinterpret_cast<_Float16 *>(base + L.vt_off));
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// flash attention: one workgroup = 4 waves x 32 queries of one (segment,
+// head); 64-key tiles of K and V^T staged through LDS (double buffered).
+// Specialised for d_pad = 80 (5 k-steps) and dv_pad = 96 (3 row tiles).
+// ---------------------------------------------------------------------------
+constexpr int FA_DP = 80;              // Q/K row length (halves)
+constexpr int FA_DV = 96;              // V^T rows
+constexpr int FA_KT = 64;              // keys per LDS tile
+constexpr int FA_KP = FA_DP + 8;       // K tile pitch (halves): conflict-free 16-byte reads
+constexpr int FA_VP = FA_KT + 4;       // V^T tile pitch (halves): conflict-free 8-byte reads
+constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
+
+__global__ __launch_bounds__(256) void k_attn(
+    const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
+    const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
+    const int32_t *__restrict__ seg_len, const uint8_t *__restrict__ key_valid,
+    int n_head, int d_head, int len_pad, float scale_log2, float *__restrict__ out,
+    int64_t ld_out) {
+    __shared__ __align__(16) _Float16 lds[2 * FA_STAGE];
+    const int qt = blockIdx.x, h = blockIdx.y, sg = blockIdx.z;
+    const int len = seg_len[sg];
+    if (qt * 128 >= len) return;  // whole workgroup past the segment
+    const int64_t row0 = seg_start[sg];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int64_t head_qk = ((int64_t)sg * n_head + h) * len_pad * FA_DP;
+    const int64_t head_vt = ((int64_t)sg * n_head + h) * FA_DV * len_pad;
+    const _Float16 *Kh = K + head_qk;
+    const _Float16 *Vh = Vt + head_vt;
+
+    // Q^T fragments (B operand): lane holds query q, d = 16 t + 8 lh + s
+    const int q = qt * 128 + wave * 32 + lr;
+    v8h qf[5];
+#pragma unroll
+    for (int t = 0; t < 5; ++t)
+        qf[t] = *reinterpret_cast<const v8h *>(Q + head_qk + (int64_t)q * FA_DP + 16 * t + 8 * lh);
+
+    v16f o[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int n_tiles = (len + FA_KT - 1) / FA_KT;
+
+    // global -> registers for one key tile: K 64x80 halves (10240 B contiguous),
+    // V^T 96 rows x 64 halves (128 B each)
+    uint4 kr[3], vr[3];
+    auto gload = [&](int t) {
+        const int k0 = t * FA_KT;
+        const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int c = tid + i * 256;  // 640 chunks of 16 B
+            if (c < FA_KT * FA_DP / 8) kr[i] = ks[c];
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
+            const int r = c >> 3, cc = (c & 7) * 8;
+            vr[i] = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
+        }
+    };
+    auto sstore = [&](int buf) {
+        _Float16 *kl = lds + buf * FA_STAGE;
+        _Float16 *vl = kl + FA_KT * FA_KP;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int c = tid + i * 256;
+            if (c < FA_KT * FA_DP / 8) {
+                const int r = c / 10, cc = (c % 10) * 8;
+                *reinterpret_cast<uint4 *>(kl + r * FA_KP + cc) = kr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int c = tid + i * 256;
+            const int r = c >> 3, cc = (c & 7) * 8;
+            uint2 *dst = reinterpret_cast<uint2 *>(vl + r * FA_VP + cc);  // 8-byte aligned
+            dst[0] = make_uint2(vr[i].x, vr[i].y);
+            dst[1] = make_uint2(vr[i].z, vr[i].w);
+        }
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < n_tiles) gload(t + 1);
+        const _Float16 *kl = lds + buf * FA_STAGE;
+        const _Float16 *vl = kl + FA_KT * FA_KP;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int kbase = t * FA_KT + sub * 32;
+            // S^T (32 keys x 32 queries)
+            v16f s = {};
+#pragma unroll
+            for (int st = 0; st < 5; ++st) {
+                const v8h kf = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
+            }
+            // scale, mask, tile max
+            float mt = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kbase + 8 * (r >> 2) + 4 * lh + (r & 3);
+                bool ok = key < len;
+                if (key_valid) ok = ok && key_valid[row0 + min(key, len - 1)] != 0;
+                const float v = ok ? s[r] * scale_log2 : -INFINITY;
+                s[r] = v;
+                mt = fmaxf(mt, v);
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            m_run = m_new;
+            float ps = 0.0f;
+            v8h pf[2];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
+                ps = ps + p;
+                pf[r >> 3][r & 7] = (_Float16)p;
+            }
+            l_run = l_run * alpha + ps;
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
+            // O^T += V^T P^T
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const _Float16 *vp = vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 4 * lh;
+                    const v4h lo = *reinterpret_cast<const v4h *>(vp);
+                    const v4h hi = *reinterpret_cast<const v4h *>(vp + 8);
+                    const v8h vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[hh], o[j], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float inv = 1.0f / l_tot;
+    if (q < len) {
+        float *orow = out + (row0 + q) * ld_out + h * d_head;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = j * 32 + 8 * g + 4 * lh;
+                if (d < d_head) {
+                    const float4 v = make_float4(o[j][4 * g] * inv, o[j][4 * g + 1] * inv,
+                                                 o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv);
+                    *reinterpret_cast<float4 *>(orow + d) = v;
+                }
+            }
+    }
+}
+
+hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
+                       const uint8_t *key_valid, const AttnLayout &L, float scale,
+                       float *out, int64_t ld_out, hipStream_t stream) {
+    if (L.n_seg == 0) return hipSuccess;
+    if (L.d_pad != FA_DP || L.dv_pad != FA_DV || (L.d_head % 4) != 0) return hipErrorInvalidValue;
+    const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
+    const float log2e = 1.4426950408889634f;
+    const dim3 grid((unsigned)((L.max_len + 127) / 128), (unsigned)L.n_head, (unsigned)L.n_seg);
+    hipLaunchKernelGGL(k_attn, grid, dim3(256), 0, stream,
+                       reinterpret_cast<const _Float16 *>(base + L.q_off),
+                       reinterpret_cast<const _Float16 *>(base + L.k_off),
+                       reinterpret_cast<const _Float16 *>(base + L.vt_off), seg_start, seg_len,
+                       key_valid, (int)L.n_head, (int)L.d_head, (int)L.len_pad,
+                       scale * log2e, out, ld_out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// single-query attention for the MAP probe head (src/siglip2_vision.cpp:
+// 249-295): the probe query against one segment's keys, K and V rounded to
+// f16 as the reference's FA inputs are.  One workgroup per (head, segment).
+// ---------------------------------------------------------------------------
+constexpr int A1_MAXLEN = (int)MAX_SEG_LEN;
+
+__global__ __launch_bounds__(256) void k_attn_1q(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    int64_t ld, const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len,
+    int n_head, int d_head, float scale, float *__restrict__ out) {
+    __shared__ float p[A1_MAXLEN];
+    __shared__ float red[256];
+    __shared__ float part[4][128];
+    const int h = blockIdx.x, sg = blockIdx.y;
+    const int len = seg_len[sg];
+    const int64_t row0 = seg_start[sg];
+    const int H = n_head * d_head;
+    const float *qh = q + h * d_head;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < len; j += 256) {
+        const float *kr = k + (row0 + j) * ld + h * d_head;
+        float acc = 0.0f;
+        for (int d = 0; d < d_head; ++d) acc = fmaf(qh[d], (float)(_Float16)kr[d], acc);
+        const float s = acc * scale;
+        p[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    mx = red[0];
+    __syncthreads();
+    float sum = 0.0f;
+    for (int j = threadIdx.x; j < len; j += 256) {
+        const float e = expf(p[j] - mx);
+        p[j] = e;
+        sum += e;
+    }
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + o];
+        __syncthreads();
+    }
+    const float den = red[0];
+    // out[d] = sum_j p_j v[j][d] / den: 4 key groups x up to 128 dims
+    const int grp = threadIdx.x >> 6, dl = threadIdx.x & 63;
+    for (int d0 = 0; d0 < d_head; d0 += 64) {
+        const int d = d0 + dl;
+        float acc = 0.0f;
+        if (d < d_head)
+            for (int j = grp; j < len; j += 4)
+                acc = fmaf(p[j], (float)(_Float16)v[(row0 + j) * ld + h * d_head + d], acc);
+        part[grp][dl] = acc;
+        __syncthreads();
+        if (grp == 0 && d < d_head)
+            out[(int64_t)sg * H + h * d_head + d] =
+                ((part[0][dl] + part[1][dl]) + (part[2][dl] + part[3][dl])) / den;
+        __syncthreads();
+    }
+}
+
+hipError_t launch_attn_1q(const float *q, const float *k, const float *v, int64_t ld,
+                          const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
+                          int64_t n_head, int64_t d_head, float scale, float *out,
+                          hipStream_t stream) {
+    if (n_seg == 0) return hipSuccess;
+    if (d_head > 128) return hipErrorInvalidValue;  // the PV pass covers 2 x 64 dims
+    hipLaunchKernelGGL(k_attn_1q, dim3((unsigned)n_head, (unsigned)n_seg), dim3(256), 0, stream,
+                       q, k, v, ld, seg_start, seg_len, (int)n_head, (int)d_head, scale, out);
+    return hipGetLastError();
+}
+
+}  // namespace s2x

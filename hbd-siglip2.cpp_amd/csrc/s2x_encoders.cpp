@@ -1,0 +1,765 @@
+// s2x_encoders.cpp -- the SigLIP2 vision and text towers on the gfx950
+// kernels, behind the s2x_vision_* / s2x_text_* C-ABI.
+//
+// Graph (src/siglip2_vision.cpp:181-244, 601-758; src/siglip2_text.cpp:
+// 115-205, 564-932), restated as a fixed launch sequence per block:
+//   LN1+Q8_1 -> QKV GEMM -> attention staging (bias, f16, V^T) -> flash
+//   attention -> Q8_1 -> O GEMM (+bias +residual, in place) -> LN2+Q8_1 ->
+//   FC1 GEMM (+bias, GELU) -> Q8_1 (K padded 4304 -> 4320) -> FC2 GEMM
+//   (+bias +residual, in place)
+// Tokens of all images are packed into one row range (M = sum of patch
+// counts); attention runs per image segment, so a batch of 32 images is one
+// GEMM of M = 23328 rows per weight.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <utility>
+#include <vector>
+
+#include "s2x.h"
+#include "s2x_internal.h"
+#include "s2x_kernels.h"
+
+namespace s2x {
+
+#define S2X_HIP_TRY(expr)                                       \
+    do {                                                        \
+        hipError_t e__ = (expr);                                \
+        if (e__ != hipSuccess) return hip_fail(e__, #expr);     \
+    } while (0)
+
+#define S2X_TRY(expr)                                           \
+    do {                                                        \
+        int s__ = (expr);                                       \
+        if (s__ != S2X_OK) return s__;                          \
+    } while (0)
+
+int weight_upload(const void *raw, bool is_host, int64_t K_pad, int64_t N, hipStream_t stream,
+                  s2x_weight **out) {
+    *out = nullptr;
+    const size_t raw_bytes = (size_t)(N * (K_pad / QK_)) * 34;
+    const void *src = raw;
+    void *tmp = nullptr;
+    if (is_host) {
+        if (hipMalloc(&tmp, raw_bytes) != hipSuccess)
+            return fail(S2X_ERR_OOM, "weight upload: hipMalloc(%zu) failed", raw_bytes);
+        hipError_t e = hipMemcpy(tmp, raw, raw_bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(tmp);
+            return hip_fail(e, "weight upload copy");
+        }
+        src = tmp;
+    }
+    void *planes = nullptr;
+    if (hipMalloc(&planes, weight_planes_bytes(K_pad, N)) != hipSuccess) {
+        if (tmp) (void)hipFree(tmp);
+        return fail(S2X_ERR_OOM, "weight upload: hipMalloc planes failed");
+    }
+    s2x_weight *w = new s2x_weight();
+    w->mem = planes;
+    w->owns = true;
+    w->view = planes_view(planes, K_pad, N);
+    hipError_t e = launch_repack_q8_0(src, K_pad, N, const_cast<int8_t *>(w->view.qs),
+                                      const_cast<float *>(w->view.d), stream);
+    if (e == hipSuccess && tmp) e = hipStreamSynchronize(stream);
+    if (tmp) (void)hipFree(tmp);
+    if (e != hipSuccess) {
+        (void)hipFree(planes);
+        delete w;
+        return hip_fail(e, "weight repack");
+    }
+    *out = w;
+    return S2X_OK;
+}
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    template <class T> T *as() const { return reinterpret_cast<T *>(p); }
+};
+
+// Grow a device buffer; waits for `stream` before releasing the old one.
+int ensure(DevBuf &b, size_t bytes, hipStream_t stream) {
+    if (b.n >= bytes && b.p) return S2X_OK;
+    if (b.p) {
+        S2X_HIP_TRY(hipStreamSynchronize(stream));
+        (void)hipFree(b.p);
+        b.p = nullptr;
+        b.n = 0;
+    }
+    const size_t n = (size_t)round_up_i((int64_t)bytes, 4096);
+    if (hipMalloc(&b.p, n) != hipSuccess) {
+        b.p = nullptr;
+        return fail(S2X_ERR_OOM, "hipMalloc(%zu) failed", n);
+    }
+    b.n = n;
+    return S2X_OK;
+}
+
+int upload_f32(const float *host, int64_t n, float **dev, const char *what) {
+    *dev = nullptr;
+    if (!host) return fail(S2X_ERR_INVALID_ARG, "missing tensor %s", what);
+    if (hipMalloc(reinterpret_cast<void **>(dev), sizeof(float) * (size_t)n) != hipSuccess)
+        return fail(S2X_ERR_OOM, "hipMalloc for %s failed", what);
+    S2X_HIP_TRY(hipMemcpy(*dev, host, sizeof(float) * (size_t)n, hipMemcpyHostToDevice));
+    return S2X_OK;
+}
+
+int upload_q8(const void *raw, int64_t K_pad, int64_t N, hipStream_t s, s2x_weight **w,
+              const char *what) {
+    if (!raw) return fail(S2X_ERR_INVALID_ARG, "missing tensor %s", what);
+    return weight_upload(raw, true, K_pad, N, s, w);
+}
+
+struct DevLayer {
+    s2x_weight *qkv = nullptr, *o = nullptr, *up = nullptr, *down = nullptr;
+    float *ln1_w = nullptr, *ln1_b = nullptr, *qkv_b = nullptr, *o_b = nullptr;
+    float *ln2_w = nullptr, *ln2_b = nullptr, *up_b = nullptr, *down_b = nullptr;
+    void release() {
+        s2x_weight_destroy(qkv);
+        s2x_weight_destroy(o);
+        s2x_weight_destroy(up);
+        s2x_weight_destroy(down);
+        for (float *p : {ln1_w, ln1_b, qkv_b, o_b, ln2_w, ln2_b, up_b, down_b})
+            if (p) (void)hipFree(p);
+    }
+};
+
+// hipEvent pairs around GEMM launches, for the roofline report
+struct GemmTiming {
+    bool on = false;
+    struct Rec {
+        hipEvent_t a, b;
+        double ops;
+    };
+    std::vector<Rec> pending;
+    std::vector<hipEvent_t> pool;
+    double ms = 0.0, ops = 0.0;
+    int64_t launches = 0;
+    hipEvent_t get() {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        (void)hipEventCreate(&e);
+        return e;
+    }
+    int collect(hipStream_t s) {
+        if (pending.empty()) return S2X_OK;
+        S2X_HIP_TRY(hipStreamSynchronize(s));
+        for (auto &r : pending) {
+            float t = 0.0f;
+            S2X_HIP_TRY(hipEventElapsedTime(&t, r.a, r.b));
+            ms += t;
+            ops += r.ops;
+            launches += 1;
+            pool.push_back(r.a);
+            pool.push_back(r.b);
+        }
+        pending.clear();
+        return S2X_OK;
+    }
+    ~GemmTiming() {
+        for (auto &r : pending) {
+            (void)hipEventDestroy(r.a);
+            (void)hipEventDestroy(r.b);
+        }
+        for (auto e : pool) (void)hipEventDestroy(e);
+    }
+};
+
+// The transformer stack shared by both towers.
+struct Tower {
+    int64_t H = 0, F = 0, F_pad = 0, n_head = 0, d_head = 0, n_layer = 0;
+    float eps = 1e-6f;
+    std::vector<DevLayer> layers;
+    hipStream_t own = nullptr, stream = nullptr;
+    DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid;
+    GemmTiming timing;
+
+    ~Tower() {
+        for (auto &L : layers) L.release();
+        if (own) (void)hipStreamDestroy(own);
+    }
+
+    int init_stream() {
+        S2X_HIP_TRY(hipStreamCreateWithFlags(&own, hipStreamNonBlocking));
+        stream = own;
+        return S2X_OK;
+    }
+
+    int load_layers(const s2x_layer_weights *lw, int64_t n) {
+        if (!lw) return fail(S2X_ERR_INVALID_ARG, "layers array is null");
+        layers.resize((size_t)n);
+        for (int64_t l = 0; l < n; ++l) {
+            const s2x_layer_weights &s = lw[l];
+            DevLayer &d = layers[(size_t)l];
+            S2X_TRY(upload_f32(s.ln1_w, H, &d.ln1_w, "ln1.weight"));
+            S2X_TRY(upload_f32(s.ln1_b, H, &d.ln1_b, "ln1.bias"));
+            S2X_TRY(upload_q8(s.qkv_w, H, 3 * H, stream, &d.qkv, "attn_qkv.weight"));
+            S2X_TRY(upload_f32(s.qkv_b, 3 * H, &d.qkv_b, "attn_qkv.bias"));
+            S2X_TRY(upload_q8(s.o_w, H, H, stream, &d.o, "attn_o.weight"));
+            S2X_TRY(upload_f32(s.o_b, H, &d.o_b, "attn_o.bias"));
+            S2X_TRY(upload_f32(s.ln2_w, H, &d.ln2_w, "ln2.weight"));
+            S2X_TRY(upload_f32(s.ln2_b, H, &d.ln2_b, "ln2.bias"));
+            S2X_TRY(upload_q8(s.up_w, H, F, stream, &d.up, "ffn_up.weight"));
+            S2X_TRY(upload_f32(s.up_b, F, &d.up_b, "ffn_up.bias"));
+            S2X_TRY(upload_q8(s.down_w, F_pad, H, stream, &d.down, "ffn_down.weight"));
+            S2X_TRY(upload_f32(s.down_b, H, &d.down_b, "ffn_down.bias"));
+        }
+        return S2X_OK;
+    }
+
+    // GEMM with optional event timing; k_logical excludes the K padding.
+    int gemm(const s2x_weight *w, int64_t M, float *y, int64_t ldy, const EpiParams &e,
+             int64_t k_logical) {
+        hipEvent_t a = nullptr, b = nullptr;
+        if (timing.on) {
+            a = timing.get();
+            b = timing.get();
+            S2X_HIP_TRY(hipEventRecord(a, stream));
+        }
+        hipError_t err = launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y, ldy, e,
+                                    stream);
+        if (err != hipSuccess) return hip_fail(err, "mmq launch");
+        if (timing.on) {
+            S2X_HIP_TRY(hipEventRecord(b, stream));
+            timing.pending.push_back({a, b, 2.0 * (double)M * (double)w->view.N * (double)k_logical});
+        }
+        return S2X_OK;
+    }
+
+    int quantize(const float *src, int64_t K, int64_t M, int64_t ldx, int64_t K_pad) {
+        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, qs.as<int8_t>(),
+                                            ds.as<uint32_t>(), stream);
+        return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize launch");
+    }
+
+    int layernorm_q(const float *src, int64_t M, const float *w, const float *b, float *y) {
+        hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, qs.as<int8_t>(),
+                                        ds.as<uint32_t>(), y, H, stream);
+        return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
+    }
+
+    int reserve(int64_t M, int64_t n_seg, int64_t max_len) {
+        const int64_t kmax = F_pad > H ? F_pad : H;
+        S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
+        S2X_TRY(ensure(qs, (size_t)(M * kmax), stream));
+        S2X_TRY(ensure(ds, sizeof(uint32_t) * (size_t)(M * (kmax / QK_)), stream));
+        S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
+        S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
+        S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
+        S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
+        S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
+        return S2X_OK;
+    }
+
+    // Upload the segment table (starts then lengths) to `seg`; skipped when
+    // it equals the table already there (steady-state batches stay async).
+    std::vector<int32_t> seg_host;
+    void *seg_dev_at = nullptr;
+    int set_segments(const std::vector<int32_t> &start, const std::vector<int32_t> &len) {
+        const size_t n = start.size();
+        std::vector<int32_t> tab(2 * n);
+        std::memcpy(tab.data(), start.data(), n * 4);
+        std::memcpy(tab.data() + n, len.data(), n * 4);
+        if (tab == seg_host && seg_dev_at == seg.p) return S2X_OK;
+        S2X_HIP_TRY(hipMemcpyAsync(seg.p, tab.data(), 8 * n, hipMemcpyHostToDevice, stream));
+        S2X_HIP_TRY(hipStreamSynchronize(stream));  // `tab` is pageable host memory
+        seg_host = std::move(tab);
+        seg_dev_at = seg.p;
+        return S2X_OK;
+    }
+    const int32_t *seg_start() const { return seg.as<int32_t>(); }
+    const int32_t *seg_len(int64_t n_seg) const { return seg.as<int32_t>() + n_seg; }
+
+    // The 27 encoder blocks in place on x (M packed rows).
+    int run_layers(int64_t M, int64_t n_seg, int64_t max_len, const uint8_t *key_valid) {
+        const AttnLayout AL = attn_layout(n_seg, max_len, n_head, d_head);
+        const float kq_scale = 1.0f / std::sqrt((float)d_head);
+        float *xp = x.as<float>();
+        for (auto &L : layers) {
+            S2X_TRY(layernorm_q(xp, M, L.ln1_w, L.ln1_b, nullptr));
+            S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
+            hipError_t e = launch_attn_prep(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(),
+                                            seg_len(n_seg), AL, attn_ws.p, stream);
+            if (e != hipSuccess) return hip_fail(e, "attn_prep launch");
+            e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
+                            att.as<float>(), H, stream);
+            if (e != hipSuccess) return hip_fail(e, "attn launch");
+            S2X_TRY(quantize(att.as<float>(), H, M, H, H));
+            S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
+            S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
+            S2X_TRY(gemm(L.up, M, u.as<float>(), F, EpiParams{EPI_BIAS_GELU, L.up_b, nullptr, 0, 0, 0}, H));
+            S2X_TRY(quantize(u.as<float>(), F, M, F, F_pad));
+            S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F));
+        }
+        return S2X_OK;
+    }
+};
+
+int check_dims(int64_t H, int64_t F, int64_t F_pad, int64_t n_head, int64_t n_layer) {
+    if (H <= 0 || H % 32 != 0 || H > 2048 || n_head <= 0 || H % n_head != 0 || n_layer < 0 ||
+        F <= 0 || F_pad < F || F_pad % 32 != 0 || F_pad - F >= 32)
+        return fail(S2X_ERR_INVALID_ARG, "bad config H=%lld F=%lld F_pad=%lld heads=%lld layers=%lld",
+                    (long long)H, (long long)F, (long long)F_pad, (long long)n_head,
+                    (long long)n_layer);
+    const int64_t dh = H / n_head;
+    if (dh < 65 || dh > 80 || dh % 4 != 0)
+        return fail(S2X_ERR_UNSUPPORTED, "head dim %lld unsupported (attention kernel: 65..80, %%4)",
+                    (long long)dh);
+    return S2X_OK;
+}
+
+}  // namespace
+}  // namespace s2x
+
+using namespace s2x;
+
+// ---------------------------------------------------------------------------
+// vision
+// ---------------------------------------------------------------------------
+struct s2x_vision {
+    Tower t;
+    int64_t patch_dim = 0, n_side = 0;
+    s2x_weight *patch = nullptr, *hkv = nullptr, *ho = nullptr, *hup = nullptr, *hdown = nullptr;
+    float *patch_b = nullptr, *pos_embd = nullptr, *post_ln_w = nullptr, *post_ln_b = nullptr;
+    float *probe_q = nullptr, *hkv_b = nullptr, *ho_b = nullptr, *hln_w = nullptr,
+          *hln_b = nullptr, *hup_b = nullptr, *hdown_b = nullptr;
+    std::vector<std::pair<std::pair<int, int>, float *>> pos_cache;  // LRU of resized grids
+    DevBuf pix, pos_packed, kv, hq, ha, hu, hout, hid;
+
+    ~s2x_vision() {
+        for (s2x_weight *w : {patch, hkv, ho, hup, hdown}) s2x_weight_destroy(w);
+        for (float *p : {patch_b, pos_embd, post_ln_w, post_ln_b, probe_q, hkv_b, ho_b, hln_w,
+                         hln_b, hup_b, hdown_b})
+            if (p) (void)hipFree(p);
+        for (auto &e : pos_cache) (void)hipFree(e.second);
+    }
+
+    // position embeddings for an n_h x n_w grid (cached, LRU of 4 shapes)
+    int pos_for(int n_h, int n_w, const float **out) {
+        if (n_h == n_side && n_w == n_side) {
+            *out = pos_embd;
+            return S2X_OK;
+        }
+        for (size_t i = 0; i < pos_cache.size(); ++i)
+            if (pos_cache[i].first == std::make_pair(n_h, n_w)) {
+                auto e = pos_cache[i];
+                pos_cache.erase(pos_cache.begin() + (long)i);
+                pos_cache.push_back(e);
+                *out = e.second;
+                return S2X_OK;
+            }
+        if (pos_cache.size() >= 4) {
+            S2X_HIP_TRY(hipStreamSynchronize(t.stream));
+            (void)hipFree(pos_cache.front().second);
+            pos_cache.erase(pos_cache.begin());
+        }
+        float *buf = nullptr;
+        if (hipMalloc(reinterpret_cast<void **>(&buf), sizeof(float) * (size_t)(n_h * n_w * t.H)) != hipSuccess)
+            return fail(S2X_ERR_OOM, "pos cache alloc");
+        hipError_t e = launch_resize_pos_embed(pos_embd, n_side, t.H, n_h, n_w, buf, t.stream);
+        if (e != hipSuccess) {
+            (void)hipFree(buf);
+            return hip_fail(e, "resize launch");
+        }
+        pos_cache.push_back({{n_h, n_w}, buf});
+        *out = buf;
+        return S2X_OK;
+    }
+
+    // After the packed, position-embedded patch rows are in t.x: the blocks,
+    // post-LN and pooling into out_dev [n_img][H].
+    int tail(int64_t M, int64_t n_img, int64_t max_len, int32_t pooling, float *out_dev) {
+        const int64_t H = t.H;
+        S2X_TRY(t.run_layers(M, n_img, max_len, nullptr));
+        if (pooling == S2X_POOL_MEAN) {
+            S2X_TRY(ensure(hid, sizeof(float) * (size_t)(M * H), t.stream));
+            hipError_t e = launch_layernorm(t.x.as<float>(), H, M, H, post_ln_w, post_ln_b, t.eps,
+                                            nullptr, nullptr, hid.as<float>(), H, t.stream);
+            if (e != hipSuccess) return hip_fail(e, "post-LN launch");
+            e = launch_mean_pool(hid.as<float>(), H, t.seg_start(), t.seg_len(n_img), n_img,
+                                 out_dev, t.stream);
+            return e == hipSuccess ? S2X_OK : hip_fail(e, "mean pool launch");
+        }
+        // MAP probe head (src/siglip2_vision.cpp:249-314)
+        S2X_TRY(t.layernorm_q(t.x.as<float>(), M, post_ln_w, post_ln_b, nullptr));
+        S2X_TRY(ensure(kv, sizeof(float) * (size_t)(M * 2 * H), t.stream));
+        S2X_TRY(ensure(hq, sizeof(float) * (size_t)(n_img * H), t.stream));
+        S2X_TRY(ensure(ha, sizeof(float) * (size_t)(n_img * H), t.stream));
+        S2X_TRY(ensure(hu, sizeof(float) * (size_t)(n_img * t.F), t.stream));
+        S2X_TRY(t.gemm(hkv, M, kv.as<float>(), 2 * H, EpiParams{EPI_BIAS, hkv_b, nullptr, 0, 0, 0}, H));
+        hipError_t e = launch_attn_1q(probe_q, kv.as<float>(), kv.as<float>() + H, 2 * H,
+                                      t.seg_start(), t.seg_len(n_img), n_img, t.n_head, t.d_head,
+                                      1.0f / std::sqrt((float)t.d_head), hq.as<float>(), t.stream);
+        if (e != hipSuccess) return hip_fail(e, "probe attention launch");
+        S2X_TRY(t.quantize(hq.as<float>(), H, n_img, H, H));
+        S2X_TRY(t.gemm(ho, n_img, ha.as<float>(), H, EpiParams{EPI_BIAS, ho_b, nullptr, 0, 0, 0}, H));
+        S2X_TRY(t.layernorm_q(ha.as<float>(), n_img, hln_w, hln_b, nullptr));
+        S2X_TRY(t.gemm(hup, n_img, hu.as<float>(), t.F, EpiParams{EPI_BIAS_GELU, hup_b, nullptr, 0, 0, 0}, H));
+        S2X_TRY(t.quantize(hu.as<float>(), t.F, n_img, t.F, t.F_pad));
+        S2X_TRY(t.gemm(hdown, n_img, out_dev, H, EpiParams{EPI_BIAS_RESID, hdown_b, ha.as<float>(), H, 0, 0}, t.F));
+        return S2X_OK;
+    }
+};
+
+extern "C" {
+
+int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
+    if (!out) return fail(S2X_ERR_INVALID_ARG, "vision_create: out is null");
+    *out = nullptr;
+    if (!w) return fail(S2X_ERR_INVALID_ARG, "vision_create: weights are null");
+    S2X_TRY(check_dims(w->hidden, w->inter, w->inter_pad, w->n_head, w->n_layer));
+    if (w->patch_dim <= 0 || w->patch_dim % 32 != 0 || w->n_side <= 0)
+        return fail(S2X_ERR_INVALID_ARG, "vision_create: bad patch_dim/n_side");
+    s2x_vision *v = new s2x_vision();
+    Tower &t = v->t;
+    t.H = w->hidden;
+    t.F = w->inter;
+    t.F_pad = w->inter_pad;
+    t.n_head = w->n_head;
+    t.d_head = t.H / t.n_head;
+    t.n_layer = w->n_layer;
+    t.eps = w->eps;
+    v->patch_dim = w->patch_dim;
+    v->n_side = w->n_side;
+    auto bail = [&](int st) {
+        delete v;
+        return st;
+    };
+    int st = t.init_stream();
+    if (st) return bail(st);
+    const int64_t H = t.H, F = t.F, F_pad = t.F_pad;
+    hipStream_t s = t.stream;
+    if ((st = upload_q8(w->patch_w, v->patch_dim, H, s, &v->patch, "patch_embd.weight")) ||
+        (st = upload_f32(w->patch_b, H, &v->patch_b, "patch_embd.bias")) ||
+        (st = upload_f32(w->pos_embd, v->n_side * v->n_side * H, &v->pos_embd, "position_embd")) ||
+        (st = upload_f32(w->post_ln_w, H, &v->post_ln_w, "post_ln.weight")) ||
+        (st = upload_f32(w->post_ln_b, H, &v->post_ln_b, "post_ln.bias")) ||
+        (st = t.load_layers(w->layers, w->n_layer)))
+        return bail(st);
+    // probe head: K and V projections share one GEMM (rows [k; v])
+    if (!w->hk_w || !w->hv_w || !w->hk_b || !w->hv_b || !w->probe || !w->hq_w || !w->hq_b)
+        return bail(fail(S2X_ERR_INVALID_ARG, "vision_create: probe head tensors missing"));
+    {
+        const size_t rb = (size_t)(H * (H / QK_)) * 34;
+        std::vector<uint8_t> kvraw(2 * rb);
+        std::memcpy(kvraw.data(), w->hk_w, rb);
+        std::memcpy(kvraw.data() + rb, w->hv_w, rb);
+        std::vector<float> kvb(2 * (size_t)H);
+        std::memcpy(kvb.data(), w->hk_b, sizeof(float) * (size_t)H);
+        std::memcpy(kvb.data() + H, w->hv_b, sizeof(float) * (size_t)H);
+        if ((st = upload_q8(kvraw.data(), H, 2 * H, s, &v->hkv, "head.attn_kv")) ||
+            (st = upload_f32(kvb.data(), 2 * H, &v->hkv_b, "head.attn_kv.bias")))
+            return bail(st);
+    }
+    if ((st = upload_q8(w->ho_w, H, H, s, &v->ho, "head.attn_o.weight")) ||
+        (st = upload_f32(w->ho_b, H, &v->ho_b, "head.attn_o.bias")) ||
+        (st = upload_f32(w->hln_w, H, &v->hln_w, "head.ln.weight")) ||
+        (st = upload_f32(w->hln_b, H, &v->hln_b, "head.ln.bias")) ||
+        (st = upload_q8(w->hup_w, H, F, s, &v->hup, "head.ffn_up.weight")) ||
+        (st = upload_f32(w->hup_b, F, &v->hup_b, "head.ffn_up.bias")) ||
+        (st = upload_q8(w->hdown_w, F_pad, H, s, &v->hdown, "head.ffn_down.weight")) ||
+        (st = upload_f32(w->hdown_b, H, &v->hdown_b, "head.ffn_down.bias")))
+        return bail(st);
+    // The probe query is image independent: q = mm(W_q, probe) + b_q, once.
+    {
+        s2x_weight *hq = nullptr;
+        float *probe = nullptr, *hq_b = nullptr;
+        if ((st = upload_q8(w->hq_w, H, H, s, &hq, "head.attn_q.weight")) ||
+            (st = upload_f32(w->probe, H, &probe, "head.probe")) ||
+            (st = upload_f32(w->hq_b, H, &hq_b, "head.attn_q.bias"))) {
+            s2x_weight_destroy(hq);
+            if (probe) (void)hipFree(probe);
+            if (hq_b) (void)hipFree(hq_b);
+            return bail(st);
+        }
+        if (hipMalloc(reinterpret_cast<void **>(&v->probe_q), sizeof(float) * (size_t)H) != hipSuccess)
+            st = fail(S2X_ERR_OOM, "probe_q alloc");
+        if (!st) st = ensure(t.qs, (size_t)H, s);
+        if (!st) st = ensure(t.ds, (size_t)(H / QK_) * 4, s);
+        if (!st) st = t.quantize(probe, H, 1, H, H);
+        if (!st) st = t.gemm(hq, 1, v->probe_q, H, EpiParams{EPI_BIAS, hq_b, nullptr, 0, 0, 0}, H);
+        if (!st && hipStreamSynchronize(s) != hipSuccess) st = fail(S2X_ERR_HIP, "probe sync");
+        s2x_weight_destroy(hq);
+        (void)hipFree(probe);
+        (void)hipFree(hq_b);
+        if (st) return bail(st);
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) return bail(fail(S2X_ERR_HIP, "create sync"));
+    *out = v;
+    return S2X_OK;
+}
+
+void s2x_vision_destroy(s2x_vision *v) {
+    if (!v) return;
+    (void)hipStreamSynchronize(v->t.stream);
+    delete v;
+}
+
+int s2x_vision_set_stream(s2x_vision *v, void *stream) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    v->t.stream = stream ? (hipStream_t)stream : v->t.own;
+    return S2X_OK;
+}
+
+int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t n_img, int32_t n_h,
+                                int32_t n_w, int32_t pooling, float *out_dev) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (n_img <= 0 || n_h <= 0 || n_w <= 0 || !pixels_dev || !out_dev ||
+        (pooling != S2X_POOL_MEAN && pooling != S2X_POOL_PROBE))
+        return fail(S2X_ERR_INVALID_ARG, "vision_encode_batch: bad arguments");
+    const int64_t n_pos = (int64_t)n_h * n_w;
+    if (n_pos > MAX_SEG_LEN) return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
+    Tower &t = v->t;
+    const int64_t M = n_pos * n_img;
+    S2X_TRY(t.reserve(M, n_img, n_pos));
+    std::vector<int32_t> st((size_t)n_img), ln((size_t)n_img, (int32_t)n_pos);
+    for (int i = 0; i < n_img; ++i) st[(size_t)i] = (int32_t)(i * n_pos);
+    S2X_TRY(t.set_segments(st, ln));
+    const float *pos = nullptr;
+    S2X_TRY(v->pos_for(n_h, n_w, &pos));
+    S2X_TRY(t.quantize(pixels_dev, v->patch_dim, M, v->patch_dim, v->patch_dim));
+    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                   EpiParams{EPI_BIAS_RESID, v->patch_b, pos, t.H, n_pos, 0}, v->patch_dim));
+    return v->tail(M, n_img, n_pos, pooling, out_dev);
+}
+
+int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h, int32_t n_w,
+                      int32_t pooling, float *out_host) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (!pixels_host || !out_host || n_h <= 0 || n_w <= 0)
+        return fail(S2X_ERR_INVALID_ARG, "vision_encode: bad arguments");
+    const size_t pix_bytes = sizeof(float) * (size_t)((int64_t)n_h * n_w * v->patch_dim);
+    S2X_TRY(ensure(v->pix, pix_bytes, v->t.stream));
+    S2X_TRY(ensure(v->hout, sizeof(float) * (size_t)v->t.H, v->t.stream));
+    S2X_HIP_TRY(hipMemcpyAsync(v->pix.p, pixels_host, pix_bytes, hipMemcpyHostToDevice, v->t.stream));
+    S2X_TRY(s2x_vision_encode_batch_dev(v, v->pix.as<float>(), 1, n_h, n_w, pooling, v->hout.as<float>()));
+    S2X_HIP_TRY(hipMemcpyAsync(out_host, v->hout.p, sizeof(float) * (size_t)v->t.H,
+                               hipMemcpyDeviceToHost, v->t.stream));
+    S2X_HIP_TRY(hipStreamSynchronize(v->t.stream));
+    return S2X_OK;
+}
+
+int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
+                                 const int32_t *shapes_host, int32_t n_img, int32_t max_patches,
+                                 int32_t pooling, float *out_dev) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (n_img <= 0 || max_patches <= 0 || !pixels_dev || !shapes_host || !out_dev ||
+        (pooling != S2X_POOL_MEAN && pooling != S2X_POOL_PROBE))
+        return fail(S2X_ERR_INVALID_ARG, "vision_encode_ragged: bad arguments");
+    if (max_patches > MAX_SEG_LEN)
+        return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
+    Tower &t = v->t;
+    std::vector<int32_t> st((size_t)n_img), ln((size_t)n_img);
+    int64_t M = 0, max_len = 0;
+    for (int i = 0; i < n_img; ++i) {
+        const int32_t h = shapes_host[2 * i], w = shapes_host[2 * i + 1];
+        if (h <= 0 || w <= 0 || (int64_t)h * w > max_patches)
+            return fail(S2X_ERR_INVALID_ARG, "vision_encode_ragged: image %d shape %dx%d invalid", i, h, w);
+        st[(size_t)i] = (int32_t)M;
+        ln[(size_t)i] = h * w;
+        M += (int64_t)h * w;
+        if (h * w > max_len) max_len = h * w;
+    }
+    S2X_TRY(t.reserve(M, n_img, max_len));
+    S2X_TRY(t.set_segments(st, ln));
+    S2X_TRY(ensure(v->pix, sizeof(float) * (size_t)(M * v->patch_dim), t.stream));
+    S2X_TRY(ensure(v->pos_packed, sizeof(float) * (size_t)(M * t.H), t.stream));
+    hipError_t e = launch_pack_rows(pixels_dev, v->patch_dim, max_patches, t.seg_start(),
+                                    t.seg_len(n_img), n_img, v->pix.as<float>(), t.stream);
+    if (e != hipSuccess) return hip_fail(e, "pack launch");
+    for (int i = 0; i < n_img; ++i) {
+        const float *pos = nullptr;
+        S2X_TRY(v->pos_for(shapes_host[2 * i], shapes_host[2 * i + 1], &pos));
+        S2X_HIP_TRY(hipMemcpyAsync(v->pos_packed.as<float>() + (int64_t)st[(size_t)i] * t.H, pos,
+                                   sizeof(float) * (size_t)(ln[(size_t)i] * t.H),
+                                   hipMemcpyDeviceToDevice, t.stream));
+    }
+    S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
+    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                   EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
+                   v->patch_dim));
+    return v->tail(M, n_img, max_len, pooling, out_dev);
+}
+
+int s2x_vision_gemm_timing(s2x_vision *v, int enable) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    S2X_TRY(v->t.timing.collect(v->t.stream));
+    v->t.timing.on = enable != 0;
+    return S2X_OK;
+}
+
+int s2x_vision_gemm_stats(s2x_vision *v, double *ms, double *ops, int64_t *launches, int reset) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    S2X_TRY(v->t.timing.collect(v->t.stream));
+    if (ms) *ms = v->t.timing.ms;
+    if (ops) *ops = v->t.timing.ops;
+    if (launches) *launches = v->t.timing.launches;
+    if (reset) {
+        v->t.timing.ms = 0.0;
+        v->t.timing.ops = 0.0;
+        v->t.timing.launches = 0;
+    }
+    return S2X_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// text
+// ---------------------------------------------------------------------------
+struct s2x_text {
+    Tower t;
+    int64_t vocab = 0, max_pos = 0, proj = 0;
+    void *tok = nullptr;  // raw Q8_0 token table (device)
+    float *pos_embd = nullptr, *fln_w = nullptr, *fln_b = nullptr, *head_b = nullptr;
+    s2x_weight *head = nullptr;
+    DevBuf ids, rows, pooled, out, kv8;
+    ~s2x_text() {
+        s2x_weight_destroy(head);
+        for (void *p : {tok, (void *)pos_embd, (void *)fln_w, (void *)fln_b, (void *)head_b})
+            if (p) (void)hipFree(p);
+    }
+
+    // n_batch prompts of n_tok ids already in `ids`; out_host n_batch*proj
+    int run(int32_t n_tok, int32_t n_batch, const uint8_t *key_valid_dev, float *out_host) {
+        const int64_t H = t.H, M = (int64_t)n_tok * n_batch;
+        std::vector<int32_t> st((size_t)n_batch), ln((size_t)n_batch, n_tok), last((size_t)n_batch);
+        for (int b = 0; b < n_batch; ++b) {
+            st[(size_t)b] = b * n_tok;
+            last[(size_t)b] = b * n_tok + n_tok - 1;
+        }
+        S2X_TRY(t.set_segments(st, ln));
+        hipError_t e = launch_get_rows_q8_0(tok, H, vocab, ids.as<int32_t>(), M, pos_embd, n_tok,
+                                            t.x.as<float>(), t.stream);
+        if (e != hipSuccess) return hip_fail(e, "get_rows launch");
+        S2X_TRY(t.run_layers(M, n_batch, n_tok, key_valid_dev));
+        e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr, nullptr,
+                             t.x.as<float>(), H, t.stream);
+        if (e != hipSuccess) return hip_fail(e, "final LN launch");
+        S2X_TRY(ensure(rows, sizeof(int32_t) * (size_t)n_batch, t.stream));
+        S2X_TRY(ensure(pooled, sizeof(float) * (size_t)(n_batch * H), t.stream));
+        S2X_TRY(ensure(out, sizeof(float) * (size_t)(n_batch * proj), t.stream));
+        S2X_HIP_TRY(hipMemcpyAsync(rows.p, last.data(), 4 * (size_t)n_batch, hipMemcpyHostToDevice, t.stream));
+        e = launch_gather_rows(t.x.as<float>(), H, rows.as<int32_t>(), n_batch, pooled.as<float>(), t.stream);
+        if (e != hipSuccess) return hip_fail(e, "gather launch");
+        S2X_TRY(t.quantize(pooled.as<float>(), H, n_batch, H, H));
+        S2X_TRY(t.gemm(head, n_batch, out.as<float>(), proj, EpiParams{EPI_BIAS, head_b, nullptr, 0, 0, 0}, H));
+        S2X_HIP_TRY(hipMemcpyAsync(out_host, out.p, sizeof(float) * (size_t)(n_batch * proj),
+                                   hipMemcpyDeviceToHost, t.stream));
+        S2X_HIP_TRY(hipStreamSynchronize(t.stream));
+        return S2X_OK;
+    }
+
+    int put_ids(const int32_t *ids_host, int64_t n) {
+        for (int64_t i = 0; i < n; ++i)
+            if (ids_host[i] < 0 || ids_host[i] >= vocab)
+                return fail(S2X_ERR_INVALID_ARG, "token id %d out of range [0, %lld)", ids_host[i],
+                            (long long)vocab);
+        S2X_TRY(ensure(ids, sizeof(int32_t) * (size_t)n, t.stream));
+        S2X_HIP_TRY(hipMemcpyAsync(ids.p, ids_host, 4 * (size_t)n, hipMemcpyHostToDevice, t.stream));
+        S2X_HIP_TRY(hipStreamSynchronize(t.stream));
+        return S2X_OK;
+    }
+};
+
+extern "C" {
+
+int s2x_text_create(const s2x_text_weights *w, s2x_text **out) {
+    if (!out) return fail(S2X_ERR_INVALID_ARG, "text_create: out is null");
+    *out = nullptr;
+    if (!w) return fail(S2X_ERR_INVALID_ARG, "text_create: weights are null");
+    S2X_TRY(check_dims(w->hidden, w->inter, w->inter_pad, w->n_head, w->n_layer));
+    if (w->vocab <= 0 || w->max_pos <= 0 || w->proj <= 0 || !w->tok_embd)
+        return fail(S2X_ERR_INVALID_ARG, "text_create: bad vocab/max_pos/proj");
+    s2x_text *x = new s2x_text();
+    Tower &t = x->t;
+    t.H = w->hidden;
+    t.F = w->inter;
+    t.F_pad = w->inter_pad;
+    t.n_head = w->n_head;
+    t.d_head = t.H / t.n_head;
+    t.n_layer = w->n_layer;
+    t.eps = w->eps;
+    x->vocab = w->vocab;
+    x->max_pos = w->max_pos;
+    x->proj = w->proj;
+    auto bail = [&](int st) {
+        delete x;
+        return st;
+    };
+    int st = t.init_stream();
+    if (st) return bail(st);
+    const size_t tok_bytes = (size_t)(x->vocab * (t.H / QK_)) * 34;
+    if (hipMalloc(&x->tok, tok_bytes) != hipSuccess) return bail(fail(S2X_ERR_OOM, "token table alloc"));
+    if (hipMemcpy(x->tok, w->tok_embd, tok_bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(S2X_ERR_HIP, "token table upload"));
+    if ((st = upload_f32(w->pos_embd, x->max_pos * t.H, &x->pos_embd, "position_embd")) ||
+        (st = upload_f32(w->final_ln_w, t.H, &x->fln_w, "final_ln.weight")) ||
+        (st = upload_f32(w->final_ln_b, t.H, &x->fln_b, "final_ln.bias")) ||
+        (st = upload_q8(w->head_w, t.H, x->proj, t.stream, &x->head, "head.weight")) ||
+        (st = upload_f32(w->head_b, x->proj, &x->head_b, "head.bias")) ||
+        (st = t.load_layers(w->layers, w->n_layer)))
+        return bail(st);
+    if (hipStreamSynchronize(t.stream) != hipSuccess) return bail(fail(S2X_ERR_HIP, "create sync"));
+    *out = x;
+    return S2X_OK;
+}
+
+void s2x_text_destroy(s2x_text *x) {
+    if (!x) return;
+    (void)hipStreamSynchronize(x->t.stream);
+    delete x;
+}
+
+int s2x_text_set_stream(s2x_text *x, void *stream) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    x->t.stream = stream ? (hipStream_t)stream : x->t.own;
+    return S2X_OK;
+}
+
+int s2x_text_encode(s2x_text *x, const int32_t *ids_host, int32_t n_tok, const int32_t *mask_host,
+                    float *out_host) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    if (!ids_host || !out_host || n_tok <= 0 || n_tok > x->max_pos)
+        return fail(S2X_ERR_INVALID_ARG, "n_tokens must be in (0, %lld], got %d",
+                    (long long)x->max_pos, n_tok);
+    S2X_TRY(x->t.reserve(n_tok, 1, n_tok));
+    S2X_TRY(x->put_ids(ids_host, n_tok));
+    const uint8_t *kv = nullptr;
+    if (mask_host) {
+        std::vector<uint8_t> m((size_t)n_tok);
+        for (int i = 0; i < n_tok; ++i) m[(size_t)i] = mask_host[i] != 0;
+        S2X_TRY(ensure(x->kv8, (size_t)n_tok, x->t.stream));
+        S2X_HIP_TRY(hipMemcpyAsync(x->kv8.p, m.data(), (size_t)n_tok, hipMemcpyHostToDevice, x->t.stream));
+        S2X_HIP_TRY(hipStreamSynchronize(x->t.stream));
+        kv = x->kv8.as<uint8_t>();
+    }
+    return x->run(n_tok, 1, kv, out_host);
+}
+
+int s2x_text_encode_batch(s2x_text *x, const int32_t *ids_host, int32_t n_tok, int32_t n_batch,
+                          float *out_host) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    if (n_batch <= 0) return fail(S2X_ERR_INVALID_ARG, "n_batch must be > 0");
+    if (!ids_host || !out_host || n_tok <= 0 || n_tok > x->max_pos)
+        return fail(S2X_ERR_INVALID_ARG, "n_tokens must be in (0, %lld], got %d",
+                    (long long)x->max_pos, n_tok);
+    const int64_t M = (int64_t)n_tok * n_batch;
+    S2X_TRY(x->t.reserve(M, n_batch, n_tok));
+    S2X_TRY(x->put_ids(ids_host, M));
+    return x->run(n_tok, n_batch, nullptr, out_host);
+}
+
+}  // extern "C"

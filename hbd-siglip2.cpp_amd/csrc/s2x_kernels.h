@@ -1,0 +1,109 @@
+// s2x_kernels.h -- host-side launchers of the gfx950 kernels (internal).
+//
+// All launchers are asynchronous on `stream`, validate nothing (the C-ABI
+// layer in s2x_abi.cpp does) and return hipError_t from the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace s2x {
+
+// Longest attention segment (tokens per image / prompt) the kernels accept.
+constexpr int64_t MAX_SEG_LEN = 4096;
+
+// Device view of a repacked Q8_0 weight (K_pad, N).
+struct WeightView {
+    const int8_t *qs;   // N rows of K_pad int8
+    const float  *d;    // N rows of KB f32 (fp16 values widened)
+    int64_t K_pad;      // multiple of 32
+    int64_t N;
+};
+
+enum EpiKind { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4 };
+
+struct EpiParams {
+    int          kind;
+    const float *bias;
+    const float *resid;
+    int64_t      ld_resid;
+    int64_t      resid_rows;  // 0: row m; >0: row m % resid_rows
+    int64_t      dump_kb;     // EPI_DUMP_I: the block whose int32 dot is written
+};
+
+// a1: F32 -> Q8_1 (qs int8 [M][K_pad], ds u32 (fp16 d | fp16 s << 16) [M][KB])
+hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
+                                int64_t K_pad, int8_t *qs, uint32_t *ds,
+                                hipStream_t stream);
+
+// a2: raw block_q8_0 (N rows of K_pad/32 34-byte blocks, device) -> WeightView planes
+hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
+                              float *d, hipStream_t stream);
+
+// a3: Y = W x X(Q8_1) with epilogue
+hipError_t launch_mmq(const WeightView &w, const int8_t *xq, const uint32_t *xds,
+                      int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                      hipStream_t stream);
+
+// a4: LayerNorm (+ Q8_1).  qs/ds may be null (no quantized output), y may be
+// null (no f32 output); at least one is set.
+hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
+                            const float *w, const float *b, float eps, int8_t *qs,
+                            uint32_t *ds, float *y, int64_t ldy, hipStream_t stream);
+
+// a5: standalone epilogues
+hipError_t launch_bias_residual(const float *mm, const float *bias, const float *resid,
+                                float *y, int64_t H, int64_t n_pos, hipStream_t stream);
+hipError_t launch_bias_gelu(const float *mm, const float *bias, float *y, int64_t H,
+                            int64_t n_pos, hipStream_t stream);
+
+// a6/a7: attention staging + flash attention over packed segments
+struct AttnLayout {
+    int64_t n_seg, max_len, n_head, d_head;
+    int64_t d_pad;     // d_head rounded up to 16 (Q/K row length)
+    int64_t dv_pad;    // d_head rounded up to 32 (V^T rows)
+    int64_t len_pad;   // max_len rounded up to 128 (query tile)
+    size_t q_off, k_off, vt_off, bytes;
+};
+AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head);
+hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                            const int32_t *seg_start, const int32_t *seg_len,
+                            const AttnLayout &L, void *ws, hipStream_t stream);
+hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
+                       const uint8_t *key_valid, const AttnLayout &L, float scale,
+                       float *out, int64_t ld_out, hipStream_t stream);
+// Single-query attention (MAP probe head): q [H] shared by all segments,
+// k/v packed rows (ld floats), out [n_seg][H].
+hipError_t launch_attn_1q(const float *q, const float *k, const float *v, int64_t ld,
+                          const int32_t *seg_start, const int32_t *seg_len,
+                          int64_t n_seg, int64_t n_head, int64_t d_head, float scale,
+                          float *out, hipStream_t stream);
+
+// a8: anti-aliased bilinear resize of the position-embedding grid
+hipError_t launch_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
+                                   int64_t out_h, int64_t out_w, float *out,
+                                   hipStream_t stream);
+
+// a11: Q8_0 get_rows (+ optional add of row i % add_rows)
+hipError_t launch_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows,
+                                const int32_t *ids, int64_t n_ids, const float *add,
+                                int64_t add_rows, float *out, hipStream_t stream);
+
+// Pooling helpers
+// out[s][c] = mean over the rows of segment s (double accumulation)
+hipError_t launch_mean_pool(const float *x, int64_t H, const int32_t *seg_start,
+                            const int32_t *seg_len, int64_t n_seg, float *out,
+                            hipStream_t stream);
+// out[i][c] = x[rows[i]][c]
+hipError_t launch_gather_rows(const float *x, int64_t H, const int32_t *rows,
+                              int64_t n, float *out, hipStream_t stream);
+// packed[t] = padded[img(t)][pos(t)] for the valid (first seg_len) rows
+hipError_t launch_pack_rows(const float *padded, int64_t row_len, int64_t max_rows,
+                            const int32_t *seg_start, const int32_t *seg_len,
+                            int64_t n_seg, float *packed, hipStream_t stream);
+// y[i] = a[i] + b[i]
+hipError_t launch_add(const float *a, const float *b, float *y, int64_t n,
+                      hipStream_t stream);
+
+}  // namespace s2x

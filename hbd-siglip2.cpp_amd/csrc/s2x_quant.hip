@@ -1,0 +1,205 @@
+// s2x_quant.hip -- F32->Q8_1 activation quantizer, fused LayerNorm(+Q8_1)
+// and the Q8_0 weight repack, for gfx950.
+//
+// All three are HBM-bound: the quantizer moves 5.125 bytes per element
+// (4 in, 1 + 4/32 out), LayerNorm+quantize 5.125 bytes per element of a row.
+// Mapping: one 32-value block = 8 consecutive lanes x 4 floats, so a wave
+// reads 1 KiB contiguous per instruction and the block amax is a 3-step
+// butterfly inside the 8-lane group.
+#include "s2x_device.h"
+#include "s2x_kernels.h"
+
+namespace s2x {
+
+// ---------------------------------------------------------------------------
+// a1: quantizer.  Semantics: src/cuda/siglip2_custom_mmq.cu:63-76 (d, inv,
+// round-half-even, clamp) plus the Q8_1 sum s = fp16(sum(q) * d).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quantize_q8_1(
+    const float *__restrict__ x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
+    int8_t *__restrict__ qs, uint32_t *__restrict__ ds, int vec4) {
+    const int64_t KB = K_pad / QK;
+    const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+    const int sub = threadIdx.x & 7;
+    if (g >= M * KB) return;  // whole 8-lane groups leave together
+    const int64_t m = g / KB;
+    const int64_t kb = g - m * KB;
+    const int64_t c = kb * QK + sub * 4;
+    const float *xr = x + m * ldx;
+    float v0, v1, v2, v3;
+    if (vec4 && c + 3 < K) {
+        const float4 t = *reinterpret_cast<const float4 *>(xr + c);
+        v0 = t.x; v1 = t.y; v2 = t.z; v3 = t.w;
+    } else {
+        v0 = c + 0 < K ? xr[c + 0] : 0.0f;
+        v1 = c + 1 < K ? xr[c + 1] : 0.0f;
+        v2 = c + 2 < K ? xr[c + 2] : 0.0f;
+        v3 = c + 3 < K ? xr[c + 3] : 0.0f;
+    }
+    float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    a = group_max<8>(a);
+    const float d = a / 127.0f;
+    const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+    const int q0 = q8_round(v0, inv), q1 = q8_round(v1, inv);
+    const int q2 = q8_round(v2, inv), q3 = q8_round(v3, inv);
+    *reinterpret_cast<uint32_t *>(qs + m * K_pad + c) = pack4_i8(q0, q1, q2, q3);
+    const int s = group_isum<8>(q0 + q1 + q2 + q3);
+    if (sub == 0) {
+        ds[g] = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
+    }
+}
+
+hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
+                                int64_t K_pad, int8_t *qs, uint32_t *ds,
+                                hipStream_t stream) {
+    const int64_t groups = M * (K_pad / QK);
+    if (groups == 0) return hipSuccess;
+    const int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+    const int64_t threads = groups * 8;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q8_1, dim3(grid), dim3(256), 0, stream, x, K, M, ldx,
+                       K_pad, qs, ds, vec4);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// a2: weight repack.  One thread per 34-byte block: the int8 qs go to a
+// 16-byte aligned row-major plane, d widens (exactly) to f32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__ raw,
+                                                     int64_t n_blocks, int8_t *__restrict__ qs,
+                                                     float *__restrict__ d) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + i * 34);  // 2-byte aligned
+    d[i] = f16_bits_to_f32(src[0]);
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = (uint32_t)src[1 + 2 * j] | ((uint32_t)src[2 + 2 * j] << 16);
+    uint4 *dst = reinterpret_cast<uint4 *>(qs + i * QK);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
+                              float *d, hipStream_t stream) {
+    const int64_t nb = N * (K_pad / QK);
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
+                       stream, reinterpret_cast<const uint8_t *>(raw), nb, qs, d);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// a4: LayerNorm(+affine)(+Q8_1).  One wave per row, the row held in
+// registers: a two-pass mean / variance from wave butterflies, then
+// y = ((x - mean) * scale) * w + b rounded after each operation
+// (src/siglip2_vision.cpp:79-88 graph; ggml_norm's two-pass variance), then
+// the 32-blocks of y quantized by 8-lane groups exactly as k_quantize_q8_1.
+// ---------------------------------------------------------------------------
+constexpr int LN_MAXIT = 8;  // H <= 8 * 256
+
+template <bool QUANT, bool WRITE_Y>
+__global__ __launch_bounds__(256) void k_layernorm(
+    const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
+    const float *__restrict__ w, const float *__restrict__ b, float eps,
+    int8_t *__restrict__ qs, uint32_t *__restrict__ ds, float *__restrict__ y,
+    int64_t ldy, int vec4) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float *xr = x + row * ldx;
+    float v[LN_MAXIT][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int it = 0; it < LN_MAXIT; ++it) {
+        const int64_t c = (int64_t)it * 256 + lane * 4;
+        if (c < H) {
+            if (vec4 & 1) {
+                const float4 t = *reinterpret_cast<const float4 *>(xr + c);
+                v[it][0] = t.x; v[it][1] = t.y; v[it][2] = t.z; v[it][3] = t.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[it][j] = xr[c + j];
+            }
+            s = s + ((v[it][0] + v[it][1]) + (v[it][2] + v[it][3]));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
+        }
+    }
+    const float mean = group_sum<64>(s) / (float)H;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int it = 0; it < LN_MAXIT; ++it) {
+        const int64_t c = (int64_t)it * 256 + lane * 4;
+        if (c < H) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float t = v[it][j] - mean;
+                s2 = s2 + t * t;
+            }
+        }
+    }
+    const float var = group_sum<64>(s2) / (float)H;
+    const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int it = 0; it < LN_MAXIT; ++it) {
+        const int64_t c = (int64_t)it * 256 + lane * 4;
+        if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float t = (v[it][j] - mean) * scale;
+            if (w) t = t * w[c + j];
+            if (b) t = t + b[c + j];
+            o[j] = t;
+        }
+        if (WRITE_Y) {
+            float *yr = y + row * ldy + c;
+            if (vec4 & 2) {
+                *reinterpret_cast<float4 *>(yr) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) yr[j] = o[j];
+            }
+        }
+        if (QUANT) {
+            float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+            a = group_max<8>(a);
+            const float d = a / 127.0f;
+            const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+            const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
+            const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
+            *reinterpret_cast<uint32_t *>(qs + row * H + c) = pack4_i8(q0, q1, q2, q3);
+            const int sq = group_isum<8>(q0 + q1 + q2 + q3);
+            if ((lane & 7) == 0) {
+                ds[row * (H / QK) + c / QK] = (uint32_t)f32_to_f16_bits(d) |
+                                              ((uint32_t)f32_to_f16_bits((float)sq * d) << 16);
+            }
+        }
+    }
+}
+
+hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
+                            const float *w, const float *b, float eps, int8_t *qs,
+                            uint32_t *ds, float *y, int64_t ldy, hipStream_t stream) {
+    if (M == 0) return hipSuccess;
+    int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+    if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
+    const dim3 grid((unsigned)((M + 3) / 4));
+    const bool quant = qs != nullptr;
+    const bool wy = y != nullptr;
+    if (quant && wy)
+        hipLaunchKernelGGL((k_layernorm<true, true>), grid, dim3(256), 0, stream, x, H, M, ldx,
+                           w, b, eps, qs, ds, y, ldy, vec4);
+    else if (quant)
+        hipLaunchKernelGGL((k_layernorm<true, false>), grid, dim3(256), 0, stream, x, H, M,
+                           ldx, w, b, eps, qs, ds, y, ldy, vec4);
+    else
+        hipLaunchKernelGGL((k_layernorm<false, true>), grid, dim3(256), 0, stream, x, H, M,
+                           ldx, w, b, eps, qs, ds, y, ldy, vec4);
+    return hipGetLastError();
+}
+
+}  // namespace s2x

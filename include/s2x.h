@@ -1,0 +1,299 @@
+/*
+ * s2x.h -- C-ABI of the MI355X (gfx950) SigLIP2 Q8_0 matmul hot path.
+ *
+ * Plain C: pointers, sizes and status codes; no C++ or torch types.
+ * Device pointers are HIP device memory owned by the caller unless stated.
+ * `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ * Every function returns an s2x_status; on failure a message is available
+ * from s2x_last_error() on the calling thread.  Launch functions are
+ * asynchronous on `stream`; they neither allocate nor synchronise unless
+ * stated.  The library keeps no global mutable state besides the per-thread
+ * error message, so concurrent calls on different streams are safe.
+ *
+ * Layouts use the reference's ggml order (innermost first): an activation
+ * X (K, M) is M rows of K floats (row stride ldx floats), a GEMM output
+ * Y (N, M) is y[m*N + n].
+ */
+#ifndef S2X_H
+#define S2X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    S2X_OK = 0,
+    S2X_ERR_INVALID_ARG = 1,   /* bad shape / null pointer / misalignment */
+    S2X_ERR_UNSUPPORTED = 2,   /* shape or feature this build does not handle */
+    S2X_ERR_HIP = 3,           /* a HIP runtime call failed */
+    S2X_ERR_WORKSPACE = 4,     /* caller workspace too small */
+    S2X_ERR_OOM = 5,           /* device allocation failed */
+    S2X_ERR_NOT_LOADED = 6     /* encoder used before load */
+} s2x_status;
+
+const char *s2x_status_string(int status);
+const char *s2x_last_error(void);
+/* Library version string, e.g. "s2x 0.1 gfx950". */
+const char *s2x_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* a1  F32 -> Q8_1 activation quantizer                                      */
+/* Replaces siglip2_custom_mmq::launch_quantize_activation                   */
+/* (src/cuda/siglip2_custom_mmq.cuh:63-67) and ggml-cuda's quantize_mmq_q8_1. */
+/* Per 32-value block: d = amax/127; q = rint_half_even(x*127/amax) clamped  */
+/* to [-128,127]; ds = (fp16(d), fp16(sum(q)*d)).  Columns K..K_pad-1 are     */
+/* zero (the K padding of src/siglip2_vision.cpp:99-107).                     */
+/*   x  : M rows, stride ldx floats, K valid columns                          */
+/*   qs : M rows of K_pad int8 (K_pad % 32 == 0, K <= K_pad)                  */
+/*   ds : M rows of K_pad/32 (fp16 d, fp16 s) pairs                           */
+/* ------------------------------------------------------------------------ */
+int s2x_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
+                      int64_t K_pad, void *qs, void *ds, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a2  Q8_0 weights, repacked once for the MFMA GEMM                          */
+/* A raw Q8_0 matrix W (K_pad, N) is N rows of K_pad/32 34-byte block_q8_0    */
+/* (fp16 d then int8 qs[32]; bench/microbench_mmq.cpp:322-343).  The repack  */
+/* is lossless: an int8 plane (N rows of K_pad) and an f32 scale plane       */
+/* (N rows of K_pad/32, fp16 values widened exactly).                         */
+/* ------------------------------------------------------------------------ */
+typedef struct s2x_weight s2x_weight;
+
+/* Bytes of device memory a prepared (K_pad, N) weight occupies. */
+size_t s2x_weight_bytes(int64_t K_pad, int64_t N);
+/* Repack raw Q8_0 blocks (host memory if `raw_is_host`, else device) into a
+ * new device-resident weight.  Allocates; synchronises `stream`. */
+int s2x_weight_create(const void *raw, int raw_is_host, int64_t K_pad,
+                      int64_t N, void *stream, s2x_weight **out);
+/* Same, into caller memory `dev_buf` of s2x_weight_bytes() bytes (no
+ * allocation; asynchronous on `stream`; raw must be device memory). */
+int s2x_weight_create_in(const void *raw_dev, int64_t K_pad, int64_t N,
+                         void *dev_buf, void *stream, s2x_weight **out);
+void s2x_weight_destroy(s2x_weight *w);
+int64_t s2x_weight_k(const s2x_weight *w);
+int64_t s2x_weight_n(const s2x_weight *w);
+
+/* ------------------------------------------------------------------------ */
+/* a3  Q8_0 x Q8_1 GEMM on int8 MFMA                                          */
+/* Y[m*N+n] = sum over 32-blocks kb, in order, of                              */
+/*   acc = fmaf((float)I_kb, d_w * d_x, acc),  I_kb = sum q_w*q_x (exact)     */
+/* then the epilogue.                                                          */
+/* Replaces ggml-cuda mul_mat_q<Q8_0> behind GGML_OP_MUL_MAT(Q8_0, F32) and   */
+/* siglip2_custom_mmq::launch_custom_mmq (src/cuda/siglip2_custom_mmq.cuh:    */
+/* 96-103); the epilogues replace the fused tails of                          */
+/* src/cuda/siglip2_megakernel.cuh:117-132.                                   */
+/* ------------------------------------------------------------------------ */
+typedef enum {
+    S2X_EPI_NONE = 0,        /* y = acc                                      */
+    S2X_EPI_BIAS = 1,        /* y = acc + bias[n]                            */
+    S2X_EPI_BIAS_GELU = 2,   /* y = gelu_tanh(acc + bias[n])                 */
+    S2X_EPI_BIAS_RESID = 3   /* y = (acc + bias[n]) + resid[r(m)*ld_resid+n] */
+} s2x_epilogue_kind;
+
+typedef struct {
+    int32_t      kind;        /* s2x_epilogue_kind */
+    const float *bias;        /* N floats, required unless kind == NONE */
+    const float *resid;       /* BIAS_RESID only; may alias y             */
+    int64_t      ld_resid;    /* row stride of resid in floats            */
+    int64_t      resid_rows;  /* 0: r(m) = m; > 0: r(m) = m % resid_rows  */
+} s2x_epilogue;
+
+int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds,
+                          int64_t M, float *y, int64_t ldy,
+                          const s2x_epilogue *epi, void *stream);
+
+/* Drop-in GGML_OP_MUL_MAT(W: Q8_0 raw device blocks (K_pad, N), X: F32
+ * (K, M)) -> Y: F32 (N, M).  X is quantized to Q8_1 (K zero-padded to K_pad)
+ * and W repacked inside `workspace`, whose size s2x_mul_mat_workspace_size()
+ * gives.  No allocation. */
+size_t s2x_mul_mat_workspace_size(int64_t K_pad, int64_t N, int64_t M);
+int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N,
+                         const float *x, int64_t K, int64_t ldx, int64_t M,
+                         float *y, void *workspace, size_t ws_bytes,
+                         void *stream);
+
+/* Debug view of the GEMM's integer stage: out[m*N+n] = I_kb (the exact
+ * int32 block dot of block `kb`) from the same MFMA data path. */
+int s2x_block_dots(const s2x_weight *w, const void *qs, int64_t M, int64_t kb,
+                   int32_t *out, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a4  LayerNorm(+affine), alone and fused with the Q8_1 quantizer           */
+/* Replaces siglip2_megakernel::launch_fused_layernorm_affine                */
+/* (src/cuda/siglip2_megakernel.cuh:50-58) and ggml_norm/mul/add.             */
+/* y = ((x - mean) * (1/sqrtf(var + eps))) * w + b, every op rounded in f32, */
+/* mean and var from a two-pass row reduction.  H % 32 == 0, H <= 2048.       */
+/* ------------------------------------------------------------------------ */
+int s2x_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
+                  const float *w, const float *b, float eps, float *y,
+                  int64_t ldy, void *stream);
+/* Fused: writes Q8_1 (qs: M rows of H int8, ds: M rows of H/32 pairs) and,
+ * if y != NULL, the f32 LayerNorm output as well. */
+int s2x_layernorm_quantize_q8_1(const float *x, int64_t H, int64_t M,
+                                int64_t ldx, const float *w, const float *b,
+                                float eps, void *qs, void *ds, float *y,
+                                int64_t ldy, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a5  standalone epilogues (src/cuda/siglip2_megakernel.cuh:117-132)        */
+/* ------------------------------------------------------------------------ */
+/* y = (mm + bias[h]) + resid, both adds rounded in f32 */
+int s2x_bias_residual(const float *mm, const float *bias, const float *resid,
+                      float *y, int64_t H, int64_t n_pos, void *stream);
+/* y = gelu_tanh(mm + bias[h]) */
+int s2x_bias_gelu(const float *mm, const float *bias, float *y, int64_t H,
+                  int64_t n_pos, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a6/a7  attention                                                          */
+/* Replaces launch_qkv_copy_to_scratch + launch_fused_qkv_prep               */
+/* (src/cuda/siglip2_megakernel.cuh:75-100), ggml_flash_attn_ext             */
+/* (src/siglip2_vision.cpp:141-175) and launch_fused_post_fa_cont            */
+/* (src/cuda/siglip2_megakernel.cuh:148-155).                                 */
+/*                                                                            */
+/* Sequences are segments of a packed token array: segment s covers rows     */
+/* seg_start[s] .. seg_start[s]+seg_len[s]-1.  Attention never crosses a     */
+/* segment.  key_valid (optional, one byte per packed row) drops keys.       */
+/* ------------------------------------------------------------------------ */
+/* Bytes of the f16 Q/K/V staging buffer for n_seg segments of at most
+ * max_len tokens with n_head heads of d_head. */
+size_t s2x_attn_workspace_size(int64_t n_seg, int64_t max_len, int64_t n_head,
+                               int64_t d_head);
+/* qkv: packed rows of 3*H floats [q | k | v] (no bias yet); adds qkv_bias
+ * and stages Q, K (f16, d zero-padded) and V^T (f16) into `ws`. */
+int s2x_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                  const int32_t *seg_start_dev, const int32_t *seg_len_dev,
+                  int64_t n_seg, int64_t max_len, int64_t n_head,
+                  int64_t d_head, void *ws, size_t ws_bytes, void *stream);
+/* softmax(Q K^T * scale) V per segment and head; out: packed rows of
+ * H = n_head*d_head floats, head-major within the row. */
+int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
+                 const int32_t *seg_len_dev, const uint8_t *key_valid,
+                 int64_t n_seg, int64_t max_len, int64_t n_head,
+                 int64_t d_head, float scale, float *out, int64_t ld_out,
+                 void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a8  position-embedding resize (replaces ggml_interpolate(BILINEAR |       */
+/* ANTIALIAS) at src/siglip2_vision.cpp:680-690): anti-aliased bilinear,     */
+/* PyTorch F.interpolate(antialias=True, align_corners=False) semantics.      */
+/* pos: n_side*n_side rows of H; out: out_h*out_w rows of H (device).         */
+/* ------------------------------------------------------------------------ */
+int s2x_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
+                         int64_t out_h, int64_t out_w, float *out,
+                         void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a11  Q8_0 get_rows (replaces ggml_get_rows on the Q8_0 token table,        */
+/* src/siglip2_text.cpp:649-658): out[i] = dequant(table row ids[i]) (+ add  */
+/* row i % add_rows of `add` when add != NULL).                               */
+/* ------------------------------------------------------------------------ */
+int s2x_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows_table,
+                      const int32_t *ids, int64_t n_ids, const float *add,
+                      int64_t add_rows, float *out, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* a10  encoders (replace siglip2::VisionEncoder / TextEncoder,               */
+/* src/siglip2_vision.h:37-68, src/siglip2_text.h:25-75).                     */
+/* Weights come from host memory: raw Q8_0 blocks for every matrix, f32 for  */
+/* biases, LayerNorms, position embeddings and the probe.                     */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    const float *ln1_w, *ln1_b;
+    const void  *qkv_w;  const float *qkv_b;   /* Q8_0 (H, 3H), rows [q;k;v] */
+    const void  *o_w;    const float *o_b;     /* Q8_0 (H, H)                */
+    const float *ln2_w, *ln2_b;
+    const void  *up_w;   const float *up_b;    /* Q8_0 (H, F)                */
+    const void  *down_w; const float *down_b;  /* Q8_0 (F_pad, H)            */
+} s2x_layer_weights;
+
+typedef struct {
+    int32_t hidden, inter, inter_pad, n_head, n_layer;
+    int32_t patch_dim, n_side;                  /* 768, 16 */
+    float   eps;
+    const void  *patch_w; const float *patch_b; /* Q8_0 (patch_dim, H)    */
+    const float *pos_embd;                      /* n_side^2 rows of H     */
+    const float *post_ln_w, *post_ln_b;
+    const float *probe;                         /* H                      */
+    const void  *hq_w, *hk_w, *hv_w, *ho_w;     /* Q8_0 (H, H)            */
+    const float *hq_b, *hk_b, *hv_b, *ho_b;
+    const float *hln_w, *hln_b;
+    const void  *hup_w; const float *hup_b;     /* Q8_0 (H, F)            */
+    const void  *hdown_w; const float *hdown_b; /* Q8_0 (F_pad, H)        */
+    const s2x_layer_weights *layers;            /* n_layer entries        */
+} s2x_vision_weights;
+
+typedef struct {
+    int32_t hidden, inter, inter_pad, n_head, n_layer, vocab, max_pos, proj;
+    float   eps;
+    const void  *tok_embd;                      /* Q8_0 (H, vocab)        */
+    const float *pos_embd;                      /* max_pos rows of H      */
+    const float *final_ln_w, *final_ln_b;
+    const void  *head_w; const float *head_b;   /* Q8_0 (H, proj)         */
+    const s2x_layer_weights *layers;
+} s2x_text_weights;
+
+typedef struct s2x_vision s2x_vision;
+typedef struct s2x_text s2x_text;
+
+enum { S2X_POOL_MEAN = 0, S2X_POOL_PROBE = 1 };
+
+/* Upload + repack all weights to the current HIP device; the encoder owns
+ * its own HIP stream (default priority). */
+int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out);
+void s2x_vision_destroy(s2x_vision *v);
+/* Run on the encoder's stream (NULL) or a caller stream. */
+int s2x_vision_set_stream(s2x_vision *v, void *stream);
+
+/* Reference signature (VisionEncoder::encode): one image, host pixels
+ * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */
+int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h,
+                      int32_t n_w, int32_t pooling, float *out_host);
+
+/* Batched, device-resident: n_img images of the same n_h x n_w grid,
+ * pixels_dev [n_img*n_h*n_w, patch_dim], out_dev [n_img, hidden].
+ * Asynchronous on the encoder's stream. */
+int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev,
+                                int32_t n_img, int32_t n_h, int32_t n_w,
+                                int32_t pooling, float *out_dev);
+
+/* Ragged (NaFlex) device-resident batch in the HF padded convention:
+ * pixels_dev [n_img, max_patches, patch_dim], image i's h*w valid patches
+ * first (row-major over its h x w grid) then padding, shapes_host
+ * [n_img][2] = (h, w).  The valid rows are packed and attention runs per
+ * image, which equals HF's key-masked attention over the padded batch.
+ * out_dev [n_img, hidden].  Asynchronous. */
+int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
+                                 const int32_t *shapes_host, int32_t n_img,
+                                 int32_t max_patches, int32_t pooling,
+                                 float *out_dev);
+
+/* Per-kernel GPU timing of the MFMA GEMM launches (HIP events on the
+ * encoder's stream) for roofline reporting.  enable != 0 turns recording
+ * on; s2x_vision_gemm_stats returns the summed milliseconds and op count
+ * (2*M*N*K_logical) of the GEMMs recorded since the last reset, plus the
+ * launch count.  Synchronises the encoder stream. */
+int s2x_vision_gemm_timing(s2x_vision *v, int enable);
+int s2x_vision_gemm_stats(s2x_vision *v, double *ms, double *ops,
+                          int64_t *launches, int reset);
+
+int s2x_text_create(const s2x_text_weights *w, s2x_text **out);
+void s2x_text_destroy(s2x_text *t);
+int s2x_text_set_stream(s2x_text *t, void *stream);
+/* TextEncoder::encode: one prompt of n_tok ids (host), optional host mask
+ * (1 = valid), out_host proj floats.  Synchronous. */
+int s2x_text_encode(s2x_text *t, const int32_t *ids_host, int32_t n_tok,
+                    const int32_t *mask_host, float *out_host);
+/* TextEncoder::encode_batch: n_batch prompts of n_tok ids each (host, batch
+ * major), no mask (the reference rejects one, src/siglip2_text.cpp:769-772);
+ * out_host n_batch*proj floats.  Synchronous. */
+int s2x_text_encode_batch(s2x_text *t, const int32_t *ids_host, int32_t n_tok,
+                          int32_t n_batch, float *out_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* S2X_H */

@@ -1,0 +1,574 @@
+/*
+ * oracle.c -- CPU restatement of the SigLIP2 Q8_0 matmul hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker and the timed CPU
+ * baseline, never part of the product.  Built with -ffp-contract=off so every
+ * float operation rounds where the restated code rounds; fused multiply-adds
+ * appear only as explicit fmaf() calls.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_BLOCK_BYTES 34 /* fp16 d + 32 int8 */
+
+static int orc_threads(int n) {
+#ifdef _OPENMP
+    return n > 0 ? n : omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp16                                                                      */
+/* ------------------------------------------------------------------------ */
+
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xffu) { /* inf / nan (nan stays quiet) */
+        return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
+    }
+    const int32_t e = (int32_t)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign; /* below half the smallest subnormal */
+        man |= 0x800000u;
+        const int shift = 14 - e;           /* 14..24 */
+        uint32_t h = man >> shift;
+        const uint32_t rem = man & ((1u << shift) - 1u);
+        const uint32_t mid = 1u << (shift - 1);
+        if (rem > mid || (rem == mid && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++; /* carry may reach inf */
+    return (uint16_t)(sign | h);
+}
+
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+    const uint32_t man = (uint32_t)h & 0x3ffu;
+    uint32_t x;
+    if (exp == 0) {
+        float v = ldexpf((float)man, -24); /* exact */
+        return sign ? -v : v;
+    } else if (exp == 31) {
+        x = sign | 0x7f800000u | (man << 13);
+    } else {
+        x = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void orc_fp32_to_fp16_n(const float *x, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_fp32_to_fp16(x[i]);
+}
+
+void orc_fp16_to_fp32_n(const uint16_t *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_fp16_to_fp32(x[i]);
+}
+
+static inline float fp16r(float f) { return orc_fp16_to_fp32(orc_fp32_to_fp16(f)); }
+
+/* ------------------------------------------------------------------------ */
+/* quantizers                                                                */
+/* ------------------------------------------------------------------------ */
+
+static void quant_q8_0_block(const float *x, uint8_t *blk) {
+    float amax = 0.0f;
+    for (int j = 0; j < ORC_QK; ++j) {
+        const float a = fabsf(x[j]);
+        if (a > amax) amax = a;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = orc_fp32_to_fp16(d);
+    memcpy(blk, &dh, 2);
+    int8_t *qs = (int8_t *)(blk + 2);
+    for (int j = 0; j < ORC_QK; ++j) qs[j] = (int8_t)roundf(x[j] * id);
+}
+
+void orc_quantize_q8_0(const float *x, int64_t n_rows, int64_t k, void *out) {
+    orc_quantize_q8_0_padded(x, n_rows, k, k, out);
+}
+
+void orc_quantize_q8_0_padded(const float *x, int64_t n_rows, int64_t k,
+                              int64_t k_pad, void *out) {
+    const int64_t nb = k_pad / ORC_QK;
+    uint8_t *o = (uint8_t *)out;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_rows; ++r) {
+        float buf[ORC_QK];
+        for (int64_t b = 0; b < nb; ++b) {
+            for (int j = 0; j < ORC_QK; ++j) {
+                const int64_t c = b * ORC_QK + j;
+                buf[j] = c < k ? x[r * k + c] : 0.0f;
+            }
+            quant_q8_0_block(buf, o + (r * nb + b) * ORC_BLOCK_BYTES);
+        }
+    }
+}
+
+void orc_dequantize_q8_0(const void *blocks, int64_t n_rows, int64_t k_pad,
+                         float *y) {
+    const int64_t nb = k_pad / ORC_QK;
+    const uint8_t *p = (const uint8_t *)blocks;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t *blk = p + (r * nb + b) * ORC_BLOCK_BYTES;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            const float d = orc_fp16_to_fp32(dh);
+            const int8_t *qs = (const int8_t *)(blk + 2);
+            for (int j = 0; j < ORC_QK; ++j) y[r * k_pad + b * ORC_QK + j] = (float)qs[j] * d;
+        }
+    }
+}
+
+void orc_quantize_q8_1(const float *x, int64_t M, int64_t K, int64_t ldx,
+                       int64_t K_pad, int8_t *qs, uint16_t *ds) {
+    const int64_t nb = K_pad / ORC_QK;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t b = 0; b < nb; ++b) {
+            float v[ORC_QK];
+            float amax = 0.0f;
+            for (int j = 0; j < ORC_QK; ++j) {
+                const int64_t c = b * ORC_QK + j;
+                v[j] = c < K ? x[m * ldx + c] : 0.0f;
+                const float a = fabsf(v[j]);
+                if (a > amax) amax = a;
+            }
+            const float d = amax / 127.0f;
+            const float inv = amax != 0.0f ? 127.0f / amax : 0.0f;
+            int sum = 0;
+            int8_t *q = qs + m * K_pad + b * ORC_QK;
+            for (int j = 0; j < ORC_QK; ++j) {
+                int iq = (int)nearbyintf(v[j] * inv); /* default mode: half-even */
+                if (iq > 127) iq = 127;
+                if (iq < -128) iq = -128;
+                q[j] = (int8_t)iq;
+                sum += iq;
+            }
+            ds[(m * nb + b) * 2 + 0] = orc_fp32_to_fp16(d);
+            ds[(m * nb + b) * 2 + 1] = orc_fp32_to_fp16((float)sum * d);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMM                                                                      */
+/* ------------------------------------------------------------------------ */
+
+int32_t orc_block_dot(const int8_t *qa, const int8_t *qb) {
+    int32_t s = 0;
+    for (int j = 0; j < ORC_QK; ++j) s += (int32_t)qa[j] * (int32_t)qb[j];
+    return s;
+}
+
+void orc_block_dots(const void *w, int64_t K_pad, int64_t n,
+                    const int8_t *qs, int64_t m, int32_t *out) {
+    const int64_t nb = K_pad / ORC_QK;
+    const uint8_t *wrow = (const uint8_t *)w + n * nb * ORC_BLOCK_BYTES;
+    for (int64_t b = 0; b < nb; ++b)
+        out[b] = orc_block_dot((const int8_t *)(wrow + b * ORC_BLOCK_BYTES + 2),
+                               qs + m * K_pad + b * ORC_QK);
+}
+
+/* Split the 34-byte blocks of W into a contiguous int8 plane and a float
+ * scale plane so the inner loop vectorises; the arithmetic is unchanged. */
+void orc_mul_mat_q8_0_q8_1(const void *w, int64_t K_pad, int64_t N,
+                           const int8_t *qs, const uint16_t *ds, int64_t M,
+                           float *y, int nthreads) {
+    const int64_t nb = K_pad / ORC_QK;
+    int8_t *wq = (int8_t *)malloc((size_t)(N * K_pad));
+    float *wd = (float *)malloc(sizeof(float) * (size_t)(N * nb));
+    float *xd = (float *)malloc(sizeof(float) * (size_t)(M * nb));
+    const uint8_t *wp = (const uint8_t *)w;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t *blk = wp + (n * nb + b) * ORC_BLOCK_BYTES;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            wd[n * nb + b] = orc_fp16_to_fp32(dh);
+            memcpy(wq + n * K_pad + b * ORC_QK, blk + 2, ORC_QK);
+        }
+    for (int64_t i = 0; i < M * nb; ++i) xd[i] = orc_fp16_to_fp32(ds[2 * i]);
+
+    const int nt = orc_threads(nthreads);
+    /* tile over (m, n) so a W tile stays in cache across a few rows */
+    const int64_t TN = 64;
+    const int64_t n_tiles = (N + TN - 1) / TN;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt) collapse(2)
+    for (int64_t mt = 0; mt < (M + 3) / 4; ++mt) {
+        for (int64_t nt_ = 0; nt_ < n_tiles; ++nt_) {
+            for (int64_t m = mt * 4; m < mt * 4 + 4 && m < M; ++m) {
+                const int8_t *xr = qs + m * K_pad;
+                const float *xdr = xd + m * nb;
+                for (int64_t n = nt_ * TN; n < nt_ * TN + TN && n < N; ++n) {
+                    const int8_t *wr = wq + n * K_pad;
+                    const float *wdr = wd + n * nb;
+                    float acc = 0.0f;
+                    for (int64_t b = 0; b < nb; ++b) {
+                        const int8_t *a = wr + b * ORC_QK;
+                        const int8_t *c = xr + b * ORC_QK;
+                        int32_t s = 0;
+                        for (int j = 0; j < ORC_QK; ++j) s += (int32_t)a[j] * (int32_t)c[j];
+                        acc = fmaf((float)s, wdr[b] * xdr[b], acc);
+                    }
+                    y[m * N + n] = acc;
+                }
+            }
+        }
+    }
+    free(wq);
+    free(wd);
+    free(xd);
+}
+
+void orc_mul_mat_q8_0_f32(const void *w, int64_t K_pad, int64_t N,
+                          const float *x, int64_t K, int64_t ldx, int64_t M,
+                          float *y, int nthreads) {
+    const int64_t nb = K_pad / ORC_QK;
+    int8_t *qs = (int8_t *)malloc((size_t)(M * K_pad));
+    uint16_t *ds = (uint16_t *)malloc(sizeof(uint16_t) * 2 * (size_t)(M * nb));
+    orc_quantize_q8_1(x, M, K, ldx, K_pad, qs, ds);
+    orc_mul_mat_q8_0_q8_1(w, K_pad, N, qs, ds, M, y, nthreads);
+    free(qs);
+    free(ds);
+}
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm / GELU                                                          */
+/* ------------------------------------------------------------------------ */
+
+void orc_layernorm(const float *x, int64_t M, int64_t H, int64_t ldx,
+                   const float *w, const float *b, float eps, float *y,
+                   int64_t ldy) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        const float *xr = x + m * ldx;
+        float *yr = y + m * ldy;
+        double sum = 0.0;
+        for (int64_t i = 0; i < H; ++i) sum += (double)xr[i];
+        const float mean = (float)(sum / (double)H);
+        double sum2 = 0.0;
+        for (int64_t i = 0; i < H; ++i) {
+            const float v = xr[i] - mean;
+            yr[i] = v;
+            sum2 += (double)(v * v);
+        }
+        const float variance = (float)(sum2 / (double)H);
+        const float scale = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < H; ++i) {
+            float t = yr[i] * scale;
+            if (w) t = t * w[i];
+            if (b) t = t + b[i];
+            yr[i] = t;
+        }
+    }
+}
+
+float orc_gelu(float x) {
+    const float GELU_COEF_A = 0.044715f;
+    const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
+    return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+}
+
+/* ------------------------------------------------------------------------ */
+/* attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
+                   int64_t d_head, float scale, const uint8_t *key_valid,
+                   float *out) {
+    const int64_t H = n_head * d_head;
+    /* fp16-rounded K and V, as cast by the reference before FA */
+    float *k16 = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    float *v16 = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    for (int64_t p = 0; p < n_pos; ++p)
+        for (int64_t i = 0; i < H; ++i) {
+            k16[p * H + i] = fp16r(qkv[p * 3 * H + H + i]);
+            v16[p * H + i] = fp16r(qkv[p * 3 * H + 2 * H + i]);
+        }
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t h = 0; h < n_head; ++h) {
+        for (int64_t i = 0; i < n_pos; ++i) {
+            double *s = (double *)malloc(sizeof(double) * (size_t)n_pos);
+            const float *q = qkv + i * 3 * H + h * d_head;
+            double mx = -INFINITY;
+            for (int64_t j = 0; j < n_pos; ++j) {
+                if (key_valid && !key_valid[j]) { s[j] = -INFINITY; continue; }
+                const float *k = k16 + j * H + h * d_head;
+                double acc = 0.0;
+                for (int64_t d = 0; d < d_head; ++d) acc += (double)q[d] * (double)k[d];
+                s[j] = acc * (double)scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            double den = 0.0;
+            for (int64_t j = 0; j < n_pos; ++j) {
+                s[j] = (s[j] == -INFINITY) ? 0.0 : exp(s[j] - mx);
+                den += s[j];
+            }
+            for (int64_t d = 0; d < d_head; ++d) {
+                double acc = 0.0;
+                for (int64_t j = 0; j < n_pos; ++j)
+                    if (s[j] != 0.0) acc += s[j] * (double)v16[j * H + h * d_head + d];
+                out[i * H + h * d_head + d] = (float)(acc / den);
+            }
+            free(s);
+        }
+    }
+    free(k16);
+    free(v16);
+}
+
+/* ------------------------------------------------------------------------ */
+/* position embedding resize                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Per-axis anti-aliased linear filter: for output i, taps start at xmin[i],
+ * count xsize[i], weights wt[i*max + j] (normalised). */
+static void aa_weights(int64_t in_size, int64_t out_size, int64_t *xmin,
+                       int64_t *xsize, float *wt, int64_t max_taps) {
+    const float scale = (float)in_size / (float)out_size;
+    const float support = scale >= 1.0f ? scale : 1.0f;
+    const float invscale = scale >= 1.0f ? 1.0f / scale : 1.0f;
+    for (int64_t i = 0; i < out_size; ++i) {
+        const float center = scale * ((float)i + 0.5f);
+        int64_t lo = (int64_t)(center - support + 0.5f);
+        if (lo < 0) lo = 0;
+        int64_t hi = (int64_t)(center + support + 0.5f);
+        if (hi > in_size) hi = in_size;
+        const int64_t n = hi - lo;
+        float total = 0.0f;
+        for (int64_t j = 0; j < max_taps; ++j) wt[i * max_taps + j] = 0.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            float t = ((float)(j + lo) - center + 0.5f) * invscale;
+            if (t < 0.0f) t = -t;
+            const float w = t < 1.0f ? 1.0f - t : 0.0f;
+            wt[i * max_taps + j] = w;
+            total += w;
+        }
+        if (total != 0.0f)
+            for (int64_t j = 0; j < n; ++j) wt[i * max_taps + j] /= total;
+        xmin[i] = lo;
+        xsize[i] = n;
+    }
+}
+
+void orc_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
+                          int64_t out_h, int64_t out_w, float *out) {
+    const int64_t mt = 2 * (n_side > out_h ? n_side : out_h) + 4;
+    int64_t *xmin = (int64_t *)malloc(sizeof(int64_t) * (size_t)(out_w + out_h));
+    int64_t *xsz = (int64_t *)malloc(sizeof(int64_t) * (size_t)(out_w + out_h));
+    float *wx = (float *)malloc(sizeof(float) * (size_t)(out_w * mt));
+    float *wy = (float *)malloc(sizeof(float) * (size_t)(out_h * mt));
+    aa_weights(n_side, out_w, xmin, xsz, wx, mt);
+    aa_weights(n_side, out_h, xmin + out_w, xsz + out_w, wy, mt);
+    /* width pass: (n_side rows, out_w cols) */
+    float *tmp = (float *)malloc(sizeof(float) * (size_t)(n_side * out_w * H));
+    for (int64_t y = 0; y < n_side; ++y)
+        for (int64_t x = 0; x < out_w; ++x)
+            for (int64_t c = 0; c < H; ++c) {
+                float t = 0.0f;
+                for (int64_t j = 0; j < xsz[x]; ++j)
+                    t += pos[(y * n_side + xmin[x] + j) * H + c] * wx[x * mt + j];
+                tmp[(y * out_w + x) * H + c] = t;
+            }
+    /* height pass */
+    for (int64_t y = 0; y < out_h; ++y)
+        for (int64_t x = 0; x < out_w; ++x)
+            for (int64_t c = 0; c < H; ++c) {
+                float t = 0.0f;
+                for (int64_t j = 0; j < xsz[out_w + y]; ++j)
+                    t += tmp[((xmin[out_w + y] + j) * out_w + x) * H + c] * wy[y * mt + j];
+                out[(y * out_w + x) * H + c] = t;
+            }
+    free(tmp);
+    free(wx);
+    free(wy);
+    free(xmin);
+    free(xsz);
+}
+
+/* ------------------------------------------------------------------------ */
+/* model                                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* y = mm(W, x) + bias  (ggml_add(ggml_mul_mat(W, x), b)) */
+static void linear(const void *w, const float *bias, int64_t K, int64_t K_pad,
+                   int64_t N, const float *x, int64_t ldx, int64_t M, float *y,
+                   int nthreads) {
+    orc_mul_mat_q8_0_f32(w, K_pad, N, x, K, ldx, M, y, nthreads);
+    if (bias)
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t n = 0; n < N; ++n) y[m * N + n] = y[m * N + n] + bias[n];
+}
+
+void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
+                       int32_t n_head, float eps, float *x, int64_t n_pos,
+                       const uint8_t *key_valid, int nthreads) {
+    const int64_t d_head = H / n_head;
+    const float kq_scale = 1.0f / sqrtf((float)d_head);
+    float *h = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    float *qkv = (float *)malloc(sizeof(float) * (size_t)(n_pos * 3 * H));
+    float *att = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    float *o = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    float *u = (float *)malloc(sizeof(float) * (size_t)(n_pos * F));
+
+    orc_layernorm(x, n_pos, H, H, L->ln1_w, L->ln1_b, eps, h, H);
+    linear(L->qkv_w, L->qkv_b, H, H, 3 * H, h, H, n_pos, qkv, nthreads);
+    orc_attention(qkv, n_pos, n_head, d_head, kq_scale, key_valid, att);
+    linear(L->o_w, L->o_b, H, H, H, att, H, n_pos, o, nthreads);
+    for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
+
+    orc_layernorm(x, n_pos, H, H, L->ln2_w, L->ln2_b, eps, h, H);
+    linear(L->up_w, L->up_b, H, H, F, h, H, n_pos, u, nthreads);
+    for (int64_t i = 0; i < n_pos * F; ++i) u[i] = orc_gelu(u[i]);
+    linear(L->down_w, L->down_b, F, F_pad, H, u, F, n_pos, o, nthreads);
+    for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
+
+    free(h);
+    free(qkv);
+    free(att);
+    free(o);
+    free(u);
+}
+
+void orc_vision_encode(const orc_vision_model *m, const float *pixels,
+                       int32_t n_h, int32_t n_w, int32_t pooling, float *out,
+                       float *hidden_out, int nthreads) {
+    const int64_t H = m->hidden, F = m->inter, F_pad = m->inter_pad;
+    const int64_t n_pos = (int64_t)n_h * n_w;
+    const int64_t d_head = H / m->n_head;
+    const float kq_scale = 1.0f / sqrtf((float)d_head);
+    float *x = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    float *pos = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+
+    /* patch embedding + position embedding (src/siglip2_vision.cpp:676-691) */
+    linear(m->patch_w, m->patch_b, m->patch_dim, m->patch_dim, H, pixels,
+           m->patch_dim, n_pos, x, nthreads);
+    if (n_h == m->n_side && n_w == m->n_side)
+        memcpy(pos, m->pos_embd, sizeof(float) * (size_t)(n_pos * H));
+    else
+        orc_resize_pos_embed(m->pos_embd, m->n_side, H, n_h, n_w, pos);
+    for (int64_t i = 0; i < n_pos * H; ++i) x[i] = x[i] + pos[i];
+
+    for (int32_t l = 0; l < m->n_layer; ++l)
+        orc_encoder_block(&m->layers[l], (int32_t)H, (int32_t)F, (int32_t)F_pad,
+                          m->n_head, m->eps, x, n_pos, NULL, nthreads);
+
+    orc_layernorm(x, n_pos, H, H, m->post_ln_w, m->post_ln_b, m->eps, x, H);
+    if (hidden_out) memcpy(hidden_out, x, sizeof(float) * (size_t)(n_pos * H));
+
+    if (pooling == 0) {
+        /* mean over patches (src/siglip2_vision.cpp:699-701) */
+        for (int64_t c = 0; c < H; ++c) {
+            double s = 0.0;
+            for (int64_t p = 0; p < n_pos; ++p) s += (double)x[p * H + c];
+            out[c] = (float)s / (float)n_pos;
+        }
+    } else {
+        /* MAP probe head (src/siglip2_vision.cpp:249-314) */
+        float *q = (float *)malloc(sizeof(float) * (size_t)H);
+        float *a = (float *)malloc(sizeof(float) * (size_t)H);
+        float *a2 = (float *)malloc(sizeof(float) * (size_t)H);
+        float *t = (float *)malloc(sizeof(float) * (size_t)H);
+        float *u = (float *)malloc(sizeof(float) * (size_t)F);
+        float *k = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+        float *v = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+        linear(m->hq_w, m->hq_b, H, H, H, m->probe, H, 1, q, nthreads);
+        linear(m->hk_w, m->hk_b, H, H, H, x, H, n_pos, k, nthreads);
+        linear(m->hv_w, m->hv_b, H, H, H, x, H, n_pos, v, nthreads);
+        /* single-query attention over the n_pos keys; K, V rounded to fp16
+         * as the reference casts them before FA */
+        {
+            const int64_t nh = m->n_head;
+            for (int64_t h = 0; h < nh; ++h) {
+                double *s = (double *)malloc(sizeof(double) * (size_t)n_pos);
+                double mx = -INFINITY;
+                for (int64_t j = 0; j < n_pos; ++j) {
+                    double acc = 0.0;
+                    for (int64_t d = 0; d < d_head; ++d)
+                        acc += (double)q[h * d_head + d] * (double)fp16r(k[j * H + h * d_head + d]);
+                    s[j] = acc * (double)kq_scale;
+                    if (s[j] > mx) mx = s[j];
+                }
+                double den = 0.0;
+                for (int64_t j = 0; j < n_pos; ++j) {
+                    s[j] = exp(s[j] - mx);
+                    den += s[j];
+                }
+                for (int64_t d = 0; d < d_head; ++d) {
+                    double acc = 0.0;
+                    for (int64_t j = 0; j < n_pos; ++j)
+                        acc += s[j] * (double)fp16r(v[j * H + h * d_head + d]);
+                    t[h * d_head + d] = (float)(acc / den);
+                }
+                free(s);
+            }
+        }
+        linear(m->ho_w, m->ho_b, H, H, H, t, H, 1, a, nthreads);
+        orc_layernorm(a, 1, H, H, m->hln_w, m->hln_b, m->eps, a2, H);
+        linear(m->hup_w, m->hup_b, H, H, F, a2, H, 1, u, nthreads);
+        for (int64_t i = 0; i < F; ++i) u[i] = orc_gelu(u[i]);
+        linear(m->hdown_w, m->hdown_b, F, F_pad, H, u, F, 1, a2, nthreads);
+        for (int64_t i = 0; i < H; ++i) out[i] = a[i] + a2[i];
+        free(q);
+        free(a);
+        free(a2);
+        free(t);
+        free(u);
+        free(k);
+        free(v);
+    }
+    free(x);
+    free(pos);
+}
+
+void orc_text_encode(const orc_text_model *m, const int32_t *tokens,
+                     int32_t n_tok, const int32_t *mask, float *out,
+                     int nthreads) {
+    if (n_tok <= 0) return;
+    const int64_t H = m->hidden;
+    const int64_t n_pos = n_tok;
+    float *x = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    uint8_t *kv = NULL;
+    /* token rows (Q8_0 get_rows = dequantize) + position rows
+     * (src/siglip2_text.cpp:649-658) */
+    for (int64_t p = 0; p < n_pos; ++p) {
+        const uint8_t *row = (const uint8_t *)m->tok_embd +
+                             (int64_t)tokens[p] * (H / ORC_QK) * ORC_BLOCK_BYTES;
+        orc_dequantize_q8_0(row, 1, H, x + p * H);
+        for (int64_t c = 0; c < H; ++c) x[p * H + c] = x[p * H + c] + m->pos_embd[p * H + c];
+    }
+    if (mask) {
+        kv = (uint8_t *)malloc((size_t)n_pos);
+        for (int64_t p = 0; p < n_pos; ++p) kv[p] = mask[p] != 0;
+    }
+    for (int32_t l = 0; l < m->n_layer; ++l)
+        orc_encoder_block(&m->layers[l], (int32_t)H, m->inter, m->inter_pad,
+                          m->n_head, m->eps, x, n_pos, kv, nthreads);
+    orc_layernorm(x, n_pos, H, H, m->final_ln_w, m->final_ln_b, m->eps, x, H);
+    /* last-token pooling + head (src/siglip2_text.cpp:667-675) */
+    linear(m->head_w, m->head_b, H, H, m->proj, x + (n_pos - 1) * H, H, 1, out,
+           nthreads);
+    free(x);
+    free(kv);
+}

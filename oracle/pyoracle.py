@@ -1,0 +1,253 @@
+"""ctypes binding of the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's CPU-baseline leg, never by the product.  Build with `make -C oracle`.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+_lib = None
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+
+class OrcLayer(ctypes.Structure):
+    _fields_ = [(n, _p) for n in (
+        "ln1_w", "ln1_b", "qkv_w", "qkv_b", "o_w", "o_b", "ln2_w", "ln2_b",
+        "up_w", "up_b", "down_w", "down_b")]
+
+
+class OrcVision(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _i32), ("inter", _i32), ("inter_pad", _i32), ("n_head", _i32),
+        ("n_layer", _i32), ("patch_dim", _i32), ("n_side", _i32), ("eps", _f32),
+        ("patch_w", _p), ("patch_b", _p), ("pos_embd", _p), ("post_ln_w", _p),
+        ("post_ln_b", _p), ("probe", _p), ("hq_w", _p), ("hk_w", _p), ("hv_w", _p),
+        ("ho_w", _p), ("hq_b", _p), ("hk_b", _p), ("hv_b", _p), ("ho_b", _p),
+        ("hln_w", _p), ("hln_b", _p), ("hup_w", _p), ("hup_b", _p), ("hdown_w", _p),
+        ("hdown_b", _p), ("layers", ctypes.POINTER(OrcLayer)),
+    ]
+
+
+class OrcText(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _i32), ("inter", _i32), ("inter_pad", _i32), ("n_head", _i32),
+        ("n_layer", _i32), ("vocab", _i32), ("max_pos", _i32), ("proj", _i32),
+        ("eps", _f32), ("tok_embd", _p), ("pos_embd", _p), ("final_ln_w", _p),
+        ("final_ln_b", _p), ("head_w", _p), ("head_b", _p),
+        ("layers", ctypes.POINTER(OrcLayer)),
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} missing; run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_fp32_to_fp16_n": ([_p, _p, _i64], None),
+            "orc_fp16_to_fp32_n": ([_p, _p, _i64], None),
+            "orc_quantize_q8_0_padded": ([_p, _i64, _i64, _i64, _p], None),
+            "orc_dequantize_q8_0": ([_p, _i64, _i64, _p], None),
+            "orc_quantize_q8_1": ([_p, _i64, _i64, _i64, _i64, _p, _p], None),
+            "orc_block_dots": ([_p, _i64, _i64, _p, _i64, _p], None),
+            "orc_mul_mat_q8_0_q8_1": ([_p, _i64, _i64, _p, _p, _i64, _p, ctypes.c_int], None),
+            "orc_mul_mat_q8_0_f32": ([_p, _i64, _i64, _p, _i64, _i64, _i64, _p, ctypes.c_int], None),
+            "orc_layernorm": ([_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64], None),
+            "orc_gelu": ([_f32], _f32),
+            "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
+            "orc_resize_pos_embed": ([_p, _i64, _i64, _i64, _i64, _p], None),
+            "orc_vision_encode": ([ctypes.POINTER(OrcVision), _p, _i32, _i32, _i32, _p, _p,
+                                   ctypes.c_int], None),
+            "orc_text_encode": ([ctypes.POINTER(OrcText), _p, _i32, _p, _p, ctypes.c_int], None),
+        }
+        for name, (args, res) in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+def fp32_to_fp16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_fp32_to_fp16_n(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def fp16_to_fp32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    y = np.empty(h.shape, np.float32)
+    lib().orc_fp16_to_fp32_n(_ptr(h), _ptr(y), h.size)
+    return y
+
+
+def quantize_q8_0(w, k_pad=None):
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    k_pad = k if k_pad is None else k_pad
+    out = np.empty((n, k_pad // 32 * 34), np.uint8)
+    lib().orc_quantize_q8_0_padded(_ptr(w), n, k, k_pad, _ptr(out))
+    return out
+
+
+def dequantize_q8_0(raw, n, k_pad):
+    y = np.empty((n, k_pad), np.float32)
+    lib().orc_dequantize_q8_0(_ptr(np.ascontiguousarray(raw)), n, k_pad, _ptr(y))
+    return y
+
+
+def quantize_q8_1(x, k_pad=None):
+    """x (M, K) float32 -> qs (M, k_pad) int8, ds (M, k_pad/32, 2) uint16."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    k_pad = K if k_pad is None else k_pad
+    qs = np.empty((M, k_pad), np.int8)
+    ds = np.empty((M, k_pad // 32, 2), np.uint16)
+    lib().orc_quantize_q8_1(_ptr(x), M, K, K, k_pad, _ptr(qs), _ptr(ds))
+    return qs, ds
+
+
+def block_dots(w_raw, k_pad, n, qs, m):
+    out = np.empty(k_pad // 32, np.int32)
+    lib().orc_block_dots(_ptr(np.ascontiguousarray(w_raw)), k_pad, n,
+                         _ptr(np.ascontiguousarray(qs)), m, _ptr(out))
+    return out
+
+
+def mul_mat_q8_0_q8_1(w_raw, k_pad, n, qs, ds, nthreads=0):
+    M = qs.shape[0]
+    y = np.empty((M, n), np.float32)
+    lib().orc_mul_mat_q8_0_q8_1(_ptr(np.ascontiguousarray(w_raw)), k_pad, n,
+                                _ptr(np.ascontiguousarray(qs)), _ptr(np.ascontiguousarray(ds)),
+                                M, _ptr(y), nthreads)
+    return y
+
+
+def mul_mat_q8_0_f32(w_raw, k_pad, n, x, nthreads=0):
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    y = np.empty((M, n), np.float32)
+    lib().orc_mul_mat_q8_0_f32(_ptr(np.ascontiguousarray(w_raw)), k_pad, n, _ptr(x), K, K, M,
+                               _ptr(y), nthreads)
+    return y
+
+
+def layernorm(x, w, b, eps=1e-6):
+    x = np.ascontiguousarray(x, np.float32)
+    M, H = x.shape
+    y = np.empty_like(x)
+    lib().orc_layernorm(_ptr(x), M, H, H, _ptr(w), _ptr(b), eps, _ptr(y), H)
+    return y
+
+
+def gelu(x):
+    f = lib().orc_gelu
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.float32).reshape(np.shape(x))
+
+
+def attention(qkv, n_head, d_head, scale, key_valid=None):
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    n_pos = qkv.shape[0]
+    out = np.empty((n_pos, n_head * d_head), np.float32)
+    kv = None if key_valid is None else np.ascontiguousarray(key_valid, np.uint8)
+    lib().orc_attention(_ptr(qkv), n_pos, n_head, d_head, scale, _ptr(kv), _ptr(out))
+    return out
+
+
+def resize_pos_embed(pos, n_side, out_h, out_w):
+    pos = np.ascontiguousarray(pos, np.float32)
+    H = pos.shape[-1]
+    out = np.empty((out_h * out_w, H), np.float32)
+    lib().orc_resize_pos_embed(_ptr(pos), n_side, H, out_h, out_w, _ptr(out))
+    return out
+
+
+LAYER_KEYS = [f[0] for f in OrcLayer._fields_]
+
+
+class _Model:
+    def __init__(self, struct, keep):
+        self.struct = struct
+        self._keep = keep
+
+
+def vision_model(host):
+    """Oracle view of an s2x.synth HostModel (vision): same host bytes."""
+    cfg, t = host.cfg, host.tensors
+    keep = []
+
+    def P(a):
+        a = np.ascontiguousarray(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    larr = (OrcLayer * max(1, cfg.n_layer))()
+    for l, L in enumerate(host.layers):
+        for k in LAYER_KEYS:
+            setattr(larr[l], k, P(L[k]))
+    keep.append(larr)
+    s = OrcVision()
+    s.hidden, s.inter, s.inter_pad, s.n_head = cfg.hidden, cfg.inter, cfg.inter_pad, cfg.n_head
+    s.n_layer, s.patch_dim, s.n_side, s.eps = cfg.n_layer, cfg.patch_dim, cfg.n_side, cfg.eps
+    for k, v in t.items():
+        setattr(s, k, P(v))
+    s.layers = ctypes.cast(larr, ctypes.POINTER(OrcLayer))
+    return _Model(s, keep)
+
+
+def text_model(host):
+    cfg, t = host.cfg, host.tensors
+    keep = []
+
+    def P(a):
+        a = np.ascontiguousarray(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    larr = (OrcLayer * max(1, cfg.n_layer))()
+    for l, L in enumerate(host.layers):
+        for k in LAYER_KEYS:
+            setattr(larr[l], k, P(L[k]))
+    keep.append(larr)
+    s = OrcText()
+    s.hidden, s.inter, s.inter_pad, s.n_head = cfg.hidden, cfg.inter, cfg.inter_pad, cfg.n_head
+    s.n_layer, s.vocab, s.max_pos, s.proj, s.eps = (cfg.n_layer, cfg.vocab, cfg.max_pos,
+                                                    cfg.proj, cfg.eps)
+    for k, v in t.items():
+        setattr(s, k, P(v))
+    s.layers = ctypes.cast(larr, ctypes.POINTER(OrcLayer))
+    return _Model(s, keep)
+
+
+def vision_encode(model, pixels, n_h, n_w, pooling=1, nthreads=0, hidden=False):
+    H = model.struct.hidden
+    out = np.empty(H, np.float32)
+    hid = np.empty((n_h * n_w, H), np.float32) if hidden else None
+    px = np.ascontiguousarray(pixels, np.float32)
+    lib().orc_vision_encode(ctypes.byref(model.struct), _ptr(px), n_h, n_w, pooling, _ptr(out),
+                            _ptr(hid), nthreads)
+    return (out, hid) if hidden else out
+
+
+def text_encode(model, ids, mask=None, nthreads=0):
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.empty(model.struct.proj, np.float32)
+    m = None if mask is None else np.ascontiguousarray(mask, np.int32)
+    lib().orc_text_encode(ctypes.byref(model.struct), _ptr(ids), ids.size, _ptr(m), _ptr(out),
+                          nthreads)
+    return out

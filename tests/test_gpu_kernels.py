@@ -1,0 +1,320 @@
+"""Kernel-level parity on the GPU, through the C-ABI, against the CPU oracle
+on identical seeded inputs.  Integer/byte stages are compared bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import s2x
+from s2x import synth
+from gpu_util import cos, dev, empty, host, ptr, say, stream, zeros
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (label, N, K, K_pad) -- the vision layer GEMMs
+    ("qkv", 3456, 1152, 1152),
+    ("out", 1152, 1152, 1152),
+    ("fc1", 4304, 1152, 1152),
+    ("fc2", 1152, 4304, 4320),
+]
+
+
+def _quant_gpu(x, k_pad):
+    M, K = x.shape
+    xd = dev(x)
+    qs = empty((M, k_pad), torch.int8)
+    ds = empty((M, k_pad // 32, 2), torch.int16)
+    s2x.call("s2x_quantize_q8_1", ptr(xd), K, M, K, k_pad, ptr(qs), ptr(ds), stream())
+    return qs, ds
+
+
+@pytest.mark.parametrize("M,K,K_pad", [(729, 1152, 1152), (23328, 1152, 1152), (729, 4304, 4320),
+                                       (100, 768, 768), (1, 1152, 1152), (3, 32, 64)])
+def test_quantize_q8_1_bit_exact(orc, M, K, K_pad):
+    say(f"quantize M={M} K={K} K_pad={K_pad}")
+    rng = np.random.default_rng(M + K)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.01, 30, (M, 1))).astype(np.float32)
+    x[0, :64] = 0.0
+    if K >= 64:
+        x[min(1, M - 1), :32] = np.float32(127.0)
+        x[min(1, M - 1), 1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5]
+    qs, ds = _quant_gpu(x, K_pad)
+    rq, rd = orc.quantize_q8_1(x, K_pad)
+    assert np.array_equal(host(qs), rq)
+    assert np.array_equal(host(ds).view(np.uint16), rd)
+
+
+def test_quantize_strided_input(orc):
+    rng = np.random.default_rng(1)
+    full = rng.standard_normal((50, 4400)).astype(np.float32)
+    xd = dev(full)
+    qs = empty((50, 4320), torch.int8)
+    ds = empty((50, 135, 2), torch.int16)
+    s2x.call("s2x_quantize_q8_1", ptr(xd), 4304, 50, 4400, 4320, ptr(qs), ptr(ds), stream())
+    rq, rd = orc.quantize_q8_1(np.ascontiguousarray(full[:, :4304]), 4320)
+    assert np.array_equal(host(qs), rq) and np.array_equal(host(ds).view(np.uint16), rd)
+
+
+def test_layernorm_quantize(orc):
+    rng = np.random.default_rng(2)
+    M, H = 729, 1152
+    x = (rng.standard_normal((M, H)) * 2 + 0.3).astype(np.float32)
+    w = rng.normal(1, 0.02, H).astype(np.float32)
+    b = rng.normal(0, 0.02, H).astype(np.float32)
+    xd, wd, bd = dev(x), dev(w), dev(b)
+    qs = empty((M, H), torch.int8)
+    ds = empty((M, H // 32, 2), torch.int16)
+    y = empty((M, H), torch.float32)
+    s2x.call("s2x_layernorm_quantize_q8_1", ptr(xd), H, M, H, ptr(wd), ptr(bd), ctypes.c_float(1e-6),
+             ptr(qs), ptr(ds), ptr(y), H, stream())
+    yg = host(y)
+    ref = orc.layernorm(x, w, b, 1e-6)
+    assert np.abs(yg - ref).max() < 2e-6 * np.abs(ref).max()
+    # the fused quantizer is bit-exact on the GPU's own LN output
+    rq, rd = orc.quantize_q8_1(yg)
+    assert np.array_equal(host(qs), rq) and np.array_equal(host(ds).view(np.uint16), rd)
+    # and within one LSB of quantizing the CPU LN output
+    cq, _ = orc.quantize_q8_1(ref)
+    assert np.abs(host(qs).astype(np.int32) - cq).max() <= 1
+    # LN alone
+    y2 = empty((M, H), torch.float32)
+    s2x.call("s2x_layernorm", ptr(xd), H, M, H, ptr(wd), ptr(bd), ctypes.c_float(1e-6), ptr(y2), H,
+             stream())
+    assert np.array_equal(host(y2), yg)
+
+
+def _weight(raw, k_pad, n):
+    w = ctypes.c_void_p()
+    s2x.call("s2x_weight_create", raw.ctypes.data, 1, k_pad, n, None, ctypes.byref(w))
+    return w
+
+
+@pytest.fixture(scope="module")
+def gemm_data():
+    data = {}
+    for label, N, K, K_pad in SHAPES:
+        rng = np.random.default_rng(N * 7 + K)
+        wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        raw = synth.quantize_q8_0(wf, K_pad)
+        data[label] = (raw, N, K, K_pad)
+    return data
+
+
+@pytest.mark.parametrize("label", [s[0] for s in SHAPES])
+def test_block_dots_bit_exact(orc, gemm_data, label):
+    raw, N, K, K_pad = gemm_data[label]
+    say(f"block dots {label}")
+    M = 729
+    x = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)
+    rq, _ = orc.quantize_q8_1(x, K_pad)
+    w = _weight(raw, K_pad, N)
+    try:
+        wq = raw.reshape(N, K_pad // 32, 34)[:, :, 2:].copy().view(np.int8).astype(np.int64)
+        KB = K_pad // 32
+        for kb in sorted({0, KB // 2, KB - 1}):
+            out = empty((M, N), torch.int32)
+            s2x.call("s2x_block_dots", w, ptr(qs), M, kb, ptr(out), stream())
+            ref = rq[:, kb * 32:(kb + 1) * 32].astype(np.int64) @ wq[:, kb, :].T
+            assert np.array_equal(host(out), ref), f"kb={kb}"
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+
+
+def _gemm_terms_abs(orc, raw, N, K_pad, rq, rd):
+    wq = raw.reshape(N, K_pad // 32, 34)[:, :, 2:].copy().view(np.int8).astype(np.float32)
+    dw = orc.fp16_to_fp32(raw.reshape(N, K_pad // 32, 34)[:, :, :2].copy().view(np.uint16)[..., 0])
+    dx = orc.fp16_to_fp32(rd[..., 0])
+    # sum_kb |I| dw dx, for the tolerance floor
+    M = rq.shape[0]
+    acc = np.zeros((M, N), np.float64)
+    for kb in range(K_pad // 32):
+        I = rq[:, kb * 32:(kb + 1) * 32].astype(np.float32) @ wq[:, kb, :].T
+        acc += np.abs(I) * dx[:, kb:kb + 1] * dw[None, :, kb]
+    return acc
+
+
+@pytest.mark.parametrize("label", [s[0] for s in SHAPES])
+def test_gemm_matches_oracle(orc, gemm_data, label):
+    raw, N, K, K_pad = gemm_data[label]
+    M = 729
+    say(f"gemm {label} M={M}")
+    x = np.random.default_rng(4).standard_normal((M, K)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)
+    rq, rd = orc.quantize_q8_1(x, K_pad)
+    ref = orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd)
+    w = _weight(raw, K_pad, N)
+    try:
+        y = empty((M, N), torch.float32)
+        s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, ptr(y), N, None, stream())
+        yg = host(y)
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+    from gpu_util import h5_rel
+    rel = h5_rel(yg, ref.astype(np.float64), _gemm_terms_abs(orc, raw, N, K_pad, rq, rd))
+    n_diff = int((yg != ref).sum())
+    say(f"  max rel err (tau=1e-3 rms) {rel:.3e}, differing elements {n_diff}")
+    assert rel <= 1e-4
+    assert n_diff == 0  # same per-block fma order as the oracle: bit-exact
+
+
+def test_gemm_large_m_batch_invariant(orc, gemm_data):
+    raw, N, K, K_pad = gemm_data["fc2"]
+    M = 23328
+    say("gemm fc2 M=23328")
+    x = np.random.default_rng(5).standard_normal((M, K)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)
+    w = _weight(raw, K_pad, N)
+    try:
+        y = empty((M, N), torch.float32)
+        s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, ptr(y), N, None, stream())
+        yg = host(y)
+        sub = 729
+        y1 = empty((sub, N), torch.float32)
+        s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs[M - sub:]), ptr(ds[M - sub:]), sub, ptr(y1), N,
+                 None, stream())
+        assert np.array_equal(host(y1), yg[M - sub:])
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+    rows = np.random.default_rng(6).choice(M, 64, replace=False)
+    rq, rd = orc.quantize_q8_1(x[rows], K_pad)
+    assert np.array_equal(orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd), yg[rows])
+
+
+def test_drop_in_mul_mat_f32(orc, gemm_data):
+    raw, N, K, K_pad = gemm_data["fc2"]
+    M = 333
+    x = np.random.default_rng(7).standard_normal((M, K)).astype(np.float32)
+    wd, xd = dev(raw), dev(x)
+    y = empty((M, N), torch.float32)
+    ws_bytes = s2x.lib.s2x_mul_mat_workspace_size(K_pad, N, M)
+    ws = empty((ws_bytes,), torch.uint8)
+    s2x.call("s2x_mul_mat_q8_0_f32", ptr(wd), K_pad, N, ptr(xd), K, K, M, ptr(y), ptr(ws),
+             ctypes.c_size_t(ws_bytes), stream())
+    assert np.array_equal(host(y), orc.mul_mat_q8_0_f32(raw, K_pad, N, x))
+    small = ctypes.c_size_t(ws_bytes - 1)
+    assert s2x.lib.s2x_mul_mat_q8_0_f32(ptr(wd), K_pad, N, ptr(xd), K, K, M, ptr(y), ptr(ws), small,
+                                        stream()) == 4
+
+
+@pytest.mark.parametrize("kind", ["bias", "gelu", "resid", "resid_rows", "resid_inplace"])
+def test_gemm_epilogues(orc, gemm_data, kind):
+    raw, N, K, K_pad = gemm_data["out"]
+    M = 300
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.normal(0, 0.02, N).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    pos = rng.standard_normal((100, N)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)
+    rq, rd = orc.quantize_q8_1(x, K_pad)
+    mm = orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd)
+    bd, rdv, pd = dev(bias), dev(res), dev(pos)
+    y = empty((M, N), torch.float32)
+    e = s2x.Epilogue()
+    e.bias = bd.data_ptr()
+    if kind == "bias":
+        e.kind, ref = s2x.EPI_BIAS, mm + bias
+    elif kind == "gelu":
+        e.kind, ref = s2x.EPI_BIAS_GELU, orc.gelu(mm + bias)
+    elif kind == "resid":
+        e.kind, e.resid, e.ld_resid = s2x.EPI_BIAS_RESID, rdv.data_ptr(), N
+        ref = (mm + bias) + res
+    elif kind == "resid_rows":
+        e.kind, e.resid, e.ld_resid, e.resid_rows = s2x.EPI_BIAS_RESID, pd.data_ptr(), N, 100
+        ref = (mm + bias) + pos[np.arange(M) % 100]
+    else:
+        y = rdv
+        e.kind, e.resid, e.ld_resid = s2x.EPI_BIAS_RESID, rdv.data_ptr(), N
+        ref = (mm + bias) + res
+    w = _weight(raw, K_pad, N)
+    try:
+        s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, ptr(y), N, ctypes.byref(e), stream())
+        yg = host(y)
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+    if kind == "gelu":  # device tanhf vs libm tanhf: a few ulp
+        assert np.abs(yg - ref).max() <= 4e-7 * max(1.0, np.abs(ref).max())
+    else:
+        assert np.array_equal(yg, ref.astype(np.float32))
+
+
+def test_standalone_epilogues(orc):
+    rng = np.random.default_rng(9)
+    H, n = 4304, 37
+    mm = rng.standard_normal((n, H)).astype(np.float32)
+    b = rng.normal(0, 0.02, H).astype(np.float32)
+    r = rng.standard_normal((n, H)).astype(np.float32)
+    md, bd, rd = dev(mm), dev(b), dev(r)
+    y = empty((n, H), torch.float32)
+    s2x.call("s2x_bias_residual", ptr(md), ptr(bd), ptr(rd), ptr(y), H, n, stream())
+    assert np.array_equal(host(y), (mm + b) + r)
+    s2x.call("s2x_bias_gelu", ptr(md), ptr(bd), ptr(y), H, n, stream())
+    assert np.abs(host(y) - orc.gelu(mm + b)).max() < 1e-6
+
+
+def _attn_case(orc, lens, n_head=16, dh=72, key_valid=None, seed=10):
+    H = n_head * dh
+    rng = np.random.default_rng(seed)
+    M = int(sum(lens))
+    qkv = (rng.standard_normal((M, 3 * H)) * 1.5).astype(np.float32)
+    bias = rng.normal(0, 0.5, 3 * H).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    lens = np.asarray(lens, np.int32)
+    max_len = int(lens.max())
+    ws_bytes = s2x.lib.s2x_attn_workspace_size(len(lens), max_len, n_head, dh)
+    ws = zeros((ws_bytes,), torch.uint8)
+    qd, bd, sd, ld = dev(qkv), dev(bias), dev(starts), dev(lens)
+    kv = dev(key_valid) if key_valid is not None else None
+    out = empty((M, H), torch.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(dh)))
+    s2x.call("s2x_attn_prep", ptr(qd), 3 * H, ptr(bd), ptr(sd), ptr(ld), len(lens), max_len, n_head,
+             dh, ptr(ws), ctypes.c_size_t(ws_bytes), stream())
+    s2x.call("s2x_attn_run", ptr(ws), ctypes.c_size_t(ws_bytes), ptr(sd), ptr(ld), ptr(kv),
+             len(lens), max_len, n_head, dh, ctypes.c_float(scale), ptr(out), H, stream())
+    og = host(out)
+    biased = qkv + bias
+    errs = []
+    for s, L in zip(starts, lens):
+        kvs = None if key_valid is None else key_valid[s:s + L]
+        ref = orc.attention(biased[s:s + L], n_head, dh, scale, kvs)
+        errs.append(np.abs(og[s:s + L] - ref).max() / np.abs(ref).max())
+        assert cos(og[s:s + L], ref) > 0.99999
+    return max(errs)
+
+
+def test_attention_segments(orc):
+    e = _attn_case(orc, [729, 1, 64, 130, 255, 128])
+    say(f"attention max err / max|out| = {e:.2e}")
+    assert e < 4e-3
+
+
+def test_attention_key_mask(orc):
+    lens = [64, 200]
+    kv = np.ones(264, np.uint8)
+    kv[40:64] = 0
+    kv[64 + 150:] = 0
+    assert _attn_case(orc, lens, key_valid=kv, seed=11) < 4e-3
+
+
+@pytest.mark.parametrize("hw", [(27, 27), (8, 32), (16, 16), (32, 32)])
+def test_resize_pos_embed(orc, hw):
+    h, w = hw
+    pos = np.random.default_rng(12).normal(0, 0.02, (256, 1152)).astype(np.float32)
+    pd = dev(pos)
+    out = empty((h * w, 1152), torch.float32)
+    s2x.call("s2x_resize_pos_embed", ptr(pd), 16, 1152, h, w, ptr(out), stream())
+    assert np.array_equal(host(out), orc.resize_pos_embed(pos, 16, h, w))
+
+
+def test_get_rows_q8_0(orc):
+    rng = np.random.default_rng(13)
+    table = synth.quantize_q8_0(rng.normal(0, 0.02, (500, 1152)).astype(np.float32))
+    ids = rng.integers(0, 500, 70).astype(np.int32)
+    pos = rng.normal(0, 0.02, (64, 1152)).astype(np.float32)
+    td, idd, pd = dev(table), dev(ids), dev(pos)
+    out = empty((70, 1152), torch.float32)
+    s2x.call("s2x_get_rows_q8_0", ptr(td), 1152, 500, ptr(idd), 70, ptr(pd), 35, ptr(out), stream())
+    deq = orc.dequantize_q8_0(table, 500, 1152)
+    assert np.array_equal(host(out), deq[ids] + pos[np.arange(70) % 35])
