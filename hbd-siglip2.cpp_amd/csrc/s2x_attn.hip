@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) void k_attn_prep(
             q = r[0] + bias[h * d_head + d];
             k = r[H] + bias[H + h * d_head + d];
         }
-        Q[head_qk + (int64_t)pos * d_pad + d] = (_Float16)q;
-        K[head_qk + (int64_t)pos * d_pad + d] = (_Float16)k;
+        Q[head_qk + (int64_t)pos * d_pad + d] = f32_to_f16(q);  // (mm + bias) in f32, then f16
+        K[head_qk + (int64_t)pos * d_pad + d] = f32_to_f16(k);
     }
     // V tile into LDS (d fastest reads), then transposed out (p fastest writes)
     for (int i = threadIdx.x; i < PREP_T * dv_pad; i += blockDim.x) {
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void k_attn_prep(
         float v = 0.0f;
         if (pos < len && d < d_head)
             v = qkv[(row0 + pos) * ld + 2 * H + h * d_head + d] + bias[2 * H + h * d_head + d];
-        vs[p][d] = (_Float16)v;
+        vs[p][d] = f32_to_f16(v);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < PREP_T * dv_pad; i += blockDim.x) {

@@ -23,11 +23,24 @@ typedef float    v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h  __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h  __attribute__((ext_vector_type(4)));
 
-// fp32 -> fp16 bits, round-to-nearest-even (v_cvt_f16_f32 under the default
-// mode register), subnormals kept, overflow to inf.
+// Materialise a value as an f32 register.  The AMDGPU backend otherwise
+// folds fptrunc(fmul/fadd ...) into v_fma_mix*_f16, which rounds the exact
+// result once to f16 instead of to f32 and then to f16 -- a different value
+// at f32 ties -- even with contraction disabled.  The empty asm is opaque to
+// that fold and emits no instruction.
+__device__ __forceinline__ float f32_materialize(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
+
+// fp32 -> fp16, round-to-nearest-even (v_cvt_f16_f32 under the default mode
+// register), subnormals kept, overflow to inf; the argument is first rounded
+// to f32 as written.
+__device__ __forceinline__ _Float16 f32_to_f16(float f) {
+    return (_Float16)f32_materialize(f);
+}
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
-    _Float16 h = (_Float16)f;
-    return __builtin_bit_cast(uint16_t, h);
+    return __builtin_bit_cast(uint16_t, f32_to_f16(f));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);

@@ -40,6 +40,19 @@ def host(t):
     return t.cpu().numpy()
 
 
+def assert_same(got, ref, what="", show=12):
+    """Bitwise equality with a report of the first mismatches."""
+    got, ref = np.asarray(got), np.asarray(ref)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    bad = np.argwhere(got != ref)
+    if len(bad):
+        say(f"{what}: {len(bad)} of {got.size} differ; first:")
+        for idx in bad[:show]:
+            t = tuple(idx)
+            say(f"   {t}: got {got[t]!r} ref {ref[t]!r}")
+    assert len(bad) == 0, f"{what}: {len(bad)} mismatches"
+
+
 def cos(a, b):
     a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))

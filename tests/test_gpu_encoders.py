@@ -1,0 +1,230 @@
+"""Encoder-level parity on the GPU: the vision and text towers through the
+C-ABI against the CPU oracle on identical seeded weights and inputs, plus
+the batch / ragged invariances (a batched or packed image must produce the
+same bits as that image alone)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import s2x
+from s2x import synth
+from gpu_util import cos, dev, empty, host, ptr, say
+
+pytestmark = pytest.mark.gpu
+
+SMALL_V = synth.VisionConfig(hidden=288, inter=1076, n_head=4, n_layer=2)
+SMALL_T = synth.TextConfig(hidden=288, inter=1076, n_head=4, n_layer=2, vocab=1000, max_pos=64,
+                           proj=288)
+
+
+class Vision:
+    def __init__(self, hostm):
+        self.host = hostm
+        self.h = ctypes.c_void_p()
+        s2x.call("s2x_vision_create", ctypes.byref(hostm.struct), ctypes.byref(self.h))
+
+    def encode(self, px, n_h, n_w, pooling):
+        out = np.empty(self.host.cfg.hidden, np.float32)
+        px = np.ascontiguousarray(px, np.float32)
+        s2x.call("s2x_vision_encode", self.h, px.ctypes.data, n_h, n_w, pooling, out.ctypes.data)
+        return out
+
+    def batch(self, px, n_img, n_h, n_w, pooling):
+        pd = dev(px)
+        out = empty((n_img, self.host.cfg.hidden), torch.float32)
+        s2x.call("s2x_vision_encode_batch_dev", self.h, ptr(pd), n_img, n_h, n_w, pooling, ptr(out))
+        return host(out)
+
+    def ragged(self, padded, shapes, max_patches, pooling):
+        pd = dev(padded)
+        sh = np.ascontiguousarray(shapes, np.int32)
+        out = empty((len(shapes), self.host.cfg.hidden), torch.float32)
+        s2x.call("s2x_vision_encode_ragged_dev", self.h, ptr(pd), sh.ctypes.data, len(shapes),
+                 max_patches, pooling, ptr(out))
+        return host(out)
+
+    def close(self):
+        s2x.lib.s2x_vision_destroy(self.h)
+
+
+@pytest.fixture(scope="module")
+def small_vision(orc):
+    hm = synth.vision_model(SMALL_V, seed=21)
+    v = Vision(hm)
+    yield v, orc.vision_model(hm)
+    v.close()
+
+
+@pytest.mark.parametrize("grid", [(16, 16), (27, 27), (12, 20), (8, 32)])
+@pytest.mark.parametrize("pooling", [s2x.POOL_PROBE, s2x.POOL_MEAN])
+def test_small_vision_vs_oracle(orc, small_vision, grid, pooling):
+    v, om = small_vision
+    h, w = grid
+    px = synth.pixels(1, h * w, seed=h * 31 + w)
+    g = v.encode(px, h, w, pooling)
+    r = orc.vision_encode(om, px, h, w, pooling=pooling)
+    c = cos(g, r)
+    say(f"small vision {grid} pooling={pooling}: cosine {c:.7f}")
+    assert c >= 0.9999
+
+
+def test_small_vision_batch_invariance(small_vision):
+    v, _ = small_vision
+    px = synth.pixels(3, 729, seed=5)
+    b = v.batch(px, 3, 27, 27, s2x.POOL_PROBE)
+    for i in range(3):
+        one = v.batch(px[i * 729:(i + 1) * 729], 1, 27, 27, s2x.POOL_PROBE)
+        assert np.array_equal(b[i], one[0]), i
+    assert np.array_equal(v.encode(px[:729], 27, 27, s2x.POOL_PROBE), b[0])
+
+
+@pytest.mark.parametrize("pooling", [s2x.POOL_PROBE, s2x.POOL_MEAN])
+def test_small_vision_ragged_equals_per_image(small_vision, pooling):
+    v, _ = small_vision
+    shapes = [(16, 16), (12, 20), (27, 27), (24, 24), (32, 32)]
+    maxp = 1024
+    padded = np.zeros((len(shapes), maxp, 768), np.float32)
+    singles = []
+    for i, (h, w) in enumerate(shapes):
+        px = synth.pixels(1, h * w, seed=100 + i)
+        padded[i, :h * w] = px
+        padded[i, h * w:] = 7.0  # padding content must not matter
+        singles.append(v.batch(px, 1, h, w, pooling)[0])
+    out = v.ragged(padded.reshape(-1, 768), shapes, maxp, pooling)
+    for i in range(len(shapes)):
+        assert np.array_equal(out[i], singles[i]), shapes[i]
+
+
+def test_vision_rejects_bad_shapes(small_vision):
+    v, _ = small_vision
+    px = np.zeros((4, 768), np.float32)
+    out = np.empty(288, np.float32)
+    assert s2x.lib.s2x_vision_encode(v.h, px.ctypes.data, 0, 4, 1, out.ctypes.data) == 1
+    sh = np.array([[40, 40]], np.int32)
+    assert s2x.lib.s2x_vision_encode_ragged_dev(v.h, ctypes.c_void_p(1), sh.ctypes.data, 1, 1024, 1,
+                                                ctypes.c_void_p(1)) == 1
+
+
+class Text:
+    def __init__(self, hostm):
+        self.host = hostm
+        self.h = ctypes.c_void_p()
+        s2x.call("s2x_text_create", ctypes.byref(hostm.struct), ctypes.byref(self.h))
+
+    def encode(self, ids, mask=None):
+        out = np.empty(self.host.cfg.proj, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        m = None if mask is None else np.ascontiguousarray(mask, np.int32)
+        s2x.call("s2x_text_encode", self.h, ids.ctypes.data, ids.size,
+                 None if m is None else m.ctypes.data, out.ctypes.data)
+        return out
+
+    def batch(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.shape[0], self.host.cfg.proj), np.float32)
+        s2x.call("s2x_text_encode_batch", self.h, ids.ctypes.data, ids.shape[1], ids.shape[0],
+                 out.ctypes.data)
+        return out
+
+    def close(self):
+        s2x.lib.s2x_text_destroy(self.h)
+
+
+def test_small_text_vs_oracle(orc):
+    hm = synth.text_model(SMALL_T, seed=22)
+    t = Text(hm)
+    try:
+        om = orc.text_model(hm)
+        ids, lens = synth.text_tokens(5, 64, vocab=SMALL_T.vocab)
+        b = t.batch(ids)
+        for i in range(5):
+            r = orc.text_encode(om, ids[i])
+            assert cos(b[i], r) >= 0.9999
+            assert np.array_equal(t.encode(ids[i]), b[i])
+        mask = np.zeros(64, np.int32)
+        mask[:lens[1]] = 1
+        c = cos(t.encode(ids[1], mask), orc.text_encode(om, ids[1], mask))
+        say(f"small text masked cosine {c:.7f}")
+        assert c >= 0.9999
+        short = ids[2, :17]
+        assert cos(t.encode(short), orc.text_encode(om, short)) >= 0.9999
+        bad = ids[0].copy()
+        bad[3] = SMALL_T.vocab
+        out = np.empty(SMALL_T.proj, np.float32)
+        assert s2x.lib.s2x_text_encode(t.h, bad.ctypes.data, 64, None, out.ctypes.data) == 1
+    finally:
+        t.close()
+
+
+# ---------------------------------------------------------------- so400m ----
+@pytest.fixture(scope="module")
+def so400m_vision(orc):
+    say("generating so400m vision weights")
+    hm = synth.vision_model(synth.SO400M_VISION, seed=0)
+    v = Vision(hm)
+    yield v, orc.vision_model(hm)
+    v.close()
+
+
+@pytest.mark.timeout(600)
+def test_so400m_vision_729_probe_vs_oracle(orc, so400m_vision):
+    v, om = so400m_vision
+    px = synth.pixels(1, 729, seed=1234)
+    g = v.encode(px, 27, 27, s2x.POOL_PROBE)
+    say("oracle so400m tower (CPU)")
+    r = orc.vision_encode(om, px, 27, 27, pooling=1)
+    c = cos(g, r)
+    say(f"so400m vision 27x27 probe: cosine {c:.7f}  max|diff| {np.abs(g - r).max():.3e}")
+    assert c >= 0.9999
+
+
+@pytest.mark.timeout(600)
+def test_so400m_vision_batch_and_ragged_invariance(so400m_vision):
+    v, _ = so400m_vision
+    px = synth.pixels(4, 729, seed=77)
+    b = v.batch(px, 4, 27, 27, s2x.POOL_PROBE)
+    for i in (0, 3):
+        one = v.batch(px[i * 729:(i + 1) * 729], 1, 27, 27, s2x.POOL_PROBE)
+        assert np.array_equal(b[i], one[0])
+    shapes = [(27, 27), (16, 16), (32, 32), (24, 24)]
+    padded = np.zeros((4, 1024, 768), np.float32)
+    singles = []
+    for i, (h, w) in enumerate(shapes):
+        p = synth.pixels(1, h * w, seed=300 + i)
+        padded[i, :h * w] = p
+        singles.append(v.batch(p, 1, h, w, s2x.POOL_PROBE)[0])
+    out = v.ragged(padded.reshape(-1, 768), shapes, 1024, s2x.POOL_PROBE)
+    for i in range(4):
+        assert np.array_equal(out[i], singles[i])
+
+
+@pytest.mark.timeout(600)
+def test_so400m_vision_naflex_vs_oracle(orc, so400m_vision):
+    v, om = so400m_vision
+    h, w = 16, 64
+    px = synth.pixels(1, h * w, seed=55)
+    g = v.encode(px, h, w, s2x.POOL_MEAN)
+    r = orc.vision_encode(om, px, h, w, pooling=0)
+    c = cos(g, r)
+    say(f"so400m vision 16x64 mean: cosine {c:.7f}")
+    assert c >= 0.9999
+
+
+@pytest.mark.timeout(600)
+def test_so400m_text_5x64_vs_oracle(orc):
+    say("generating so400m text weights")
+    hm = synth.text_model(synth.SO400M_TEXT, seed=0)
+    t = Text(hm)
+    try:
+        om = orc.text_model(hm)
+        ids, _ = synth.text_tokens(5, 64)
+        b = t.batch(ids)
+        for i in (0, 4):
+            r = orc.text_encode(om, ids[i])
+            c = cos(b[i], r)
+            say(f"so400m text prompt {i}: cosine {c:.7f}")
+            assert c >= 0.9999
+    finally:
+        t.close()

@@ -8,7 +8,7 @@ import torch
 
 import s2x
 from s2x import synth
-from gpu_util import cos, dev, empty, host, ptr, say, stream, zeros
+from gpu_util import assert_same, cos, dev, empty, host, ptr, say, stream, zeros
 
 pytestmark = pytest.mark.gpu
 
@@ -41,8 +41,8 @@ def test_quantize_q8_1_bit_exact(orc, M, K, K_pad):
         x[min(1, M - 1), 1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5]
     qs, ds = _quant_gpu(x, K_pad)
     rq, rd = orc.quantize_q8_1(x, K_pad)
-    assert np.array_equal(host(qs), rq)
-    assert np.array_equal(host(ds).view(np.uint16), rd)
+    assert_same(host(qs), rq, "qs")
+    assert_same(host(ds).view(np.uint16), rd, "ds")
 
 
 def test_quantize_strided_input(orc):
