@@ -335,6 +335,23 @@ int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
     return e == hipSuccess ? S2X_OK : hip_fail(e, "attn launch");
 }
 
+int s2x_attn_fp64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                  const int32_t *seg_start_dev, const int32_t *seg_len_dev,
+                  const uint8_t *key_valid, int64_t n_seg, int64_t max_len, int64_t n_head,
+                  int64_t d_head, float scale, float *out, int64_t ld_out, void *stream) {
+    if (n_seg < 0 || max_len <= 0 || n_head <= 0 || d_head <= 0 || d_head > 80)
+        return fail(S2X_ERR_INVALID_ARG, "attn_fp64: bad shape (d_head <= 80)");
+    if (n_seg == 0) return S2X_OK;
+    if (!qkv || !qkv_bias || !seg_start_dev || !seg_len_dev || !out)
+        return fail(S2X_ERR_INVALID_ARG, "attn_fp64: null pointer");
+    if (ld_qkv < 3 * n_head * d_head || ld_out < n_head * d_head)
+        return fail(S2X_ERR_INVALID_ARG, "attn_fp64: ld_qkv < 3H or ld_out < H");
+    hipError_t e = launch_attn_f64(qkv, ld_qkv, qkv_bias, seg_start_dev, seg_len_dev, key_valid,
+                                   n_seg, max_len, n_head, d_head, scale, out, ld_out,
+                                   (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "attn_fp64 launch");
+}
+
 // ---------------------------------------------------------------------------
 // a8 / a11
 // ---------------------------------------------------------------------------

@@ -121,6 +121,7 @@ constexpr int FA_KP = FA_DP + 8;       // K tile pitch (halves): conflict-free 1
 constexpr int FA_VP = FA_KT + 4;       // V^T tile pitch (halves): conflict-free 8-byte reads
 constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
 
+template <bool P_SPLIT>
 __global__ __launch_bounds__(256) void k_attn(
     const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
     const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
@@ -163,8 +164,10 @@ __global__ __launch_bounds__(256) void k_attn(
         const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            const int c = tid + i * 256;  // 640 chunks of 16 B
-            if (c < FA_KT * FA_DP / 8) kr[i] = ks[c];
+            // 640 chunks of 16 B; threads past the end re-load the last chunk
+            // (always in bounds) so kr[] stays in registers
+            const int c = min(tid + i * 256, FA_KT * FA_DP / 8 - 1);
+            kr[i] = ks[c];
         }
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
@@ -178,11 +181,11 @@ __global__ __launch_bounds__(256) void k_attn(
         _Float16 *vl = kl + FA_KT * FA_KP;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            const int c = tid + i * 256;
-            if (c < FA_KT * FA_DP / 8) {
-                const int r = c / 10, cc = (c % 10) * 8;
-                *reinterpret_cast<uint4 *>(kl + r * FA_KP + cc) = kr[i];
-            }
+            // same clamp as the load: past-the-end threads rewrite the last
+            // chunk with the value it already has
+            const int c = min(tid + i * 256, FA_KT * FA_DP / 8 - 1);
+            const int r = c / 10, cc = (c % 10) * 8;
+            *reinterpret_cast<uint4 *>(kl + r * FA_KP + cc) = kr[i];
         }
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
@@ -229,13 +232,21 @@ __global__ __launch_bounds__(256) void k_attn(
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
             m_run = m_new;
+            // P as f16 for the PV product; with P_SPLIT as an exact pair
+            // p = hi + lo (hi = f16(p), lo = f16(p - hi); p - hi is exact in
+            // f32), i.e. ~22 significant bits instead of 11.
             float ps = 0.0f;
-            v8h pf[2];
+            v8h ph0, ph1, pl0, pl1;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
                 ps = ps + p;
-                pf[r >> 3][r & 7] = (_Float16)p;
+                const _Float16 hi = f32_to_f16(p);
+                if (r < 8) ph0[r] = hi; else ph1[r - 8] = hi;
+                if (P_SPLIT) {
+                    const _Float16 lo = f32_to_f16(p - (float)hi);
+                    if (r < 8) pl0[r] = lo; else pl1[r - 8] = lo;
+                }
             }
             l_run = l_run * alpha + ps;
 #pragma unroll
@@ -251,7 +262,9 @@ __global__ __launch_bounds__(256) void k_attn(
                     const v4h lo = *reinterpret_cast<const v4h *>(vp);
                     const v4h hi = *reinterpret_cast<const v4h *>(vp + 8);
                     const v8h vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[hh], o[j], 0, 0, 0);
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? ph1 : ph0, o[j], 0, 0, 0);
+                    if (P_SPLIT)
+                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? pl1 : pl0, o[j], 0, 0, 0);
                 }
             }
         }
@@ -285,7 +298,8 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
     const float log2e = 1.4426950408889634f;
     const dim3 grid((unsigned)((L.max_len + 127) / 128), (unsigned)L.n_head, (unsigned)L.n_seg);
-    hipLaunchKernelGGL(k_attn, grid, dim3(256), 0, stream,
+    auto kern = L.p_split ? k_attn<true> : k_attn<false>;
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream,
                        reinterpret_cast<const _Float16 *>(base + L.q_off),
                        reinterpret_cast<const _Float16 *>(base + L.k_off),
                        reinterpret_cast<const _Float16 *>(base + L.vt_off), seg_start, seg_len,
@@ -295,8 +309,115 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
 }
 
 // ---------------------------------------------------------------------------
+// fp64 attention for short sequences (the text tower: 64 tokens).  Straight
+// from the QKV GEMM rows: q/k/v = f16(f32(mm + bias)) as the reference casts
+// them, then in double and in a fixed order -- score s_j = (sum_d q_d k_jd)
+// * scale, max over valid keys, p_j = exp(s_j - max), den = sum_j p_j,
+// acc_d = sum_j p_j v_jd (j ascending), out = f32(acc_d / den).  All but
+// exp() round identically on any IEEE machine summing in the same order.
+// One workgroup = one wave = 64 queries of one (segment, head); 64-key
+// tiles of K and V staged in LDS as floats holding the f16 values.
+// ---------------------------------------------------------------------------
+constexpr int A64_T = 64;
+constexpr int A64_DMAX = 80;
+
+__global__ __launch_bounds__(64) void k_attn_f64(
+    const float *__restrict__ qkv, int64_t ld, const float *__restrict__ bias,
+    const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len,
+    const uint8_t *__restrict__ key_valid, int n_head, int d_head, double scale,
+    float *__restrict__ out, int64_t ld_out) {
+    __shared__ float qs[A64_T][A64_DMAX + 1];
+    __shared__ float ks[A64_T][A64_DMAX];
+    __shared__ float vs[A64_T][A64_DMAX];
+    const int qb = blockIdx.x, h = blockIdx.y, sg = blockIdx.z;
+    const int len = seg_len[sg];
+    if (qb * A64_T >= len) return;
+    const int64_t row0 = seg_start[sg];
+    const int H = n_head * d_head;
+    const int lane = threadIdx.x;
+    const int q = qb * A64_T + lane;
+    auto f16r = [](float x) { return (float)f32_to_f16(x); };
+    for (int i = lane; i < A64_T * d_head; i += A64_T) {
+        const int p = i / d_head, d = i % d_head;
+        const int pos = qb * A64_T + p;
+        qs[p][d] = pos < len ? f16r(qkv[(row0 + pos) * ld + h * d_head + d] + bias[h * d_head + d]) : 0.0f;
+    }
+    const bool active = q < len;
+    const int n_tiles = (len + A64_T - 1) / A64_T;
+    auto load_kv = [&](int t) {
+        __syncthreads();
+        for (int i = lane; i < A64_T * d_head; i += A64_T) {
+            const int p = i / d_head, d = i % d_head;
+            const int pos = t * A64_T + p;
+            float k = 0.0f, v = 0.0f;
+            if (pos < len) {
+                const float *r = qkv + (row0 + pos) * ld + h * d_head + d;
+                k = f16r(r[H] + bias[H + h * d_head + d]);
+                v = f16r(r[2 * H] + bias[2 * H + h * d_head + d]);
+            }
+            ks[p][d] = k;
+            vs[p][d] = v;
+        }
+        __syncthreads();
+    };
+    auto score = [&](int j) {  // j local to the tile
+        double acc = 0.0;
+        for (int d = 0; d < d_head; ++d) acc = acc + (double)qs[lane][d] * (double)ks[j][d];
+        return acc * scale;
+    };
+    auto valid = [&](int key) {
+        return key < len && (key_valid == nullptr || key_valid[row0 + key] != 0);
+    };
+    // pass 1: max over valid keys
+    double mx = -INFINITY;
+    for (int t = 0; t < n_tiles; ++t) {
+        load_kv(t);
+        if (active)
+            for (int j = 0; j < A64_T; ++j)
+                if (valid(t * A64_T + j)) mx = fmax(mx, score(j));
+    }
+    // pass 2: exp, sum, PV
+    double acc[A64_DMAX];
+    for (int d = 0; d < A64_DMAX; ++d) acc[d] = 0.0;
+    double den = 0.0;
+    for (int t = 0; t < n_tiles; ++t) {
+        load_kv(t);
+        if (!active) continue;
+        for (int j = 0; j < A64_T; ++j) {
+            const int key = t * A64_T + j;
+            if (key >= len) break;
+            if (!valid(key)) continue;
+            const double p = exp(score(j) - mx);
+            den = den + p;
+#pragma unroll
+            for (int d = 0; d < A64_DMAX; ++d)
+                if (d < d_head) acc[d] = acc[d] + p * (double)vs[j][d];
+        }
+    }
+    if (active) {
+        float *orow = out + (row0 + q) * ld_out + h * d_head;
+#pragma unroll
+        for (int d = 0; d < A64_DMAX; ++d)
+            if (d < d_head) orow[d] = (float)(acc[d] / den);
+    }
+}
+
+hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                           const int32_t *seg_start, const int32_t *seg_len,
+                           const uint8_t *key_valid, int64_t n_seg, int64_t max_len,
+                           int64_t n_head, int64_t d_head, float scale, float *out,
+                           int64_t ld_out, hipStream_t stream) {
+    if (n_seg == 0) return hipSuccess;
+    if (d_head > A64_DMAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((max_len + A64_T - 1) / A64_T), (unsigned)n_head, (unsigned)n_seg);
+    hipLaunchKernelGGL(k_attn_f64, grid, dim3(A64_T), 0, stream, qkv, ld_qkv, qkv_bias, seg_start,
+                       seg_len, key_valid, (int)n_head, (int)d_head, (double)scale, out, ld_out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // single-query attention for the MAP probe head (src/siglip2_vision.cpp:
-// 249-295): the probe query against one segment's keys, K and V rounded to
+// 249-295): the probe query against one segment's keys, Q, K and V rounded to
 // f16 as the reference's FA inputs are.  One workgroup per (head, segment).
 // ---------------------------------------------------------------------------
 constexpr int A1_MAXLEN = (int)MAX_SEG_LEN;
@@ -317,7 +438,8 @@ __global__ __launch_bounds__(256) void k_attn_1q(
     for (int j = threadIdx.x; j < len; j += 256) {
         const float *kr = k + (row0 + j) * ld + h * d_head;
         float acc = 0.0f;
-        for (int d = 0; d < d_head; ++d) acc = fmaf(qh[d], (float)(_Float16)kr[d], acc);
+        for (int d = 0; d < d_head; ++d)
+            acc = fmaf((float)f32_to_f16(qh[d]), (float)f32_to_f16(kr[d]), acc);
         const float s = acc * scale;
         p[j] = s;
         mx = fmaxf(mx, s);

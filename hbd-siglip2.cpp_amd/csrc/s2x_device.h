@@ -61,6 +61,12 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 template <int W>
+__device__ __forceinline__ double group_dsum(double v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, W);
+    return v;
+}
+template <int W>
 __device__ __forceinline__ int group_isum(int v) {
 #pragma unroll
     for (int o = W / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, W);
@@ -82,12 +88,58 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
            ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
+// tanh in f32 from IEEE primitives only (mul, add, fma, divide, rint,
+// ldexp), so that it rounds identically on every IEEE machine:
+//   |u| < 0.5 : Maclaurin series of tanh through u^15 (coefficients are the
+//               exact series terms 2^2n (2^2n - 1) B_2n / (2n)!), Horner in
+//               z = u^2; truncation error < 1e-8 relative
+//   |u| < 9   : (e - 1) / (e + 1), e = e^(2|u|) by Cody-Waite reduction
+//               t = k ln2 + r (ln2 split into a 9-bit head and a tail) and
+//               the degree-7 Taylor polynomial of e^r, |r| <= ln2/2
+//   |u| >= 9  : +-1 (tanh(9) rounds to 1 in f32)
+// Accuracy: within 3 ulp of tanh.
+__device__ __forceinline__ float exp_cw(float t) {
+    const float k = __builtin_rintf(t * 1.44269504088896341f);
+    float r = fmaf(-k, 0.693359375f, t);
+    r = fmaf(-k, -2.12194440e-4f, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)k);
+}
+__device__ __forceinline__ float tanh_f32(float u) {
+    const float a = fabsf(u);
+    float r;
+    if (a >= 9.0f) {
+        r = 1.0f;
+    } else if (a < 0.5f) {
+        const float z = a * a;
+        float p = -929569.0f / 638512875.0f;
+        p = fmaf(p, z, 21844.0f / 6081075.0f);
+        p = fmaf(p, z, -1382.0f / 155925.0f);
+        p = fmaf(p, z, 62.0f / 2835.0f);
+        p = fmaf(p, z, -17.0f / 315.0f);
+        p = fmaf(p, z, 2.0f / 15.0f);
+        p = fmaf(p, z, -1.0f / 3.0f);
+        r = fmaf(a * z, p, a);
+    } else {
+        const float e = exp_cw(2.0f * a);
+        r = (e - 1.0f) / (e + 1.0f);
+    }
+    return __builtin_copysignf(r, u);
+}
+
 // GELU tanh form, same expression and operation order as the reference's
-// fused epilogue (src/cuda/siglip2_megakernel.cu:276-280).
+// fused epilogue (src/cuda/siglip2_megakernel.cu:276-280), with tanh_f32.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
-    return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+    return 0.5f * x * (1.0f + tanh_f32(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
 }
 
 }  // namespace s2x

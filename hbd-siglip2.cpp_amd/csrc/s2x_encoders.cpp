@@ -185,6 +185,8 @@ struct Tower {
     hipStream_t own = nullptr, stream = nullptr;
     DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid;
     GemmTiming timing;
+    // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
+    bool attn_f64 = false;
 
     ~Tower() {
         for (auto &L : layers) L.release();
@@ -290,12 +292,20 @@ struct Tower {
         for (auto &L : layers) {
             S2X_TRY(layernorm_q(xp, M, L.ln1_w, L.ln1_b, nullptr));
             S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
-            hipError_t e = launch_attn_prep(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(),
-                                            seg_len(n_seg), AL, attn_ws.p, stream);
-            if (e != hipSuccess) return hip_fail(e, "attn_prep launch");
-            e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
-                            att.as<float>(), H, stream);
-            if (e != hipSuccess) return hip_fail(e, "attn launch");
+            hipError_t e;
+            if (attn_f64) {
+                e = launch_attn_f64(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
+                                    key_valid, n_seg, max_len, n_head, d_head, kq_scale,
+                                    att.as<float>(), H, stream);
+                if (e != hipSuccess) return hip_fail(e, "attn_f64 launch");
+            } else {
+                e = launch_attn_prep(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
+                                     AL, attn_ws.p, stream);
+                if (e != hipSuccess) return hip_fail(e, "attn_prep launch");
+                e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
+                                att.as<float>(), H, stream);
+                if (e != hipSuccess) return hip_fail(e, "attn launch");
+            }
             S2X_TRY(quantize(att.as<float>(), H, M, H, H));
             S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
             S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
@@ -513,6 +523,12 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream) {
     return S2X_OK;
 }
 
+int s2x_vision_set_attention_fp64(s2x_vision *v, int enable) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    v->t.attn_f64 = enable != 0;
+    return S2X_OK;
+}
+
 int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t n_img, int32_t n_h,
                                 int32_t n_w, int32_t pooling, float *out_dev) {
     if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
@@ -695,6 +711,7 @@ int s2x_text_create(const s2x_text_weights *w, s2x_text **out) {
     x->vocab = w->vocab;
     x->max_pos = w->max_pos;
     x->proj = w->proj;
+    t.attn_f64 = true;  // 64-token prompts: fp64 attention costs little
     auto bail = [&](int st) {
         delete x;
         return st;
@@ -726,6 +743,12 @@ void s2x_text_destroy(s2x_text *x) {
 int s2x_text_set_stream(s2x_text *x, void *stream) {
     if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
     x->t.stream = stream ? (hipStream_t)stream : x->t.own;
+    return S2X_OK;
+}
+
+int s2x_text_set_attention_fp64(s2x_text *x, int enable) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    x->t.attn_f64 = enable != 0;
     return S2X_OK;
 }
 

@@ -65,6 +65,9 @@ struct AttnLayout {
     int64_t dv_pad;    // d_head rounded up to 32 (V^T rows)
     int64_t len_pad;   // max_len rounded up to 128 (query tile)
     size_t q_off, k_off, vt_off, bytes;
+    // softmax probabilities enter the PV product as an exact f16 pair
+    // (hi + lo, ~22 bits) instead of one f16 (11 bits)
+    bool p_split = true;
 };
 AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head);
 hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
@@ -73,6 +76,13 @@ hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_b
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
                        const uint8_t *key_valid, const AttnLayout &L, float scale,
                        float *out, int64_t ld_out, hipStream_t stream);
+// fp64 attention straight from the QKV GEMM rows (+bias), fixed summation
+// order; for short sequences (the text tower).
+hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                           const int32_t *seg_start, const int32_t *seg_len,
+                           const uint8_t *key_valid, int64_t n_seg, int64_t max_len,
+                           int64_t n_head, int64_t d_head, float scale, float *out,
+                           int64_t ld_out, hipStream_t stream);
 // Single-query attention (MAP probe head): q [H] shared by all segments,
 // k/v packed rows (ld floats), out [n_seg][H].
 hipError_t launch_attn_1q(const float *q, const float *k, const float *v, int64_t ld,

@@ -92,7 +92,7 @@ hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t 
 
 // ---------------------------------------------------------------------------
 // a4: LayerNorm(+affine)(+Q8_1).  One wave per row, the row held in
-// registers: a two-pass mean / variance from wave butterflies, then
+// registers: a two-pass mean / variance (double sums) from wave butterflies, then
 // y = ((x - mean) * scale) * w + b rounded after each operation
 // (src/siglip2_vision.cpp:79-88 graph; ggml_norm's two-pass variance), then
 // the 32-blocks of y quantized by 8-lane groups exactly as k_quantize_q8_1.
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
     if (row >= M) return;
     const float *xr = x + row * ldx;
     float v[LN_MAXIT][4];
-    float s = 0.0f;
+    double s = 0.0;
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
@@ -122,14 +122,17 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[it][j] = xr[c + j];
             }
-            s = s + ((v[it][0] + v[it][1]) + (v[it][2] + v[it][3]));
+            s = s + (((double)v[it][0] + (double)v[it][1]) + ((double)v[it][2] + (double)v[it][3]));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
         }
     }
-    const float mean = group_sum<64>(s) / (float)H;
-    float s2 = 0.0f;
+    // sums in double, as ggml's CPU norm accumulates: the f32 mean and
+    // variance then equal the CPU's (the double sum's rounding, whatever
+    // its order, is ~1e-16 relative and vanishes in the f32 conversion)
+    const float mean = (float)(group_dsum<64>(s) / (double)H);
+    double s2 = 0.0;
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
@@ -137,11 +140,11 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float t = v[it][j] - mean;
-                s2 = s2 + t * t;
+                s2 = s2 + (double)(t * t);
             }
         }
     }
-    const float var = group_sum<64>(s2) / (float)H;
+    const float var = (float)(group_dsum<64>(s2) / (double)H);
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {

@@ -104,11 +104,14 @@ _sig("s2x_bias_gelu", [_p, _p, _p, _i64, _i64, _p])
 _sig("s2x_attn_workspace_size", [_i64, _i64, _i64, _i64], _sz)
 _sig("s2x_attn_prep", [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p])
 _sig("s2x_attn_run", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])
+_sig("s2x_attn_fp64", [_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])
 _sig("s2x_resize_pos_embed", [_p, _i64, _i64, _i64, _i64, _p, _p])
 _sig("s2x_get_rows_q8_0", [_p, _i64, _i64, _p, _i64, _p, _i64, _p, _p])
 _sig("s2x_vision_create", [ctypes.POINTER(VisionWeights), ctypes.POINTER(_p)])
 _sig("s2x_vision_destroy", [_p], None)
 _sig("s2x_vision_set_stream", [_p, _p])
+_sig("s2x_vision_set_attention_fp64", [_p, ctypes.c_int])
+_sig("s2x_text_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_vision_encode", [_p, _p, _i32, _i32, _i32, _p])
 _sig("s2x_vision_encode_batch_dev", [_p, _p, _i32, _i32, _i32, _i32, _p])
 _sig("s2x_vision_encode_ragged_dev", [_p, _p, _p, _i32, _i32, _i32, _p])

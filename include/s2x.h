@@ -176,6 +176,16 @@ int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
                  int64_t d_head, float scale, float *out, int64_t ld_out,
                  void *stream);
 
+/* fp64 attention straight from the QKV rows (bias added in f32, Q/K/V
+ * rounded to f16 as the reference casts them, then scores, softmax and PV in
+ * double in a fixed key order).  Needs no staging workspace; meant for short
+ * sequences such as the 64-token text prompts.  d_head <= 80. */
+int s2x_attn_fp64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
+                  const int32_t *seg_start_dev, const int32_t *seg_len_dev,
+                  const uint8_t *key_valid, int64_t n_seg, int64_t max_len,
+                  int64_t n_head, int64_t d_head, float scale, float *out,
+                  int64_t ld_out, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* a8  position-embedding resize (replaces ggml_interpolate(BILINEAR |       */
 /* ANTIALIAS) at src/siglip2_vision.cpp:680-690): anti-aliased bilinear,     */
@@ -247,6 +257,9 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out);
 void s2x_vision_destroy(s2x_vision *v);
 /* Run on the encoder's stream (NULL) or a caller stream. */
 int s2x_vision_set_stream(s2x_vision *v, void *stream);
+/* Attention precision: 0 (default) = f16-MFMA flash attention with f32
+ * softmax and an exact f16 hi/lo split of P; 1 = s2x_attn_fp64. */
+int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
 
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */
@@ -283,6 +296,9 @@ int s2x_vision_gemm_stats(s2x_vision *v, double *ms, double *ops,
 int s2x_text_create(const s2x_text_weights *w, s2x_text **out);
 void s2x_text_destroy(s2x_text *t);
 int s2x_text_set_stream(s2x_text *t, void *stream);
+/* Attention precision for the text tower: 1 (default) = s2x_attn_fp64,
+ * 0 = the f16-MFMA flash kernel. */
+int s2x_text_set_attention_fp64(s2x_text *t, int enable);
 /* TextEncoder::encode: one prompt of n_tok ids (host), optional host mask
  * (1 = valid), out_host proj floats.  Synchronous. */
 int s2x_text_encode(s2x_text *t, const int32_t *ids_host, int32_t n_tok,

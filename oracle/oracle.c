@@ -284,10 +284,49 @@ void orc_layernorm(const float *x, int64_t M, int64_t H, int64_t ldx,
     }
 }
 
+/* tanh from IEEE f32 primitives only (see oracle.h), so that the CPU and
+ * any other IEEE machine running the same operations agree bit for bit. */
+static float exp_cw(float t) {
+    const float k = rintf(t * 1.44269504088896341f);
+    float r = fmaf(-k, 0.693359375f, t);
+    r = fmaf(-k, -2.12194440e-4f, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)k);
+}
+
+float orc_tanh_f32(float u) {
+    const float a = fabsf(u);
+    float r;
+    if (a >= 9.0f) {
+        r = 1.0f;
+    } else if (a < 0.5f) {
+        const float z = a * a;
+        float p = -929569.0f / 638512875.0f;
+        p = fmaf(p, z, 21844.0f / 6081075.0f);
+        p = fmaf(p, z, -1382.0f / 155925.0f);
+        p = fmaf(p, z, 62.0f / 2835.0f);
+        p = fmaf(p, z, -17.0f / 315.0f);
+        p = fmaf(p, z, 2.0f / 15.0f);
+        p = fmaf(p, z, -1.0f / 3.0f);
+        r = fmaf(a * z, p, a);
+    } else {
+        const float e = exp_cw(2.0f * a);
+        r = (e - 1.0f) / (e + 1.0f);
+    }
+    return copysignf(r, u);
+}
+
 float orc_gelu(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
-    return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+    return 0.5f * x * (1.0f + orc_tanh_f32(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
 }
 
 /* ------------------------------------------------------------------------ */
@@ -310,7 +349,10 @@ void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
     for (int64_t h = 0; h < n_head; ++h) {
         for (int64_t i = 0; i < n_pos; ++i) {
             double *s = (double *)malloc(sizeof(double) * (size_t)n_pos);
-            const float *q = qkv + i * 3 * H + h * d_head;
+            /* Q enters flash attention as fp16, as ggml's FA converts it to the
+             * K vec-dot type [ggml, not in tree] */
+            float q[512];
+            for (int64_t d = 0; d < d_head && d < 512; ++d) q[d] = fp16r(qkv[i * 3 * H + h * d_head + d]);
             double mx = -INFINITY;
             for (int64_t j = 0; j < n_pos; ++j) {
                 if (key_valid && !key_valid[j]) { s[j] = -INFINITY; continue; }
@@ -496,8 +538,8 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
         linear(m->hq_w, m->hq_b, H, H, H, m->probe, H, 1, q, nthreads);
         linear(m->hk_w, m->hk_b, H, H, H, x, H, n_pos, k, nthreads);
         linear(m->hv_w, m->hv_b, H, H, H, x, H, n_pos, v, nthreads);
-        /* single-query attention over the n_pos keys; K, V rounded to fp16
-         * as the reference casts them before FA */
+        /* single-query attention over the n_pos keys; Q, K, V rounded to
+         * fp16 as they enter flash attention (see orc_attention) */
         {
             const int64_t nh = m->n_head;
             for (int64_t h = 0; h < nh; ++h) {
@@ -506,7 +548,8 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
                 for (int64_t j = 0; j < n_pos; ++j) {
                     double acc = 0.0;
                     for (int64_t d = 0; d < d_head; ++d)
-                        acc += (double)q[h * d_head + d] * (double)fp16r(k[j * H + h * d_head + d]);
+                        acc += (double)fp16r(q[h * d_head + d]) *
+                               (double)fp16r(k[j * H + h * d_head + d]);
                     s[j] = acc * (double)kq_scale;
                     if (s[j] > mx) mx = s[j];
                 }

@@ -100,7 +100,17 @@ void orc_layernorm(const float *x, int64_t M, int64_t H, int64_t ldx,
                    const float *w, const float *b, float eps, float *y,
                    int64_t ldy);
 
-/* GELU tanh form, src/cuda/siglip2_megakernel.cu:276-280. */
+/* tanh in f32 from IEEE primitives only (mul, add, fma, divide, rint,
+ * ldexp): |u| < 0.5 Maclaurin series through u^15 (exact series
+ * coefficients), |u| < 9 (e - 1)/(e + 1) with e = e^(2|u|) by Cody-Waite
+ * reduction and a degree-7 Taylor polynomial, else +-1.  Any IEEE machine
+ * running these operations in this order gets the same bits. */
+float orc_tanh_f32(float u);
+
+/* GELU tanh form, src/cuda/siglip2_megakernel.cu:276-280 (expression and
+ * operation order), with orc_tanh_f32 for tanh.  ggml's CPU path instead
+ * looks GELU up in an fp16 table [ggml, not in tree]; this restatement keeps
+ * the f32 formula the reference's CUDA epilogue uses. */
 float orc_gelu(float x);
 
 /* ---- attention ------------------------------------------------------------ */
@@ -108,7 +118,10 @@ float orc_gelu(float x);
  * qkv: n_pos rows of 3*H floats laid out [q | k | v], head h at h*d_head
  * (src/siglip2_vision.cpp:201-206).  K and V are rounded to fp16 first, as
  * the reference casts them before flash attention (src/siglip2_vision.cpp:
- * 164-167); Q stays f32.  Scores, softmax and PV run in double.
+ * 164-167); Q is rounded to fp16 as ggml's flash attention converts it to
+ * the K vec-dot type [ggml, not in tree].  Scores, softmax and PV then run
+ * in double (ggml's CPU kernel accumulates V*p in fp16; this restatement
+ * keeps that sum exact instead).
  * key_valid: NULL (all valid) or n_pos flags; invalid keys get weight 0.
  * out: n_pos rows of H floats, head-major within the row. */
 void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,

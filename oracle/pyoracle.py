@@ -63,6 +63,7 @@ def lib():
             "orc_mul_mat_q8_0_f32": ([_p, _i64, _i64, _p, _i64, _i64, _i64, _p, ctypes.c_int], None),
             "orc_layernorm": ([_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64], None),
             "orc_gelu": ([_f32], _f32),
+            "orc_tanh_f32": ([_f32], _f32),
             "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
             "orc_resize_pos_embed": ([_p, _i64, _i64, _i64, _i64, _p], None),
             "orc_vision_encode": ([ctypes.POINTER(OrcVision), _p, _i32, _i32, _i32, _p, _p,
@@ -156,6 +157,12 @@ def layernorm(x, w, b, eps=1e-6):
 
 def gelu(x):
     f = lib().orc_gelu
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.float32).reshape(np.shape(x))
+
+
+def tanh_f32(x):
+    f = lib().orc_tanh_f32
     return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
                     np.float32).reshape(np.shape(x))
 

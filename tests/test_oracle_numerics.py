@@ -220,6 +220,17 @@ def test_layernorm_constant_row(orc):
     assert np.array_equal(y, np.full((2, 64), 0.5, np.float32))
 
 
+def test_tanh_f32_accuracy(orc):
+    x = np.concatenate([np.linspace(-12, 12, 120001), np.logspace(-10, 1.2, 20001),
+                        -np.logspace(-10, 1.2, 20001), [0.0, 0.5, -0.5, 9.0, -9.0]]).astype(np.float32)
+    t = orc.tanh_f32(x)
+    ref = np.tanh(x.astype(np.float64))
+    ulp = np.abs(t - ref) / np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 3.0
+    assert np.array_equal(orc.tanh_f32(-x), -t)  # odd
+    assert orc.tanh_f32(np.float32(0.0)) == 0.0
+
+
 def test_gelu_closed_form(orc):
     x = np.linspace(-12, 12, 4001).astype(np.float32)
     g = orc.gelu(x)
@@ -234,7 +245,7 @@ def test_gelu_closed_form(orc):
 # ------------------------------------------------------------ attention --
 def _attn_ref(qkv, n_head, dh, scale, valid=None):
     H = n_head * dh
-    q = qkv[:, :H].astype(np.float64)
+    q = qkv[:, :H].astype(np.float16).astype(np.float64)
     k = qkv[:, H:2 * H].astype(np.float16).astype(np.float64)
     v = qkv[:, 2 * H:].astype(np.float16).astype(np.float64)
     out = np.zeros((qkv.shape[0], H))
