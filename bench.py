@@ -24,6 +24,11 @@ sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
+KERNELS = {
+    "f16": "k_mmq_f16 (Q8_0 x Q8_1 GEMM: exact int8-valued block dots and the dx*dw scale "
+           "tile on v_mfma_f32_32x32x16_f16; priced against the int8 peak)",
+    "i8": "k_mmq (Q8_0 x Q8_1 GEMM: v_mfma_i32_32x32x32_i8 block dots, VALU rescale)",
+}
 
 
 def log(*a):
@@ -38,6 +43,9 @@ def main():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--cpu-images", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemm", choices=["f16", "i8"], default="f16",
+                    help="GEMM kernel: f16-MFMA block dots + scale tile (default) or "
+                         "int8-MFMA block dots with VALU rescale; same bits")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (the tower "
@@ -58,6 +66,8 @@ def main():
     hm = synth.vision_model(cfg, seed=0)
     v = ctypes.c_void_p()
     s2x.call("s2x_vision_create", ctypes.byref(hm.struct), ctypes.byref(v))
+    s2x.call("s2x_vision_set_gemm_variant", v,
+             s2x.GEMM_F16_MFMA if args.gemm == "f16" else s2x.GEMM_I8_MFMA)
     stream = torch.cuda.ExternalStream  # noqa: F841 (the encoder owns its stream)
     px = synth.pixels(B, n_pos, seed=1234)
     pd = torch.from_numpy(px).to("cuda:0")
@@ -139,7 +149,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "kernel": "k_mmq (Q8_0 x Q8_1 int8 MFMA GEMM)",
+                     "kernel": KERNELS[args.gemm],
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "launches": int(launches.value)},
         "cpu_baseline": cpu,

@@ -47,7 +47,10 @@ def _compile(src, asm=False):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     cmd = [HIPCC, *COMMON]
     if src.endswith(".hip"):
-        cmd += ["-x", "hip"]
+        # MFMA results straight into VGPRs: the GEMM and attention kernels
+        # post-process every MFMA tile on the VALU, and the default AGPR
+        # destinations cost one v_accvgpr_read per element before each use
+        cmd += ["-x", "hip", "-mllvm", "-amdgpu-mfma-vgpr-form"]
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]
     if asm and src.endswith(".hip"):
         cmd += ["-save-temps=obj"]

@@ -68,8 +68,8 @@ int s2x_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx, int64_t
     if (!x || !qs || !ds) return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: null pointer");
     if (!aligned(qs, 4) || !aligned(ds, 4) || !aligned(x, 4))
         return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: qs/ds/x must be 4-byte aligned");
-    hipError_t e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)qs, (uint32_t *)ds,
-                                        (hipStream_t)stream);
+    hipError_t e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)qs, nullptr,
+                                        (uint32_t *)ds, (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize_q8_1 launch");
 }
 
@@ -95,8 +95,7 @@ int s2x_weight_create_in(const void *raw_dev, int64_t K_pad, int64_t N, void *de
     w->mem = dev_buf;
     w->owns = false;
     w->view = planes_view(dev_buf, K_pad, N);
-    hipError_t e = launch_repack_q8_0(raw_dev, K_pad, N, const_cast<int8_t *>(w->view.qs),
-                                      const_cast<float *>(w->view.d), (hipStream_t)stream);
+    hipError_t e = repack_into(raw_dev, w->view, (hipStream_t)stream);
     if (e != hipSuccess) {
         delete w;
         return hip_fail(e, "repack launch");
@@ -200,15 +199,14 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
     uint8_t *ws = (uint8_t *)workspace;
     hipStream_t s = (hipStream_t)stream;
     const WeightView wv = planes_view(ws + L.w_off, K_pad, N);
-    hipError_t e = launch_repack_q8_0(w_raw, K_pad, N, const_cast<int8_t *>(wv.qs),
-                                      const_cast<float *>(wv.d), s);
+    hipError_t e = repack_into(w_raw, wv, s);
     if (e != hipSuccess) return hip_fail(e, "repack launch");
-    e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)(ws + L.qs_off),
+    e = launch_quantize_q8_1(x, K, M, ldx, K_pad, nullptr, (_Float16 *)(ws + L.qh_off),
                              (uint32_t *)(ws + L.ds_off), s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
-    e = launch_mmq(wv, (const int8_t *)(ws + L.qs_off), (const uint32_t *)(ws + L.ds_off), M, y, N,
-                   p, s);
+    e = launch_mmq_f16(wv, (const _Float16 *)(ws + L.qh_off), (const uint32_t *)(ws + L.ds_off), M,
+                       y, N, p, s);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
 }
 
@@ -243,7 +241,7 @@ int s2x_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx, const float
     if (st != S2X_OK) return st;
     if (M == 0) return S2X_OK;
     if (!y || ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm: y null or ldy < H");
-    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, nullptr, nullptr, y, ldy,
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, nullptr, nullptr, nullptr, y, ldy,
                                     (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
 }
@@ -257,7 +255,7 @@ int s2x_layernorm_quantize_q8_1(const float *x, int64_t H, int64_t M, int64_t ld
     if (!qs || !ds || !aligned(qs, 4) || !aligned(ds, 4))
         return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: qs/ds null or misaligned");
     if (y && ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: ldy < H");
-    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, (int8_t *)qs, (uint32_t *)ds, y, ldy,
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, (int8_t *)qs, nullptr, (uint32_t *)ds, y, ldy,
                                     (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm_quantize launch");
 }

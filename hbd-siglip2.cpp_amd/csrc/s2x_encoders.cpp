@@ -61,8 +61,7 @@ int weight_upload(const void *raw, bool is_host, int64_t K_pad, int64_t N, hipSt
     w->mem = planes;
     w->owns = true;
     w->view = planes_view(planes, K_pad, N);
-    hipError_t e = launch_repack_q8_0(src, K_pad, N, const_cast<int8_t *>(w->view.qs),
-                                      const_cast<float *>(w->view.d), stream);
+    hipError_t e = repack_into(src, w->view, stream);
     if (e == hipSuccess && tmp) e = hipStreamSynchronize(stream);
     if (tmp) (void)hipFree(tmp);
     if (e != hipSuccess) {
@@ -187,6 +186,9 @@ struct Tower {
     GemmTiming timing;
     // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
     bool attn_f64 = false;
+    // GEMM variant: f16-coded operands on f16 MFMA (true) or int8 MFMA; the
+    // quantized activations in `qs` are f16 or int8 accordingly
+    bool gemm_f16 = true;
 
     ~Tower() {
         for (auto &L : layers) L.release();
@@ -230,8 +232,10 @@ struct Tower {
             b = timing.get();
             S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        hipError_t err = launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y, ldy, e,
-                                    stream);
+        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, qs.as<_Float16>(), ds.as<uint32_t>(),
+                                                   M, y, ldy, e, stream)
+                                  : launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y,
+                                               ldy, e, stream);
         if (err != hipSuccess) return hip_fail(err, "mmq launch");
         if (timing.on) {
             S2X_HIP_TRY(hipEventRecord(b, stream));
@@ -240,14 +244,17 @@ struct Tower {
         return S2X_OK;
     }
 
+    int8_t *q_i8() { return gemm_f16 ? nullptr : qs.as<int8_t>(); }
+    _Float16 *q_f16() { return gemm_f16 ? qs.as<_Float16>() : nullptr; }
+
     int quantize(const float *src, int64_t K, int64_t M, int64_t ldx, int64_t K_pad) {
-        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, qs.as<int8_t>(),
+        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, q_i8(), q_f16(),
                                             ds.as<uint32_t>(), stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize launch");
     }
 
     int layernorm_q(const float *src, int64_t M, const float *w, const float *b, float *y) {
-        hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, qs.as<int8_t>(),
+        hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, q_i8(), q_f16(),
                                         ds.as<uint32_t>(), y, H, stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
     }
@@ -255,7 +262,7 @@ struct Tower {
     int reserve(int64_t M, int64_t n_seg, int64_t max_len) {
         const int64_t kmax = F_pad > H ? F_pad : H;
         S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
-        S2X_TRY(ensure(qs, (size_t)(M * kmax), stream));
+        S2X_TRY(ensure(qs, 2 * (size_t)(M * kmax), stream));  // f16 or int8 quants
         S2X_TRY(ensure(ds, sizeof(uint32_t) * (size_t)(M * (kmax / QK_)), stream));
         S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
@@ -396,7 +403,8 @@ struct s2x_vision {
         if (pooling == S2X_POOL_MEAN) {
             S2X_TRY(ensure(hid, sizeof(float) * (size_t)(M * H), t.stream));
             hipError_t e = launch_layernorm(t.x.as<float>(), H, M, H, post_ln_w, post_ln_b, t.eps,
-                                            nullptr, nullptr, hid.as<float>(), H, t.stream);
+                                            nullptr, nullptr, nullptr, hid.as<float>(), H,
+                                            t.stream);
             if (e != hipSuccess) return hip_fail(e, "post-LN launch");
             e = launch_mean_pool(hid.as<float>(), H, t.seg_start(), t.seg_len(n_img), n_img,
                                  out_dev, t.stream);
@@ -496,7 +504,7 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
         }
         if (hipMalloc(reinterpret_cast<void **>(&v->probe_q), sizeof(float) * (size_t)H) != hipSuccess)
             st = fail(S2X_ERR_OOM, "probe_q alloc");
-        if (!st) st = ensure(t.qs, (size_t)H, s);
+        if (!st) st = ensure(t.qs, 2 * (size_t)H, s);
         if (!st) st = ensure(t.ds, (size_t)(H / QK_) * 4, s);
         if (!st) st = t.quantize(probe, H, 1, H, H);
         if (!st) st = t.gemm(hq, 1, v->probe_q, H, EpiParams{EPI_BIAS, hq_b, nullptr, 0, 0, 0}, H);
@@ -526,6 +534,15 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream) {
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable) {
     if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
     v->t.attn_f64 = enable != 0;
+    return S2X_OK;
+}
+
+int s2x_vision_set_gemm_variant(s2x_vision *v, int variant) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (variant != S2X_GEMM_F16_MFMA && variant != S2X_GEMM_I8_MFMA)
+        return fail(S2X_ERR_INVALID_ARG, "gemm variant %d unknown", variant);
+    S2X_HIP_TRY(hipStreamSynchronize(v->t.stream));  // the activation buffer changes format
+    v->t.gemm_f16 = variant == S2X_GEMM_F16_MFMA;
     return S2X_OK;
 }
 
@@ -662,7 +679,7 @@ struct s2x_text {
         if (e != hipSuccess) return hip_fail(e, "get_rows launch");
         S2X_TRY(t.run_layers(M, n_batch, n_tok, key_valid_dev));
         e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr, nullptr,
-                             t.x.as<float>(), H, t.stream);
+                             nullptr, t.x.as<float>(), H, t.stream);
         if (e != hipSuccess) return hip_fail(e, "final LN launch");
         S2X_TRY(ensure(rows, sizeof(int32_t) * (size_t)n_batch, t.stream));
         S2X_TRY(ensure(pooled, sizeof(float) * (size_t)(n_batch * H), t.stream));

@@ -15,9 +15,20 @@ namespace s2x {
 // a1: quantizer.  Semantics: src/cuda/siglip2_custom_mmq.cu:63-76 (d, inv,
 // round-half-even, clamp) plus the Q8_1 sum s = fp16(sum(q) * d).
 // ---------------------------------------------------------------------------
+// Store the four quants of a lane: as int8 (4 bytes) and/or as f16 (8 bytes,
+// exact: |q| <= 128).
+__device__ __forceinline__ void store_q4(int8_t *qs, _Float16 *qh, int64_t off, int q0, int q1,
+                                         int q2, int q3) {
+    if (qs) *reinterpret_cast<uint32_t *>(qs + off) = pack4_i8(q0, q1, q2, q3);
+    if (qh) {
+        const v4h h = {(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};
+        *reinterpret_cast<v4h *>(qh + off) = h;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_quantize_q8_1(
     const float *__restrict__ x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
-    int8_t *__restrict__ qs, uint32_t *__restrict__ ds, int vec4) {
+    int8_t *__restrict__ qs, _Float16 *__restrict__ qh, uint32_t *__restrict__ ds, int vec4) {
     const int64_t KB = K_pad / QK;
     const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
     const int sub = threadIdx.x & 7;
@@ -42,7 +53,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;
     const int q0 = q8_round(v0, inv), q1 = q8_round(v1, inv);
     const int q2 = q8_round(v2, inv), q3 = q8_round(v3, inv);
-    *reinterpret_cast<uint32_t *>(qs + m * K_pad + c) = pack4_i8(q0, q1, q2, q3);
+    store_q4(qs, qh, m * K_pad + c, q0, q1, q2, q3);
     const int s = group_isum<8>(q0 + q1 + q2 + q3);
     if (sub == 0) {
         ds[g] = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
@@ -50,7 +61,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
 }
 
 hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
-                                int64_t K_pad, int8_t *qs, uint32_t *ds,
+                                int64_t K_pad, int8_t *qs, _Float16 *qh, uint32_t *ds,
                                 hipStream_t stream) {
     const int64_t groups = M * (K_pad / QK);
     if (groups == 0) return hipSuccess;
@@ -58,35 +69,50 @@ hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ld
     const int64_t threads = groups * 8;
     const unsigned grid = (unsigned)((threads + 255) / 256);
     hipLaunchKernelGGL(k_quantize_q8_1, dim3(grid), dim3(256), 0, stream, x, K, M, ldx,
-                       K_pad, qs, ds, vec4);
+                       K_pad, qs, qh, ds, vec4);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // a2: weight repack.  One thread per 34-byte block: the int8 qs go to a
-// 16-byte aligned row-major plane, d widens (exactly) to f32.
+// 16-byte aligned row-major plane, d widens (exactly) to f32; optionally the
+// same quants as f16 (exact) and d's fp16 bits for the f16-MFMA GEMM.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__ raw,
                                                      int64_t n_blocks, int8_t *__restrict__ qs,
-                                                     float *__restrict__ d) {
+                                                     float *__restrict__ d,
+                                                     _Float16 *__restrict__ qh,
+                                                     uint16_t *__restrict__ dh) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_blocks) return;
     const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + i * 34);  // 2-byte aligned
     d[i] = f16_bits_to_f32(src[0]);
+    if (dh) dh[i] = src[0];
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = (uint32_t)src[1 + 2 * j] | ((uint32_t)src[2 + 2 * j] << 16);
     uint4 *dst = reinterpret_cast<uint4 *>(qs + i * QK);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    if (qh) {
+        v8h *hd = reinterpret_cast<v8h *>(qh + i * QK);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v8h h;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                h[j] = (_Float16)(int8_t)((w[(c * 8 + j) >> 2] >> (8 * ((c * 8 + j) & 3))) & 0xff);
+            hd[c] = h;
+        }
+    }
 }
 
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
-                              float *d, hipStream_t stream) {
+                              float *d, _Float16 *qh, uint16_t *dh, hipStream_t stream) {
     const int64_t nb = N * (K_pad / QK);
     if (nb == 0) return hipSuccess;
     hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
-                       stream, reinterpret_cast<const uint8_t *>(raw), nb, qs, d);
+                       stream, reinterpret_cast<const uint8_t *>(raw), nb, qs, d, qh, dh);
     return hipGetLastError();
 }
 
@@ -103,8 +129,8 @@ template <bool QUANT, bool WRITE_Y>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
     const float *__restrict__ w, const float *__restrict__ b, float eps,
-    int8_t *__restrict__ qs, uint32_t *__restrict__ ds, float *__restrict__ y,
-    int64_t ldy, int vec4) {
+    int8_t *__restrict__ qs, _Float16 *__restrict__ qh, uint32_t *__restrict__ ds,
+    float *__restrict__ y, int64_t ldy, int vec4) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
@@ -174,7 +200,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
             const float inv = a != 0.0f ? 127.0f / a : 0.0f;
             const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
             const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
-            *reinterpret_cast<uint32_t *>(qs + row * H + c) = pack4_i8(q0, q1, q2, q3);
+            store_q4(qs, qh, row * H + c, q0, q1, q2, q3);
             const int sq = group_isum<8>(q0 + q1 + q2 + q3);
             if ((lane & 7) == 0) {
                 ds[row * (H / QK) + c / QK] = (uint32_t)f32_to_f16_bits(d) |
@@ -186,22 +212,23 @@ __global__ __launch_bounds__(256) void k_layernorm(
 
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
                             const float *w, const float *b, float eps, int8_t *qs,
-                            uint32_t *ds, float *y, int64_t ldy, hipStream_t stream) {
+                            _Float16 *qh, uint32_t *ds, float *y, int64_t ldy,
+                            hipStream_t stream) {
     if (M == 0) return hipSuccess;
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
     const dim3 grid((unsigned)((M + 3) / 4));
-    const bool quant = qs != nullptr;
+    const bool quant = qs != nullptr || qh != nullptr;
     const bool wy = y != nullptr;
     if (quant && wy)
         hipLaunchKernelGGL((k_layernorm<true, true>), grid, dim3(256), 0, stream, x, H, M, ldx,
-                           w, b, eps, qs, ds, y, ldy, vec4);
+                           w, b, eps, qs, qh, ds, y, ldy, vec4);
     else if (quant)
         hipLaunchKernelGGL((k_layernorm<true, false>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qs, ds, y, ldy, vec4);
+                           ldx, w, b, eps, qs, qh, ds, y, ldy, vec4);
     else
         hipLaunchKernelGGL((k_layernorm<false, true>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qs, ds, y, ldy, vec4);
+                           ldx, w, b, eps, qs, qh, ds, y, ldy, vec4);
     return hipGetLastError();
 }
 

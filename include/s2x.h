@@ -260,6 +260,12 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream);
 /* Attention precision: 0 (default) = f16-MFMA flash attention with f32
  * softmax and an exact f16 hi/lo split of P; 1 = s2x_attn_fp64. */
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
+/* GEMM kernel: S2X_GEMM_F16_MFMA (default; block dots and the dx*dw scale
+ * tile on f16 MFMA, one VALU fma per element and block) or S2X_GEMM_I8_MFMA
+ * (v_mfma_i32_32x32x32_i8 block dots, VALU convert + scale + fma).  Both
+ * give the same bits. */
+enum { S2X_GEMM_F16_MFMA = 0, S2X_GEMM_I8_MFMA = 1 };
+int s2x_vision_set_gemm_variant(s2x_vision *v, int variant);
 
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */

@@ -97,6 +97,19 @@ def test_small_vision_ragged_equals_per_image(small_vision, pooling):
         assert np.array_equal(out[i], singles[i]), shapes[i]
 
 
+def test_small_vision_gemm_variants_same_bits(small_vision):
+    # the int8-MFMA and f16-MFMA GEMMs compute the same per-block integers and
+    # the same fma chain, so the whole tower must agree bit for bit
+    v, _ = small_vision
+    px = synth.pixels(2, 27 * 27, seed=77)
+    outs = []
+    for variant in (s2x.GEMM_I8_MFMA, s2x.GEMM_F16_MFMA):
+        s2x.call("s2x_vision_set_gemm_variant", v.h, variant)
+        outs.append(v.batch(px, 2, 27, 27, s2x.POOL_PROBE))
+    assert np.array_equal(outs[0], outs[1])
+    assert s2x.lib.s2x_vision_set_gemm_variant(v.h, 7) == 1
+
+
 def test_vision_rejects_bad_shapes(small_vision):
     v, _ = small_vision
     px = np.zeros((4, 768), np.float32)
