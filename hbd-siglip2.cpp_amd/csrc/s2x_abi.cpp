@@ -68,8 +68,10 @@ int s2x_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx, int64_t
     if (!x || !qs || !ds) return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: null pointer");
     if (!aligned(qs, 4) || !aligned(ds, 4) || !aligned(x, 4))
         return fail(S2X_ERR_INVALID_ARG, "quantize_q8_1: qs/ds/x must be 4-byte aligned");
-    hipError_t e = launch_quantize_q8_1(x, K, M, ldx, K_pad, (int8_t *)qs, nullptr,
-                                        (uint32_t *)ds, (hipStream_t)stream);
+    Q81Out o;
+    o.qs = (int8_t *)qs;
+    o.ds = (uint32_t *)ds;
+    hipError_t e = launch_quantize_q8_1(x, K, M, ldx, K_pad, o, (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize_q8_1 launch");
 }
 
@@ -201,12 +203,14 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
     const WeightView wv = planes_view(ws + L.w_off, K_pad, N);
     hipError_t e = repack_into(w_raw, wv, s);
     if (e != hipSuccess) return hip_fail(e, "repack launch");
-    e = launch_quantize_q8_1(x, K, M, ldx, K_pad, nullptr, (_Float16 *)(ws + L.qh_off),
-                             (uint32_t *)(ws + L.ds_off), s);
+    Q81Out o;
+    o.qh = (_Float16 *)(ws + L.qh_off);
+    o.dT = (uint16_t *)(ws + L.dT_off);
+    o.ldT = mmq16_ld_dx(M);
+    e = launch_quantize_q8_1(x, K, M, ldx, K_pad, o, s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
-    e = launch_mmq_f16(wv, (const _Float16 *)(ws + L.qh_off), (const uint32_t *)(ws + L.ds_off), M,
-                       y, N, p, s);
+    e = launch_mmq_f16(wv, o.qh, o.dT, o.ldT, M, y, N, p, s);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
 }
 
@@ -241,8 +245,7 @@ int s2x_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx, const float
     if (st != S2X_OK) return st;
     if (M == 0) return S2X_OK;
     if (!y || ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm: y null or ldy < H");
-    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, nullptr, nullptr, nullptr, y, ldy,
-                                    (hipStream_t)stream);
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, nullptr, y, ldy, (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
 }
 
@@ -255,8 +258,10 @@ int s2x_layernorm_quantize_q8_1(const float *x, int64_t H, int64_t M, int64_t ld
     if (!qs || !ds || !aligned(qs, 4) || !aligned(ds, 4))
         return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: qs/ds null or misaligned");
     if (y && ldy < H) return fail(S2X_ERR_INVALID_ARG, "layernorm_quantize: ldy < H");
-    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, (int8_t *)qs, nullptr, (uint32_t *)ds, y, ldy,
-                                    (hipStream_t)stream);
+    Q81Out o;
+    o.qs = (int8_t *)qs;
+    o.ds = (uint32_t *)ds;
+    hipError_t e = launch_layernorm(x, H, M, ldx, w, b, eps, &o, y, ldy, (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm_quantize launch");
 }
 

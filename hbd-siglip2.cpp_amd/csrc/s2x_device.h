@@ -142,4 +142,28 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanh_f32(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
 }
 
+// Output tile order: XCD-aware (gfx950 dispatches workgroup i to XCD i % 8,
+// so consecutive tile ids are given to the same XCD) and grouped (GM rows of
+// tiles walk N together) so an XCD's concurrent workgroups share X and W
+// tiles in its L2.
+template <int GM>
+__device__ __forceinline__ void tile_coords(int bid, int G, int m_tiles, int n_tiles,
+                                            int &tm, int &tn) {
+    constexpr int NX = 8;
+    int t = bid;
+    if (G >= NX) {
+        const int xcd = bid % NX, local = bid / NX;
+        const int per = G / NX, rem = G % NX;
+        // xcd < rem own per+1 tiles, the rest per
+        t = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    }
+    const int group_size = GM * n_tiles;
+    const int group = t / group_size;
+    const int first_m = group * GM;
+    const int gm = min(GM, m_tiles - first_m);
+    const int in_group = t - group * group_size;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
 }  // namespace s2x

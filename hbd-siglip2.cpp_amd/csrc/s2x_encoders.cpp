@@ -186,8 +186,10 @@ struct Tower {
     GemmTiming timing;
     // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
     bool attn_f64 = false;
-    // GEMM variant: f16-coded operands on f16 MFMA (true) or int8 MFMA; the
-    // quantized activations in `qs` are f16 or int8 accordingly
+    // GEMM variant: f16-coded operands on f16 MFMA (true) or int8 MFMA.  The
+    // quantized activations in `qs` are f16 or int8 accordingly, and `ds`
+    // holds the transposed fp16 scales [KB][mmq16_ld_dx(M)] or the
+    // block_q8_1 scale words [M][KB].
     bool gemm_f16 = true;
 
     ~Tower() {
@@ -232,8 +234,8 @@ struct Tower {
             b = timing.get();
             S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, qs.as<_Float16>(), ds.as<uint32_t>(),
-                                                   M, y, ldy, e, stream)
+        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, qs.as<_Float16>(), ds.as<uint16_t>(),
+                                                   mmq16_ld_dx(M), M, y, ldy, e, stream)
                                   : launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y,
                                                ldy, e, stream);
         if (err != hipSuccess) return hip_fail(err, "mmq launch");
@@ -244,18 +246,33 @@ struct Tower {
         return S2X_OK;
     }
 
-    int8_t *q_i8() { return gemm_f16 ? nullptr : qs.as<int8_t>(); }
-    _Float16 *q_f16() { return gemm_f16 ? qs.as<_Float16>() : nullptr; }
+    // Quantized-activation planes for a GEMM over M rows.
+    Q81Out qout(int64_t M) {
+        Q81Out o;
+        if (gemm_f16) {
+            o.qh = qs.as<_Float16>();
+            o.dT = ds.as<uint16_t>();
+            o.ldT = mmq16_ld_dx(M);
+        } else {
+            o.qs = qs.as<int8_t>();
+            o.ds = ds.as<uint32_t>();
+        }
+        return o;
+    }
+    static size_t ds_bytes(int64_t M, int64_t kmax) {
+        const size_t words = sizeof(uint32_t) * (size_t)(M * (kmax / QK_));
+        const size_t trans = sizeof(uint16_t) * (size_t)(mmq16_ld_dx(M) * (kmax / QK_));
+        return words > trans ? words : trans;
+    }
 
     int quantize(const float *src, int64_t K, int64_t M, int64_t ldx, int64_t K_pad) {
-        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, q_i8(), q_f16(),
-                                            ds.as<uint32_t>(), stream);
+        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, qout(M), stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize launch");
     }
 
     int layernorm_q(const float *src, int64_t M, const float *w, const float *b, float *y) {
-        hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, q_i8(), q_f16(),
-                                        ds.as<uint32_t>(), y, H, stream);
+        const Q81Out o = qout(M);
+        hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, &o, y, H, stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
     }
 
@@ -263,7 +280,7 @@ struct Tower {
         const int64_t kmax = F_pad > H ? F_pad : H;
         S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
         S2X_TRY(ensure(qs, 2 * (size_t)(M * kmax), stream));  // f16 or int8 quants
-        S2X_TRY(ensure(ds, sizeof(uint32_t) * (size_t)(M * (kmax / QK_)), stream));
+        S2X_TRY(ensure(ds, ds_bytes(M, kmax), stream));
         S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
         S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
@@ -403,8 +420,7 @@ struct s2x_vision {
         if (pooling == S2X_POOL_MEAN) {
             S2X_TRY(ensure(hid, sizeof(float) * (size_t)(M * H), t.stream));
             hipError_t e = launch_layernorm(t.x.as<float>(), H, M, H, post_ln_w, post_ln_b, t.eps,
-                                            nullptr, nullptr, nullptr, hid.as<float>(), H,
-                                            t.stream);
+                                            nullptr, hid.as<float>(), H, t.stream);
             if (e != hipSuccess) return hip_fail(e, "post-LN launch");
             e = launch_mean_pool(hid.as<float>(), H, t.seg_start(), t.seg_len(n_img), n_img,
                                  out_dev, t.stream);
@@ -505,7 +521,7 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
         if (hipMalloc(reinterpret_cast<void **>(&v->probe_q), sizeof(float) * (size_t)H) != hipSuccess)
             st = fail(S2X_ERR_OOM, "probe_q alloc");
         if (!st) st = ensure(t.qs, 2 * (size_t)H, s);
-        if (!st) st = ensure(t.ds, (size_t)(H / QK_) * 4, s);
+        if (!st) st = ensure(t.ds, Tower::ds_bytes(1, H), s);
         if (!st) st = t.quantize(probe, H, 1, H, H);
         if (!st) st = t.gemm(hq, 1, v->probe_q, H, EpiParams{EPI_BIAS, hq_b, nullptr, 0, 0, 0}, H);
         if (!st && hipStreamSynchronize(s) != hipSuccess) st = fail(S2X_ERR_HIP, "probe sync");
@@ -678,8 +694,8 @@ struct s2x_text {
                                             t.x.as<float>(), t.stream);
         if (e != hipSuccess) return hip_fail(e, "get_rows launch");
         S2X_TRY(t.run_layers(M, n_batch, n_tok, key_valid_dev));
-        e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr, nullptr,
-                             nullptr, t.x.as<float>(), H, t.stream);
+        e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr,
+                             t.x.as<float>(), H, t.stream);
         if (e != hipSuccess) return hip_fail(e, "final LN launch");
         S2X_TRY(ensure(rows, sizeof(int32_t) * (size_t)n_batch, t.stream));
         S2X_TRY(ensure(pooled, sizeof(float) * (size_t)(n_batch * H), t.stream));

@@ -27,9 +27,9 @@ inline int64_t round_up_i(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
 
 // Planes of a repacked (K_pad, N) weight in one buffer, each at a 256-byte
 // boundary: int8 qs [N][K_pad], f32 d [N][KB], f16 qh [N][K_pad] (the same
-// integers), fp16 bits dh [N][KB].
+// integers), fp16 bits of d transposed, dT [KB][mmq16_ld_dw(N)].
 struct WeightPlanes {
-    size_t qs, d, qh, dh, total;
+    size_t qs, d, qh, dT, total;
 };
 inline WeightPlanes weight_planes(int64_t K_pad, int64_t N) {
     const int64_t KB = K_pad / QK_;
@@ -37,8 +37,8 @@ inline WeightPlanes weight_planes(int64_t K_pad, int64_t N) {
     p.qs = 0;
     p.d = p.qs + (size_t)round_up_i(K_pad * N, 256);
     p.qh = p.d + (size_t)round_up_i(N * KB * 4, 256);
-    p.dh = p.qh + (size_t)round_up_i(K_pad * N * 2, 256);
-    p.total = p.dh + (size_t)round_up_i(N * KB * 2, 256);
+    p.dT = p.qh + (size_t)round_up_i(K_pad * N * 2, 256);
+    p.total = p.dT + (size_t)round_up_i(KB * mmq16_ld_dw(N) * 2, 256);
     return p;
 }
 inline size_t weight_planes_bytes(int64_t K_pad, int64_t N) {
@@ -51,7 +51,8 @@ inline WeightView planes_view(void *base, int64_t K_pad, int64_t N) {
     v.qs = reinterpret_cast<const int8_t *>(b + p.qs);
     v.d = reinterpret_cast<const float *>(b + p.d);
     v.qh = reinterpret_cast<const _Float16 *>(b + p.qh);
-    v.dh = reinterpret_cast<const uint16_t *>(b + p.dh);
+    v.dT = reinterpret_cast<const uint16_t *>(b + p.dT);
+    v.ldT = mmq16_ld_dw(N);
     v.K_pad = K_pad;
     v.N = N;
     return v;
@@ -59,19 +60,20 @@ inline WeightView planes_view(void *base, int64_t K_pad, int64_t N) {
 inline hipError_t repack_into(const void *raw, const WeightView &v, hipStream_t s) {
     return launch_repack_q8_0(raw, v.K_pad, v.N, const_cast<int8_t *>(v.qs),
                               const_cast<float *>(v.d), const_cast<_Float16 *>(v.qh),
-                              const_cast<uint16_t *>(v.dh), s);
+                              const_cast<uint16_t *>(v.dT), v.ldT, s);
 }
 
-// Workspace of the drop-in MUL_MAT: repacked W, then X as f16-coded Q8_1.
+// Workspace of the drop-in MUL_MAT: repacked W, then X as f16-coded Q8_1
+// (quants [M][K_pad] and transposed scales [KB][mmq16_ld_dx(M)]).
 struct MulMatWs {
-    size_t w_off, qh_off, ds_off, total;
+    size_t w_off, qh_off, dT_off, total;
 };
 inline MulMatWs mul_mat_ws_layout(int64_t K_pad, int64_t N, int64_t M) {
     MulMatWs L;
     L.w_off = 0;
     L.qh_off = weight_planes_bytes(K_pad, N);
-    L.ds_off = L.qh_off + (size_t)round_up_i(M * K_pad * 2, 256);
-    L.total = L.ds_off + (size_t)round_up_i(M * (K_pad / QK_) * 4, 256);
+    L.dT_off = L.qh_off + (size_t)round_up_i(M * K_pad * 2, 256);
+    L.total = L.dT_off + (size_t)round_up_i((K_pad / QK_) * mmq16_ld_dx(M) * 2, 256);
     return L;
 }
 

@@ -18,9 +18,25 @@ struct WeightView {
     const int8_t *qs;     // N rows of K_pad int8
     const float  *d;      // N rows of KB f32 (fp16 values widened)
     const _Float16 *qh;   // N rows of K_pad f16 holding the same integers
-    const uint16_t *dh;   // N rows of KB fp16 bits of d
+    const uint16_t *dT;   // KB rows of ldT fp16 bits of d (transposed)
+    int64_t ldT;          // >= round_up(N, MMQ16_BN)
     int64_t K_pad;        // multiple of 32
     int64_t N;
+};
+
+// Output tile of the f16-MFMA GEMM; transposed scale planes are padded to it.
+constexpr int64_t MMQ16_BM = 256;
+constexpr int64_t MMQ16_BN = 128;
+inline int64_t mmq16_ld_dx(int64_t M) { return (M + MMQ16_BM - 1) / MMQ16_BM * MMQ16_BM; }
+inline int64_t mmq16_ld_dw(int64_t N) { return (N + MMQ16_BN - 1) / MMQ16_BN * MMQ16_BN; }
+
+// Destination planes of a Q8_1 quantization (any subset may be null).
+struct Q81Out {
+    int8_t   *qs = nullptr;  // [M][K_pad] int8 quants
+    _Float16 *qh = nullptr;  // [M][K_pad] the same quants as f16 (exact)
+    uint32_t *ds = nullptr;  // [M][KB] fp16 d | fp16 s << 16 (block_q8_1 scales)
+    uint16_t *dT = nullptr;  // [KB][ldT] fp16 bits of d, transposed
+    int64_t   ldT = 0;
 };
 
 enum EpiKind { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4 };
@@ -34,35 +50,34 @@ struct EpiParams {
     int64_t      dump_kb;     // EPI_DUMP_I: the block whose int32 dot is written
 };
 
-// a1: F32 -> Q8_1: ds u32 (fp16 d | fp16 s << 16) [M][KB] and the quants as
-// int8 qs [M][K_pad] and/or as f16 qh [M][K_pad] (same integers; either may
-// be null).
+// a1: F32 -> Q8_1 into the planes of `out`.
 hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
-                                int64_t K_pad, int8_t *qs, _Float16 *qh, uint32_t *ds,
-                                hipStream_t stream);
+                                int64_t K_pad, const Q81Out &out, hipStream_t stream);
 
 // a2: raw block_q8_0 (N rows of K_pad/32 34-byte blocks, device) -> WeightView
-// planes (qh / dh may be null)
+// planes (qh / dT may be null)
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
-                              float *d, _Float16 *qh, uint16_t *dh, hipStream_t stream);
+                              float *d, _Float16 *qh, uint16_t *dT, int64_t ldT,
+                              hipStream_t stream);
 
 // a3: Y = W x X(Q8_1) with epilogue.
 // launch_mmq: int8 operands, v_mfma_i32_32x32x32_i8 block dots, VALU rescale.
 hipError_t launch_mmq(const WeightView &w, const int8_t *xq, const uint32_t *xds,
                       int64_t M, float *y, int64_t ldy, const EpiParams &epi,
                       hipStream_t stream);
-// launch_mmq_f16: f16-coded operands (w.qh / w.dh and xh), block dots and the
-// dx*dw scale tile both on f16 MFMA, one VALU fma per element and block.
-hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint32_t *xds,
-                          int64_t M, float *y, int64_t ldy, const EpiParams &epi,
-                          hipStream_t stream);
+// launch_mmq_f16: f16-coded operands (w.qh / w.dT, xh [M][K_pad] and the
+// transposed X scales xdT [KB][ld_dx], ld_dx >= mmq16_ld_dx(M)), block dots
+// and the dx*dw scale tile on f16 MFMA, one VALU fma per element and block.
+// xh, xdT, w.qh and w.dT must be 16-byte aligned and ld_dx a multiple of 8.
+hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
+                          int64_t ld_dx, int64_t M, float *y, int64_t ldy,
+                          const EpiParams &epi, hipStream_t stream);
 
-// a4: LayerNorm (+ Q8_1).  qs/qh/ds may be null (no quantized output), y may
-// be null (no f32 output); at least one is set.
+// a4: LayerNorm (+ Q8_1).  q may be null (no quantized output), y may be
+// null (no f32 output); at least one is set.
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
-                            const float *w, const float *b, float eps, int8_t *qs,
-                            _Float16 *qh, uint32_t *ds, float *y, int64_t ldy,
-                            hipStream_t stream);
+                            const float *w, const float *b, float eps, const Q81Out *q,
+                            float *y, int64_t ldy, hipStream_t stream);
 
 // a5: standalone epilogues
 hipError_t launch_bias_residual(const float *mm, const float *bias, const float *resid,

@@ -44,30 +44,6 @@ struct MmqCfg {
     static_assert((BM * KS * 2) % NT == 0 && (BN * KS * 2) % NT == 0, "chunks");
 };
 
-// Output tile order: XCD-aware (gfx950 dispatches workgroup i to XCD i % 8,
-// so consecutive tile ids are given to the same XCD) and grouped (GM rows of
-// tiles walk N together) so an XCD's concurrent workgroups share X and W
-// tiles in its L2.
-__device__ __forceinline__ void tile_coords(int bid, int G, int m_tiles, int n_tiles,
-                                            int &tm, int &tn) {
-    constexpr int NX = 8;
-    int t = bid;
-    if (G >= NX) {
-        const int xcd = bid % NX, local = bid / NX;
-        const int per = G / NX, rem = G % NX;
-        // xcd < rem own per+1 tiles, the rest per
-        t = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    }
-    constexpr int GM = 8;
-    const int group_size = GM * n_tiles;
-    const int group = t / group_size;
-    const int first_m = group * GM;
-    const int gm = min(GM, m_tiles - first_m);
-    const int in_group = t - group * group_size;
-    tm = first_m + in_group % gm;
-    tn = in_group / gm;
-}
-
 template <int BM, int BN, int WM, int WN, int KS, int EPI>
 __global__ __launch_bounds__(WM *WN *WAVE) void k_mmq(
     const int8_t *__restrict__ xq, const uint32_t *__restrict__ xds,
@@ -82,7 +58,7 @@ __global__ __launch_bounds__(WM *WN *WAVE) void k_mmq(
     const int wm = wave / WN, wn = wave % WN;
     const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
     int tmi, tni;
-    tile_coords(blockIdx.x, gridDim.x, m_tiles, n_tiles, tmi, tni);
+    tile_coords<8>(blockIdx.x, gridDim.x, m_tiles, n_tiles, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const int64_t K_pad = (int64_t)KB * QK;
 
@@ -310,265 +286,6 @@ hipError_t launch_mmq(const WeightView &w, const int8_t *xq, const uint32_t *xds
         return run_mmq<BM, BN, WM, WN, KS, EPI_BIAS_RESID>(w, xq, xds, M, y, ldy, epi, stream);
     case EPI_DUMP_I:
         return run_mmq<BM, BN, WM, WN, KS, EPI_DUMP_I>(w, xq, xds, M, y, ldy, epi, stream);
-    default: return hipErrorInvalidValue;
-    }
-}
-
-// ===========================================================================
-// f16-MFMA variant.  The per-block rescale above costs three VALU
-// instructions per output element and block (convert, scale product, fma)
-// against one 32-cycle int8 MFMA per 1,024 block dots, i.e. 6x the VALU
-// issue budget.  Here both integer and scale work move to the matrix pipe:
-//   * the quants are stored as f16 (exact integers, |q| <= 128), and two
-//     v_mfma_f32_32x32x16_f16 give the block dot I as an exact f32 (every
-//     product is an integer < 2^14, every partial sum an integer < 2^24);
-//   * the scale tile s[i][j] = dx[i] * dw[j] is one more f16 MFMA: A holds
-//     dx[row] in all k slots, B holds dw[col] in one k slot and zeros
-//     elsewhere, so each output is one exact f16 x f16 product;
-//   * the VALU does acc = fmaf(I, s, acc): the same value as the int8 path
-//     and the CPU (fmaf((float)I, dw*dx, acc)), one instruction.
-// Per 32x32 subtile and block: 3 MFMAs (96 cycles) and 16 VALU FMAs per
-// lane (64 issue cycles): matrix-pipe bound.
-// ===========================================================================
-template <int BM, int BN, int WM, int WN, int KS>
-struct Mmq16Cfg {
-    static constexpr int NT = WM * WN * WAVE;
-    static constexpr int TM = BM / WM / 32;
-    static constexpr int TN = BN / WN / 32;
-    static constexpr int ROWB = KS * QK * 2 + 16;    // LDS row pitch in bytes (f16 quants)
-    static constexpr int XCH = BM * KS * 4 / NT;     // 16-byte X chunks per thread
-    static constexpr int WCH = BN * KS * 4 / NT;
-    static constexpr int XSC = (BM * KS + NT - 1) / NT;
-    static constexpr int WSC = (BN * KS + NT - 1) / NT;
-    static constexpr int LDS_X = BM * ROWB;
-    static constexpr int LDS_W = BN * ROWB;
-    static constexpr int LDS_D = ((BM + BN) * KS * 2 + 15) / 16 * 16;
-    static constexpr int LDS_STAGE = LDS_X + LDS_W + LDS_D;
-    static_assert(BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "tile");
-    static_assert((BM * KS * 4) % NT == 0 && (BN * KS * 4) % NT == 0, "chunks");
-};
-
-template <int BM, int BN, int WM, int WN, int KS, int EPI>
-__global__ __launch_bounds__(WM *WN *WAVE) void k_mmq_f16(
-    const _Float16 *__restrict__ xq, const uint32_t *__restrict__ xds,
-    const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdh, int M, int N, int KB,
-    float *__restrict__ y, int64_t ldy, EpiParams epi) {
-    using C = Mmq16Cfg<BM, BN, WM, WN, KS>;
-    extern __shared__ __align__(16) uint8_t lds[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
-    int tmi, tni;
-    tile_coords(blockIdx.x, gridDim.x, m_tiles, n_tiles, tmi, tni);
-    const int m0 = tmi * BM, n0 = tni * BN;
-    const int64_t K_pad = (int64_t)KB * QK;
-    const int n_stages = (KB + KS - 1) / KS;
-
-    v4i xr[C::XCH], wr[C::WCH];
-    uint16_t xsr[C::XSC], wsr[C::WSC];
-
-    auto gload = [&](int stage) {
-        const int kb0 = stage * KS;
-#pragma unroll
-        for (int i = 0; i < C::XCH; ++i) {
-            const int idx = tid + i * C::NT;
-            const int r = idx / (KS * 4), c = idx % (KS * 4);  // c: 16-byte chunk, 4 per block
-            const int m = m0 + r, kb = kb0 + (c >> 2);
-            v4i v = {0, 0, 0, 0};
-            if (m < M && kb < KB)
-                v = *reinterpret_cast<const v4i *>(xq + (int64_t)m * K_pad + (int64_t)kb * QK + (c & 3) * 8);
-            xr[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < C::WCH; ++i) {
-            const int idx = tid + i * C::NT;
-            const int r = idx / (KS * 4), c = idx % (KS * 4);
-            const int n = n0 + r, kb = kb0 + (c >> 2);
-            v4i v = {0, 0, 0, 0};
-            if (n < N && kb < KB)
-                v = *reinterpret_cast<const v4i *>(wq + (int64_t)n * K_pad + (int64_t)kb * QK + (c & 3) * 8);
-            wr[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < C::XSC; ++i) {
-            const int idx = tid + i * C::NT;
-            uint16_t v = 0;
-            if (idx < BM * KS) {
-                const int r = idx / KS, k = idx % KS;
-                const int m = m0 + r, kb = kb0 + k;
-                if (m < M && kb < KB) v = (uint16_t)(xds[(int64_t)m * KB + kb] & 0xffffu);
-            }
-            xsr[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < C::WSC; ++i) {
-            const int idx = tid + i * C::NT;
-            uint16_t v = 0;
-            if (idx < BN * KS) {
-                const int r = idx / KS, k = idx % KS;
-                const int n = n0 + r, kb = kb0 + k;
-                if (n < N && kb < KB) v = wdh[(int64_t)n * KB + kb];
-            }
-            wsr[i] = v;
-        }
-    };
-    auto sstore = [&](int buf) {
-        uint8_t *base = lds + buf * C::LDS_STAGE;
-        uint8_t *xs = base;
-        uint8_t *ws = base + C::LDS_X;
-        uint16_t *xd = reinterpret_cast<uint16_t *>(base + C::LDS_X + C::LDS_W);  // [KS][BM]
-        uint16_t *wdl = xd + KS * BM;                                             // [KS][BN]
-#pragma unroll
-        for (int i = 0; i < C::XCH; ++i) {
-            const int idx = tid + i * C::NT;
-            const int r = idx / (KS * 4), c = idx % (KS * 4);
-            *reinterpret_cast<v4i *>(xs + r * C::ROWB + c * 16) = xr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::WCH; ++i) {
-            const int idx = tid + i * C::NT;
-            const int r = idx / (KS * 4), c = idx % (KS * 4);
-            *reinterpret_cast<v4i *>(ws + r * C::ROWB + c * 16) = wr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::XSC; ++i) {
-            const int idx = tid + i * C::NT;
-            if (idx < BM * KS) xd[(idx % KS) * BM + idx / KS] = xsr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::WSC; ++i) {
-            const int idx = tid + i * C::NT;
-            if (idx < BN * KS) wdl[(idx % KS) * BN + idx / KS] = wsr[i];
-        }
-    };
-
-    float acc[C::TM][C::TN][16];
-#pragma unroll
-    for (int a = 0; a < C::TM; ++a)
-#pragma unroll
-        for (int b = 0; b < C::TN; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-    const int wrow0 = wm * (BM / WM);
-    const int wcol0 = wn * (BN / WN);
-    const int lr = lane & 31;
-    const int lh = lane >> 5;
-
-    gload(0);
-    sstore(0);
-    __syncthreads();
-
-    for (int s = 0; s < n_stages; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < n_stages) gload(s + 1);
-
-        const uint8_t *base = lds + buf * C::LDS_STAGE;
-        const uint8_t *xs = base;
-        const uint8_t *ws = base + C::LDS_X;
-        const uint16_t *xd = reinterpret_cast<const uint16_t *>(base + C::LDS_X + C::LDS_W);
-        const uint16_t *wdl = xd + KS * BM;
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-            if (s * KS + kk >= KB) break;
-            v8h af[C::TM][2], bfr[C::TN][2], sa[C::TM], sb[C::TN];
-#pragma unroll
-            for (int a = 0; a < C::TM; ++a) {
-                const uint8_t *p = xs + (wrow0 + a * 32 + lr) * C::ROWB + kk * 64 + lh * 16;
-                af[a][0] = *reinterpret_cast<const v8h *>(p);
-                af[a][1] = *reinterpret_cast<const v8h *>(p + 32);
-                const _Float16 dx = __builtin_bit_cast(_Float16, xd[kk * BM + wrow0 + a * 32 + lr]);
-                sa[a] = v8h{dx, dx, dx, dx, dx, dx, dx, dx};
-            }
-#pragma unroll
-            for (int b = 0; b < C::TN; ++b) {
-                const uint8_t *p = ws + (wcol0 + b * 32 + lr) * C::ROWB + kk * 64 + lh * 16;
-                bfr[b][0] = *reinterpret_cast<const v8h *>(p);
-                bfr[b][1] = *reinterpret_cast<const v8h *>(p + 32);
-                const _Float16 dw = __builtin_bit_cast(_Float16, wdl[kk * BN + wcol0 + b * 32 + lr]);
-                const _Float16 z = (_Float16)0.0f;
-                sb[b] = v8h{lh ? z : dw, z, z, z, z, z, z, z};
-            }
-#pragma unroll
-            for (int a = 0; a < C::TM; ++a)
-#pragma unroll
-                for (int b = 0; b < C::TN; ++b) {
-                    const v16f zero = {};
-                    v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][0], bfr[b][0], zero, 0, 0, 0);
-                    I = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][1], bfr[b][1], I, 0, 0, 0);
-                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa[a], sb[b], zero, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], sc[r], acc[a][b][r]);
-                }
-        }
-
-        if (s + 1 < n_stages) sstore(buf ^ 1);
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int a = 0; a < C::TM; ++a)
-#pragma unroll
-        for (int b = 0; b < C::TN; ++b) {
-            const int n = n0 + wcol0 + b * 32 + lr;
-            if (n >= N) continue;
-            float bias = 0.0f;
-            if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID) bias = epi.bias[n];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wrow0 + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m >= M) continue;
-                float v = acc[a][b][r];
-                if (EPI == EPI_BIAS) {
-                    v = v + bias;
-                } else if (EPI == EPI_BIAS_GELU) {
-                    v = gelu_tanh(v + bias);
-                } else if (EPI == EPI_BIAS_RESID) {
-                    const int64_t rm = epi.resid_rows > 0 ? (int64_t)m % epi.resid_rows : (int64_t)m;
-                    v = (v + bias) + epi.resid[rm * epi.ld_resid + n];
-                }
-                y[(int64_t)m * ldy + n] = v;
-            }
-        }
-}
-
-template <int BM, int BN, int WM, int WN, int KS, int EPI>
-static hipError_t run_mmq_f16(const WeightView &w, const _Float16 *xq, const uint32_t *xds,
-                              int64_t M, float *y, int64_t ldy, const EpiParams &epi,
-                              hipStream_t stream) {
-    using C = Mmq16Cfg<BM, BN, WM, WN, KS>;
-    const int m_tiles = (int)((M + BM - 1) / BM), n_tiles = (int)((w.N + BN - 1) / BN);
-    const int G = m_tiles * n_tiles;
-    const size_t lds = 2 * (size_t)C::LDS_STAGE;
-    auto kern = k_mmq_f16<BM, BN, WM, WN, KS, EPI>;
-    static bool attr_set = false;  // idempotent; a racing second call repeats it harmlessly
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(kern, dim3(G), dim3(C::NT), lds, stream, xq, xds, w.qh, w.dh, (int)M,
-                       (int)w.N, (int)(w.K_pad / QK), y, ldy, epi);
-    return hipGetLastError();
-}
-
-hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint32_t *xds, int64_t M,
-                          float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
-    if (M == 0 || w.N == 0) return hipSuccess;
-    if (!w.qh || !w.dh) return hipErrorInvalidValue;
-    constexpr int BM = 128, BN = 128, WM = 2, WN = 2, KS = 2;
-    switch (epi.kind) {
-    case EPI_NONE: return run_mmq_f16<BM, BN, WM, WN, KS, EPI_NONE>(w, xh, xds, M, y, ldy, epi, stream);
-    case EPI_BIAS: return run_mmq_f16<BM, BN, WM, WN, KS, EPI_BIAS>(w, xh, xds, M, y, ldy, epi, stream);
-    case EPI_BIAS_GELU:
-        return run_mmq_f16<BM, BN, WM, WN, KS, EPI_BIAS_GELU>(w, xh, xds, M, y, ldy, epi, stream);
-    case EPI_BIAS_RESID:
-        return run_mmq_f16<BM, BN, WM, WN, KS, EPI_BIAS_RESID>(w, xh, xds, M, y, ldy, epi, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -1,0 +1,342 @@
+// s2x_mmq16.hip -- Q8_0 (weights) x Q8_1 (activations) GEMM on gfx950 f16
+// MFMA, bit-identical to the int8 formulation of s2x_mmq.hip:
+//
+//   Y[m, n] = sum_kb  fmaf(I_kb[m,n], dw[n,kb] * dx[m,kb], acc)   (kb in order)
+//
+// Why f16: with v_mfma_i32_32x32x32_i8 the per-block rescale costs three
+// VALU instructions per output and block (convert, scale product, fma)
+// against one 32-cycle MFMA per 1,024 outputs, i.e. 6x the VALU issue
+// budget.  Here the quants are stored as f16 (exact integers, |q| <= 128):
+//   * two v_mfma_f32_32x32x16_f16 give the block dot I as an exact f32
+//     (products are integers < 2^14, partial sums integers < 2^20);
+//   * the scale tile s[i][j] = dx[i] * dw[j] is one more f16 MFMA: A holds
+//     dx[row] in every k slot, B holds dw[col] in k slot 0 and zeros
+//     elsewhere, so each output is one exact f16 x f16 product in f32;
+//   * the VALU does acc = fmaf(I, s, acc) -- the CPU's operation, one
+//     instruction.
+// Per 32x32 subtile and block: 3 MFMAs (96 cycles) against 16 VALU fmas
+// (64 cycles): the matrix pipe bounds the kernel at 1/3 of the int8 peak.
+//
+// Tile: BM x 128 outputs per workgroup of BM/64 x 2 waves, each wave 64 x 64
+// (2 x 2 subtiles).  One pipeline stage is one 32-value block of K: BM X rows
+// and 128 W rows of 64 bytes plus their fp16 scales.  Stages are filled by
+// LDS DMA (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
+// LDS base + 16 * lane), so no staging registers; NS stages rotate, and the
+// only waits are the wave's own DMA count (s_waitcnt vmcnt) and one barrier
+// per block.  With PIPE the next stage's fragments are read from LDS into a
+// second register set while the current one feeds the MFMAs.
+//
+// LDS layout of a stage's quant rows: 16-byte chunk c of row r is stored at
+// chunk position c ^ ((r >> 2) & 3) of the row (64-byte rows): the MFMA
+// operand reads (32 rows x one chunk per half-wave) then hit 16 distinct
+// 16-byte bank groups per 16 lanes, which measured conflict-free on gfx950.
+// The DMA side applies the same permutation on the global address each
+// lane fetches.
+//
+// MFMA f16 32x32x16 layout: lane l supplies row (l & 31) of A and column
+// (l & 31) of B, k-slots 8*(l >> 5) .. +7; result register r of lane l holds
+// row 8*(r/4) + 4*(l/32) + (r%4), column (l & 31).
+#include "s2x_device.h"
+#include "s2x_kernels.h"
+
+#include <type_traits>
+
+namespace s2x {
+namespace mmq16 {
+
+constexpr int BN = (int)MMQ16_BN;
+constexpr int ROWB = QK * 2;  // one block of f16 quants per row and stage
+constexpr int GM = 8;         // tile-row group of the tile order
+constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
+
+template <int BM_, int NS_>
+struct Cfg {
+    static constexpr int BM = BM_, NS = NS_;
+    static constexpr int WGM = BM / 64;                 // waves along M (2 along N)
+    static constexpr int NT = WGM * 2 * WAVE;
+    static constexpr int XI = BM * 4 / NT;              // X DMA instructions per stage
+    static constexpr int WI = BN * 4 / NT;              // W DMA instructions per stage
+    static constexpr int X_BYTES = BM * ROWB;
+    static constexpr int DX_OFF = X_BYTES + BN * ROWB;  // BM fp16 X scales
+    static constexpr int DW_OFF = DX_OFF + BM * 2;      // BN fp16 W scales
+    static constexpr int Z_OFF = DW_OFF + BN * 2;       // 16 zero bytes
+    static constexpr int STAGE = Z_OFF + 16;
+    static constexpr int LDS = NS * STAGE;
+    static_assert(BM % 64 == 0 && XI >= 1 && WI >= 1 && BM / 8 <= WAVE && BN / 8 <= WAVE, "config");
+    static_assert(NS >= 2 && NS <= 4, "wait table / unroll");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct Frag {
+    v8h a[2][2], b[2][2];   // [subtile][k half]
+    uint32_t dx[2], dw[2];  // fp16 bits of the row / column scales (0 on lanes 32..63)
+};
+
+// 16 bytes per lane from buffer r at voffset + soffset into LDS at
+// lds_wave_base + 16 * lane; reads past the buffer's size return zeros.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                      uint8_t *lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 16, voff, soff, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// This wave's LDS reads done, then the workgroup barrier (no vmcnt wait:
+// later stages' DMA stays in flight).
+__device__ __forceinline__ void block_sync_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Wait until a stage has landed, given `after` later stages already issued
+// and L DMA instructions per stage from this wave.
+template <int L>
+__device__ __forceinline__ void wait_after(int after) {
+    switch (after) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<L>(); break;
+    case 2: wait_vm<2 * L>(); break;
+    default: wait_vm<3 * L>(); break;
+    }
+}
+
+// Waves 0 and 1 also fetch the X and the W scales.
+template <class C>
+__device__ __forceinline__ void wait_stage(bool scale_wave, int after) {
+    if (scale_wave)
+        wait_after<C::XI + C::WI + 1>(after);
+    else
+        wait_after<C::XI + C::WI>(after);
+}
+
+template <class C, int EPI>
+__global__ __launch_bounds__(C::NT) void k_mmq16(
+    const _Float16 *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
+    const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
+    int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
+    constexpr int BM = C::BM, NS = C::NS, NT = C::NT;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
+    int tmi, tni;
+    tile_coords<GM>(blockIdx.x, gridDim.x, m_tiles, n_tiles, tmi, tni);
+    const int m0 = tmi * BM, n0 = tni * BN;
+    const int64_t K_pad = (int64_t)KB * QK;
+    const uint32_t row_bytes = (uint32_t)(K_pad * 2);
+
+    // Buffers over this tile's rows: rows past M / N read as zeros (their
+    // outputs are never stored).  Position p (16-byte unit) of a stage's
+    // quant rows holds chunk (p & 3) ^ ((row >> 2) & 3) of row p >> 2.
+    const auto clip = [](int64_t bytes) { return (int)min(bytes, (int64_t)0x7fffffff); };
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(xq + (int64_t)m0 * K_pad), (short)0, clip((int64_t)(M - m0) * K_pad * 2), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(wq + (int64_t)n0 * K_pad), (short)0, clip((int64_t)(N - n0) * K_pad * 2), BUF_DW3);
+    uint32_t xv[C::XI], wv[C::WI];
+#pragma unroll
+    for (int i = 0; i < C::XI; ++i) {
+        const int p = i * NT + tid;
+        const int row = p >> 2, chunk = (p & 3) ^ ((row >> 2) & 3);
+        xv[i] = (uint32_t)row * row_bytes + (uint32_t)chunk * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::WI; ++i) {
+        const int p = i * NT + tid;
+        const int row = p >> 2, chunk = (p & 3) ^ ((row >> 2) & 3);
+        wv[i] = (uint32_t)row * row_bytes + (uint32_t)chunk * 16;
+    }
+    // wave 0: X scales (BM/8 lanes x 8), wave 1: W scales (BN/8 lanes x 8)
+    const bool scale_wave = wave < 2;
+    const bool s_lane = lane < (wave == 0 ? BM / 8 : BN / 8);
+    const __amdgpu_buffer_rsrc_t sr =
+        wave == 0 ? __builtin_amdgcn_make_buffer_rsrc((void *)(xdT + m0), (short)0,
+                                                      clip((KB * ld_dx - m0) * 2), BUF_DW3)
+                  : __builtin_amdgcn_make_buffer_rsrc((void *)(wdT + n0), (short)0,
+                                                      clip((KB * ld_dw - n0) * 2), BUF_DW3);
+    const uint32_t s_stride = (uint32_t)((wave == 0 ? ld_dx : ld_dw) * 2);
+    const int s_dst = wave == 0 ? C::DX_OFF : C::DW_OFF;
+
+    // Fill stage buffer `buf` with block kb.  buf is free: every wave has
+    // finished reading it before the last barrier.
+    auto issue = [&](int kb, int buf) {
+        uint8_t *sb = lds + buf * C::STAGE;
+        const uint32_t koff = (uint32_t)kb * ROWB;
+#pragma unroll
+        for (int i = 0; i < C::XI; ++i) dma16(xr, xv[i], koff, sb + (i * NT + wave * 64) * 16);
+#pragma unroll
+        for (int i = 0; i < C::WI; ++i)
+            dma16(wr, wv[i], koff, sb + C::X_BYTES + (i * NT + wave * 64) * 16);
+        if (scale_wave && s_lane) dma16(sr, (uint32_t)lane * 16, (uint32_t)kb * s_stride, sb + s_dst);
+    };
+
+    // the zero words read by lanes 32..63 for the scale operands
+    if (tid < NS) *reinterpret_cast<v4i *>(lds + tid * C::STAGE + C::Z_OFF) = v4i{0, 0, 0, 0};
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    const int lr = lane & 31, lh = lane >> 5;
+    const int sw = (lr >> 2) & 3;  // chunk permutation of the rows this lane reads
+    const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
+    const int xrow0 = wm * 64 + lr, wcol0 = wn * 64 + lr;
+    const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
+    // scale operands: k slot 0 (lanes 0..31) holds the scale, the rest zeros
+    const int dxo0 = lh ? C::Z_OFF : C::DX_OFF + xrow0 * 2;
+    const int dxo1 = lh ? C::Z_OFF : C::DX_OFF + (xrow0 + 32) * 2;
+    const int dwo0 = lh ? C::Z_OFF : C::DW_OFF + wcol0 * 2;
+    const int dwo1 = lh ? C::Z_OFF : C::DW_OFF + (wcol0 + 32) * 2;
+
+    auto load_frag = [&](const uint8_t *sb, Frag &f) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            f.a[a][0] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c0);
+            f.a[a][1] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c1);
+        }
+        f.dx[0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
+        f.dx[1] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f.b[b][0] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c0);
+            f.b[b][1] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c1);
+        }
+        f.dw[0] = *reinterpret_cast<const uint16_t *>(sb + dwo0);
+        f.dw[1] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
+    };
+
+    // One block of K.  Subtile k = 2a + b gets I (two MFMAs) and the scale
+    // tile (one MFMA); acc = fmaf(I, s, acc) for subtile k runs after subtile
+    // k+1's MFMAs are issued, and subtile 3's in the next block, so the VALU
+    // work overlaps the matrix pipe.  Each acc element still receives its
+    // fmas in block order.
+    v16f Ip, Sp;
+    bool pending = false;
+    auto mma = [&](const Frag &f) {
+        const v16f zero = {};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int a = k >> 1, b = k & 1;
+            v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][0], f.b[b][0], zero, 0, 0, 0);
+            const v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(v8h, v4i{(int)f.dx[a], 0, 0, 0}),
+                __builtin_bit_cast(v8h, v4i{(int)f.dw[b], 0, 0, 0}), zero, 0, 0, 0);
+            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
+            const int pa = ((k + 3) & 3) >> 1, pb = (k + 3) & 1;
+            if (k > 0 || pending) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf(Ip[r], Sp[r], acc[pa][pb][r]);
+            }
+            Ip = I;
+            Sp = S;
+        }
+        pending = true;
+    };
+
+    // NS-1 blocks in flight; stage s+NS-1 refills the buffer of stage s-1.
+    // The stage loop is unrolled NS times so each LDS read's stage offset is
+    // an instruction immediate.
+    const int npro = min(NS - 1, KB);
+    for (int s = 0; s < npro; ++s) issue(s, s);
+    Frag F;
+    auto step = [&](int s, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        wait_stage<C>(scale_wave, min(NS - 2, KB - 1 - s));
+        block_sync_lds();
+        if (s + NS - 1 < KB) issue(s + NS - 1, (buf + NS - 1) % NS);
+        load_frag(lds + buf * C::STAGE, F);
+        mma(F);
+    };
+    for (int s = 0; s < KB; s += NS) {
+        step(s, std::integral_constant<int, 0>{});
+        if (s + 1 < KB) step(s + 1, std::integral_constant<int, 1 % NS>{});
+        if constexpr (NS > 2) {
+            if (s + 2 < KB) step(s + 2, std::integral_constant<int, 2 % NS>{});
+        }
+        if constexpr (NS > 3) {
+            if (s + 3 < KB) step(s + 3, std::integral_constant<int, 3 % NS>{});
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[1][1][r] = fmaf(Ip[r], Sp[r], acc[1][1][r]);
+
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = n0 + wcol0 + b * 32;
+            if (n >= N) continue;
+            float bias = 0.0f;
+            if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID) bias = epi.bias[n];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m >= M) continue;
+                float v = acc[a][b][r];
+                if (EPI == EPI_BIAS) {
+                    v = v + bias;
+                } else if (EPI == EPI_BIAS_GELU) {
+                    v = gelu_tanh(v + bias);
+                } else if (EPI == EPI_BIAS_RESID) {
+                    const int64_t rm = epi.resid_rows > 0 ? (int64_t)m % epi.resid_rows : (int64_t)m;
+                    v = (v + bias) + epi.resid[rm * epi.ld_resid + n];
+                }
+                y[(int64_t)m * ldy + n] = v;
+            }
+        }
+}
+
+template <class C, int EPI>
+hipError_t run(const WeightView &w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+               int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    const int m_tiles = (int)((M + C::BM - 1) / C::BM), n_tiles = (int)((w.N + BN - 1) / BN);
+    auto kern = k_mmq16<C, EPI>;
+    static bool attr_set = false;  // idempotent; a racing second call repeats it harmlessly
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 C::LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(m_tiles * n_tiles), dim3(C::NT), C::LDS, stream, xh, xdT,
+                       ld_dx, w.qh, w.dT, w.ldT, (int)M, (int)w.N, (int)(w.K_pad / QK), y, ldy,
+                       epi);
+    return hipGetLastError();
+}
+
+template <class C>
+hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+                    int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    switch (epi.kind) {
+    case EPI_NONE: return run<C, EPI_NONE>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    case EPI_BIAS: return run<C, EPI_BIAS>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    case EPI_BIAS_GELU: return run<C, EPI_BIAS_GELU>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    case EPI_BIAS_RESID: return run<C, EPI_BIAS_RESID>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mmq16
+
+hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
+                          int64_t ld_dx, int64_t M, float *y, int64_t ldy,
+                          const EpiParams &epi, hipStream_t stream) {
+    if (M == 0 || w.N == 0) return hipSuccess;
+    if (!w.qh || !w.dT || !xh || !xdT || ld_dx < mmq16_ld_dx(M) || (ld_dx & 7) ||
+        w.ldT < mmq16_ld_dw(w.N) || (w.ldT & 7) || (w.K_pad % QK) || w.K_pad == 0)
+        return hipErrorInvalidValue;
+    return mmq16::dispatch<mmq16::Cfg<128, 3>>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+}
+
+}  // namespace s2x

@@ -26,9 +26,18 @@ __device__ __forceinline__ void store_q4(int8_t *qs, _Float16 *qh, int64_t off, 
     }
 }
 
+// The block's scale words: d | s << 16 in ds [row][KB] and d alone in the
+// transposed plane dT [kb][row].
+__device__ __forceinline__ void store_scales(const Q81Out &o, int64_t row, int64_t kb, int64_t KB,
+                                             float d, int s) {
+    const uint32_t dbits = f32_to_f16_bits(d);
+    if (o.ds) o.ds[row * KB + kb] = dbits | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
+    if (o.dT) o.dT[kb * o.ldT + row] = (uint16_t)dbits;
+}
+
 __global__ __launch_bounds__(256) void k_quantize_q8_1(
-    const float *__restrict__ x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
-    int8_t *__restrict__ qs, _Float16 *__restrict__ qh, uint32_t *__restrict__ ds, int vec4) {
+    const float *__restrict__ x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad, Q81Out o,
+    int vec4) {
     const int64_t KB = K_pad / QK;
     const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
     const int sub = threadIdx.x & 7;
@@ -53,41 +62,43 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;
     const int q0 = q8_round(v0, inv), q1 = q8_round(v1, inv);
     const int q2 = q8_round(v2, inv), q3 = q8_round(v3, inv);
-    store_q4(qs, qh, m * K_pad + c, q0, q1, q2, q3);
+    store_q4(o.qs, o.qh, m * K_pad + c, q0, q1, q2, q3);
     const int s = group_isum<8>(q0 + q1 + q2 + q3);
-    if (sub == 0) {
-        ds[g] = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
-    }
+    if (sub == 0) store_scales(o, m, kb, KB, d, s);
 }
 
 hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
-                                int64_t K_pad, int8_t *qs, _Float16 *qh, uint32_t *ds,
-                                hipStream_t stream) {
+                                int64_t K_pad, const Q81Out &o, hipStream_t stream) {
     const int64_t groups = M * (K_pad / QK);
     if (groups == 0) return hipSuccess;
     const int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     const int64_t threads = groups * 8;
     const unsigned grid = (unsigned)((threads + 255) / 256);
     hipLaunchKernelGGL(k_quantize_q8_1, dim3(grid), dim3(256), 0, stream, x, K, M, ldx,
-                       K_pad, qs, qh, ds, vec4);
+                       K_pad, o, vec4);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // a2: weight repack.  One thread per 34-byte block: the int8 qs go to a
 // 16-byte aligned row-major plane, d widens (exactly) to f32; optionally the
-// same quants as f16 (exact) and d's fp16 bits for the f16-MFMA GEMM.
+// same quants as f16 (exact) and d's fp16 bits transposed ([kb][n]) for the
+// f16-MFMA GEMM.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__ raw,
-                                                     int64_t n_blocks, int8_t *__restrict__ qs,
+                                                     int64_t n_blocks, int64_t KB,
+                                                     int8_t *__restrict__ qs,
                                                      float *__restrict__ d,
                                                      _Float16 *__restrict__ qh,
-                                                     uint16_t *__restrict__ dh) {
+                                                     uint16_t *__restrict__ dT, int64_t ldT) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_blocks) return;
     const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + i * 34);  // 2-byte aligned
     d[i] = f16_bits_to_f32(src[0]);
-    if (dh) dh[i] = src[0];
+    if (dT) {
+        const int64_t n = i / KB, kb = i - n * KB;
+        dT[kb * ldT + n] = src[0];
+    }
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = (uint32_t)src[1 + 2 * j] | ((uint32_t)src[2 + 2 * j] << 16);
@@ -108,11 +119,13 @@ __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__
 }
 
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
-                              float *d, _Float16 *qh, uint16_t *dh, hipStream_t stream) {
+                              float *d, _Float16 *qh, uint16_t *dT, int64_t ldT,
+                              hipStream_t stream) {
     const int64_t nb = N * (K_pad / QK);
     if (nb == 0) return hipSuccess;
     hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
-                       stream, reinterpret_cast<const uint8_t *>(raw), nb, qs, d, qh, dh);
+                       stream, reinterpret_cast<const uint8_t *>(raw), nb, K_pad / QK, qs, d,
+                       qh, dT, ldT);
     return hipGetLastError();
 }
 
@@ -128,8 +141,7 @@ constexpr int LN_MAXIT = 8;  // H <= 8 * 256
 template <bool QUANT, bool WRITE_Y>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
-    const float *__restrict__ w, const float *__restrict__ b, float eps,
-    int8_t *__restrict__ qs, _Float16 *__restrict__ qh, uint32_t *__restrict__ ds,
+    const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
     float *__restrict__ y, int64_t ldy, int vec4) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -200,35 +212,32 @@ __global__ __launch_bounds__(256) void k_layernorm(
             const float inv = a != 0.0f ? 127.0f / a : 0.0f;
             const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
             const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
-            store_q4(qs, qh, row * H + c, q0, q1, q2, q3);
+            store_q4(q.qs, q.qh, row * H + c, q0, q1, q2, q3);
             const int sq = group_isum<8>(q0 + q1 + q2 + q3);
-            if ((lane & 7) == 0) {
-                ds[row * (H / QK) + c / QK] = (uint32_t)f32_to_f16_bits(d) |
-                                              ((uint32_t)f32_to_f16_bits((float)sq * d) << 16);
-            }
+            if ((lane & 7) == 0) store_scales(q, row, c / QK, H / QK, d, sq);
         }
     }
 }
 
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
-                            const float *w, const float *b, float eps, int8_t *qs,
-                            _Float16 *qh, uint32_t *ds, float *y, int64_t ldy,
-                            hipStream_t stream) {
+                            const float *w, const float *b, float eps, const Q81Out *q,
+                            float *y, int64_t ldy, hipStream_t stream) {
     if (M == 0) return hipSuccess;
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
     const dim3 grid((unsigned)((M + 3) / 4));
-    const bool quant = qs != nullptr || qh != nullptr;
+    const bool quant = q != nullptr;
+    const Q81Out qo = q ? *q : Q81Out{};
     const bool wy = y != nullptr;
     if (quant && wy)
         hipLaunchKernelGGL((k_layernorm<true, true>), grid, dim3(256), 0, stream, x, H, M, ldx,
-                           w, b, eps, qs, qh, ds, y, ldy, vec4);
+                           w, b, eps, qo, y, ldy, vec4);
     else if (quant)
         hipLaunchKernelGGL((k_layernorm<true, false>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qs, qh, ds, y, ldy, vec4);
+                           ldx, w, b, eps, qo, y, ldy, vec4);
     else
         hipLaunchKernelGGL((k_layernorm<false, true>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qs, qh, ds, y, ldy, vec4);
+                           ldx, w, b, eps, qo, y, ldy, vec4);
     return hipGetLastError();
 }
 

@@ -181,6 +181,25 @@ def test_gemm_large_m_batch_invariant(orc, gemm_data):
     assert np.array_equal(orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd), yg[rows])
 
 
+def test_drop_in_large_m(orc, gemm_data):
+    # batch-32 row count through the drop-in (f16-MFMA) GEMM: partial last
+    # row tile (23328 = 91 * 256 + 32) and column tile (4304 = 33 * 128 + 80)
+    raw, N, K, K_pad = gemm_data["fc1"]
+    M = 23328
+    say("drop-in fc1 M=23328")
+    x = np.random.default_rng(8).standard_normal((M, K)).astype(np.float32)
+    wd, xd = dev(raw), dev(x)
+    y = empty((M, N), torch.float32)
+    ws_bytes = s2x.lib.s2x_mul_mat_workspace_size(K_pad, N, M)
+    ws = empty((ws_bytes,), torch.uint8)
+    s2x.call("s2x_mul_mat_q8_0_f32", ptr(wd), K_pad, N, ptr(xd), K, K, M, ptr(y), ptr(ws),
+             ctypes.c_size_t(ws_bytes), stream())
+    yg = host(y)
+    rows = np.concatenate([np.arange(M - 40, M), np.random.default_rng(9).choice(M - 40, 40,
+                                                                                   replace=False)])
+    assert_same(yg[rows], orc.mul_mat_q8_0_f32(raw, K_pad, N, x[rows]), "drop-in M=23328")
+
+
 @pytest.mark.parametrize("label", [s[0] for s in SHAPES])
 def test_drop_in_mul_mat_f32(orc, gemm_data, label):
     # the drop-in op runs the f16-MFMA GEMM; rows 0-7 carry tiny values so
