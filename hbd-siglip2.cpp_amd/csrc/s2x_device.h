@@ -134,12 +134,16 @@ __device__ __forceinline__ float tanh_f32(float u) {
     return __builtin_copysignf(r, u);
 }
 
-// GELU tanh form, same expression and operation order as the reference's
-// fused epilogue (src/cuda/siglip2_megakernel.cu:276-280), with tanh_f32.
+// GELU tanh form: the reference's inner argument
+// (src/cuda/siglip2_megakernel.cu:276-280) through 0.5 x (1 + tanh(g)) =
+// x / (1 + e^(-2g)) -- one exp_cw, one IEEE division, no branch; the same
+// operations as the CPU restatement, so the bits agree.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
-    return 0.5f * x * (1.0f + tanh_f32(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+    const float g = SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x);
+    const float t = fminf(fmaxf(-2.0f * g, -100.0f), 100.0f);
+    return x / (1.0f + exp_cw(t));
 }
 
 // Output tile order: XCD-aware (gfx950 dispatches workgroup i to XCD i % 8,

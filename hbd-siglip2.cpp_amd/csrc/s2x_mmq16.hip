@@ -49,10 +49,11 @@ constexpr int ROWB = QK * 2;  // one block of f16 quants per row and stage
 constexpr int GM = 8;         // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-template <int BM_, int NS_>
+template <int BM_, int NS_, bool PIPE_, int TM_ = 2>
 struct Cfg {
-    static constexpr int BM = BM_, NS = NS_;
-    static constexpr int WGM = BM / 64;                 // waves along M (2 along N)
+    static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
+    static constexpr bool PIPE = PIPE_;
+    static constexpr int WGM = BM / (32 * TM);          // waves along M (2 along N)
     static constexpr int NT = WGM * 2 * WAVE;
     static constexpr int XI = BM * 4 / NT;              // X DMA instructions per stage
     static constexpr int WI = BN * 4 / NT;              // W DMA instructions per stage
@@ -62,15 +63,16 @@ struct Cfg {
     static constexpr int Z_OFF = DW_OFF + BN * 2;       // 16 zero bytes
     static constexpr int STAGE = Z_OFF + 16;
     static constexpr int LDS = NS * STAGE;
-    static_assert(BM % 64 == 0 && XI >= 1 && WI >= 1 && BM / 8 <= WAVE && BN / 8 <= WAVE, "config");
+    static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && XI >= 1 && WI >= 1 && BM / 8 <= WAVE && BN / 8 <= WAVE, "config");
     static_assert(NS >= 2 && NS <= 4, "wait table / unroll");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+template <int TM>
 struct Frag {
-    v8h a[2][2], b[2][2];   // [subtile][k half]
-    uint32_t dx[2], dw[2];  // fp16 bits of the row / column scales (0 on lanes 32..63)
+    v8h a[TM][2], b[2][2];   // [subtile][k half]
+    uint32_t dx[TM], dw[2];  // fp16 bits of the row / column scales (0 on lanes 32..63)
 };
 
 // 16 bytes per lane from buffer r at voffset + soffset into LDS at
@@ -117,7 +119,8 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
     const _Float16 *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
     const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
     int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
-    constexpr int BM = C::BM, NS = C::NS, NT = C::NT;
+    constexpr int BM = C::BM, NS = C::NS, NT = C::NT, TM = C::TM;
+    using Frag = mmq16::Frag<TM>;
     extern __shared__ __align__(16) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -179,9 +182,9 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
     // the zero words read by lanes 32..63 for the scale operands
     if (tid < NS) *reinterpret_cast<v4i *>(lds + tid * C::STAGE + C::Z_OFF) = v4i{0, 0, 0, 0};
 
-    float acc[2][2][16];
+    float acc[TM][2][16];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -190,22 +193,22 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
     const int lr = lane & 31, lh = lane >> 5;
     const int sw = (lr >> 2) & 3;  // chunk permutation of the rows this lane reads
     const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
-    const int xrow0 = wm * 64 + lr, wcol0 = wn * 64 + lr;
+    const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 64 + lr;
     const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
     // scale operands: k slot 0 (lanes 0..31) holds the scale, the rest zeros
     const int dxo0 = lh ? C::Z_OFF : C::DX_OFF + xrow0 * 2;
-    const int dxo1 = lh ? C::Z_OFF : C::DX_OFF + (xrow0 + 32) * 2;
+    const int dxo1 = lh ? C::Z_OFF : C::DX_OFF + (xrow0 + 32 * (TM - 1)) * 2;
     const int dwo0 = lh ? C::Z_OFF : C::DW_OFF + wcol0 * 2;
     const int dwo1 = lh ? C::Z_OFF : C::DW_OFF + (wcol0 + 32) * 2;
 
     auto load_frag = [&](const uint8_t *sb, Frag &f) {
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
+        for (int a = 0; a < TM; ++a) {
             f.a[a][0] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c0);
             f.a[a][1] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c1);
         }
         f.dx[0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
-        f.dx[1] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
+        if constexpr (TM == 2) f.dx[1] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             f.b[b][0] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c0);
@@ -225,53 +228,101 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
     auto mma = [&](const Frag &f) {
         const v16f zero = {};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 2 * TM; ++k) {
             const int a = k >> 1, b = k & 1;
             v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][0], f.b[b][0], zero, 0, 0, 0);
             const v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                 __builtin_bit_cast(v8h, v4i{(int)f.dx[a], 0, 0, 0}),
                 __builtin_bit_cast(v8h, v4i{(int)f.dw[b], 0, 0, 0}), zero, 0, 0, 0);
             I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
-            const int pa = ((k + 3) & 3) >> 1, pb = (k + 3) & 1;
+            const int pk = (k + 2 * TM - 1) % (2 * TM), pa = pk >> 1, pb = pk & 1;
             if (k > 0 || pending) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf(Ip[r], Sp[r], acc[pa][pb][r]);
             }
             Ip = I;
             Sp = S;
+            // issue order: each MFMA followed by a third of the previous
+            // subtile's fmas, so a wave alone keeps the matrix pipe fed
+            if (k > 0 || pending) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
         }
         pending = true;
     };
 
-    // NS-1 blocks in flight; stage s+NS-1 refills the buffer of stage s-1.
-    // The stage loop is unrolled NS times so each LDS read's stage offset is
-    // an instruction immediate.
-    const int npro = min(NS - 1, KB);
-    for (int s = 0; s < npro; ++s) issue(s, s);
-    Frag F;
-    auto step = [&](int s, auto bufc) {
-        constexpr int buf = decltype(bufc)::value;
-        wait_stage<C>(scale_wave, min(NS - 2, KB - 1 - s));
-        block_sync_lds();
-        if (s + NS - 1 < KB) issue(s + NS - 1, (buf + NS - 1) % NS);
-        load_frag(lds + buf * C::STAGE, F);
-        mma(F);
-    };
-    for (int s = 0; s < KB; s += NS) {
-        step(s, std::integral_constant<int, 0>{});
-        if (s + 1 < KB) step(s + 1, std::integral_constant<int, 1 % NS>{});
-        if constexpr (NS > 2) {
-            if (s + 2 < KB) step(s + 2, std::integral_constant<int, 2 % NS>{});
+    if constexpr (!C::PIPE) {
+        // NS-1 blocks in flight; stage s+NS-1 refills the buffer of stage
+        // s-1.  The stage loop is unrolled NS times so each LDS read's stage
+        // offset is an instruction immediate.
+        const int npro = min(NS - 1, KB);
+        for (int s = 0; s < npro; ++s) issue(s, s);
+        Frag F;
+        auto step = [&](int s, auto bufc) {
+            constexpr int buf = decltype(bufc)::value;
+            wait_stage<C>(scale_wave, min(NS - 2, KB - 1 - s));
+            block_sync_lds();
+            if (s + NS - 1 < KB) issue(s + NS - 1, (buf + NS - 1) % NS);
+            load_frag(lds + buf * C::STAGE, F);
+            mma(F);
+        };
+        for (int s = 0; s < KB; s += NS) {
+            step(s, std::integral_constant<int, 0>{});
+            if (s + 1 < KB) step(s + 1, std::integral_constant<int, 1 % NS>{});
+            if constexpr (NS > 2) {
+                if (s + 2 < KB) step(s + 2, std::integral_constant<int, 2 % NS>{});
+            }
+            if constexpr (NS > 3) {
+                if (s + 3 < KB) step(s + 3, std::integral_constant<int, 3 % NS>{});
+            }
         }
-        if constexpr (NS > 3) {
-            if (s + 3 < KB) step(s + 3, std::integral_constant<int, 3 % NS>{});
+    } else {
+        // NS blocks in flight; block s+1's fragments are read from LDS while
+        // block s's are in the MFMAs, and block s+NS refills the buffer of s
+        // (read into registers during the previous step).  Unrolled 2*NS
+        // times: stage offsets are immediates and the fragment sets alternate.
+        const int npro = min(NS, KB);
+        for (int s = 0; s < npro; ++s) issue(s, s);
+        wait_stage<C>(scale_wave, npro - 1);
+        block_sync_lds();
+        Frag F0, F1;
+        load_frag(lds, F0);
+        auto step = [&](int s, auto bufc, Frag &cur, Frag &nxt) {
+            constexpr int buf = decltype(bufc)::value;  // buffer of block s
+            if (s + 1 < KB) {
+                wait_stage<C>(scale_wave, min(NS - 2, KB - 2 - s));
+                block_sync_lds();
+                load_frag(lds + ((buf + 1) % NS) * C::STAGE, nxt);
+                if (s + NS < KB) issue(s + NS, buf);
+            }
+            mma(cur);
+        };
+        static_assert(NS == 2 || NS == 3 || NS == 4, "unroll");
+        for (int s = 0; s < KB; s += 2 * NS) {
+            step(s, std::integral_constant<int, 0>{}, F0, F1);
+            if (s + 1 < KB) step(s + 1, std::integral_constant<int, 1 % NS>{}, F1, F0);
+            if (s + 2 < KB) step(s + 2, std::integral_constant<int, 2 % NS>{}, F0, F1);
+            if (s + 3 < KB) step(s + 3, std::integral_constant<int, 3 % NS>{}, F1, F0);
+            if constexpr (NS > 2) {
+                if (s + 4 < KB) step(s + 4, std::integral_constant<int, 4 % NS>{}, F0, F1);
+                if (s + 5 < KB) step(s + 5, std::integral_constant<int, 5 % NS>{}, F1, F0);
+            }
+            if constexpr (NS > 3) {
+                if (s + 6 < KB) step(s + 6, std::integral_constant<int, 6 % NS>{}, F0, F1);
+                if (s + 7 < KB) step(s + 7, std::integral_constant<int, 7 % NS>{}, F1, F0);
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[1][1][r] = fmaf(Ip[r], Sp[r], acc[1][1][r]);
+    for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
 
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int n = n0 + wcol0 + b * 32;
@@ -280,7 +331,7 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
             if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID) bias = epi.bias[n];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (m >= M) continue;
                 float v = acc[a][b][r];
                 if (EPI == EPI_BIAS) {
@@ -336,7 +387,7 @@ hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_
     if (!w.qh || !w.dT || !xh || !xdT || ld_dx < mmq16_ld_dx(M) || (ld_dx & 7) ||
         w.ldT < mmq16_ld_dw(w.N) || (w.ldT & 7) || (w.K_pad % QK) || w.K_pad == 0)
         return hipErrorInvalidValue;
-    return mmq16::dispatch<mmq16::Cfg<128, 3>>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    return mmq16::dispatch<mmq16::Cfg<128, 3, false, 1>>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
 }
 
 }  // namespace s2x

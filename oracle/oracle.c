@@ -326,7 +326,9 @@ float orc_tanh_f32(float u) {
 float orc_gelu(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
-    return 0.5f * x * (1.0f + orc_tanh_f32(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+    const float g = SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x);
+    const float t = fminf(fmaxf(-2.0f * g, -100.0f), 100.0f);
+    return x / (1.0f + exp_cw(t));
 }
 
 /* ------------------------------------------------------------------------ */

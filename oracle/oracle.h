@@ -107,10 +107,13 @@ void orc_layernorm(const float *x, int64_t M, int64_t H, int64_t ldx,
  * running these operations in this order gets the same bits. */
 float orc_tanh_f32(float u);
 
-/* GELU tanh form, src/cuda/siglip2_megakernel.cu:276-280 (expression and
- * operation order), with orc_tanh_f32 for tanh.  ggml's CPU path instead
- * looks GELU up in an fp16 table [ggml, not in tree]; this restatement keeps
- * the f32 formula the reference's CUDA epilogue uses. */
+/* GELU tanh form of src/cuda/siglip2_megakernel.cu:276-280 with the same
+ * inner argument g = sqrt(2/pi) * x * (1 + 0.044715 x^2), evaluated through
+ * the identity 0.5 * x * (1 + tanh(g)) = x / (1 + e^(-2g)): one exp (the
+ * Cody-Waite exp of orc_tanh_f32, argument clamped to +-100) and one IEEE
+ * division, no branch.  ggml's CPU path instead looks GELU up in an fp16
+ * table [ggml, not in tree]; this restatement keeps the f32 formula the
+ * reference's CUDA epilogue uses. */
 float orc_gelu(float x);
 
 /* ---- attention ------------------------------------------------------------ */
