@@ -94,6 +94,38 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     }
 }
 
+__global__ __launch_bounds__(256) void k_rowmap(const int32_t *__restrict__ seg_start,
+                                                const int32_t *__restrict__ seg_len,
+                                                int32_t *__restrict__ rowmap) {
+    const int sg = blockIdx.y;
+    const int pos = blockIdx.x * 256 + threadIdx.x;
+    if (pos < seg_len[sg]) rowmap[seg_start[sg] + pos] = (sg << 16) | pos;
+}
+
+hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
+                         int64_t max_len, int32_t *rowmap, hipStream_t stream) {
+    if (n_seg == 0 || max_len == 0) return hipSuccess;
+    if (n_seg > 32767 || max_len > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rowmap, dim3((unsigned)((max_len + 255) / 256), (unsigned)n_seg),
+                       dim3(256), 0, stream, seg_start, seg_len, rowmap);
+    return hipGetLastError();
+}
+
+EpiParams epi_qkv(const AttnLayout &L, void *ws, const float *qkv_bias, const int32_t *rowmap) {
+    uint8_t *base = reinterpret_cast<uint8_t *>(ws);
+    EpiParams p{EPI_QKV, qkv_bias, nullptr, 0, 0, 0};
+    p.q = reinterpret_cast<_Float16 *>(base + L.q_off);
+    p.k = reinterpret_cast<_Float16 *>(base + L.k_off);
+    p.vt = reinterpret_cast<_Float16 *>(base + L.vt_off);
+    p.rowmap = rowmap;
+    p.n_head = (int)L.n_head;
+    p.d_head = (int)L.d_head;
+    p.d_pad = (int)L.d_pad;
+    p.dv_pad = (int)L.dv_pad;
+    p.len_pad = (int)L.len_pad;
+    return p;
+}
+
 hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                             const int32_t *seg_start, const int32_t *seg_len,
                             const AttnLayout &L, void *ws, hipStream_t stream) {
@@ -173,7 +205,20 @@ __global__ __launch_bounds__(256) void k_attn(
         for (int i = 0; i < 3; ++i) {
             const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
             const int r = c >> 3, cc = (c & 7) * 8;
-            vr[i] = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
+            uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
+            // keys past the segment hold zeros or stale finite data; zero them
+            // so a stale NaN/Inf can never meet a zero probability
+            const int valid = len - (k0 + cc);
+            if (valid < 8) {
+                uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t keep = (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
+                    w[j] &= keep;
+                }
+                v = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+            vr[i] = v;
         }
     };
     auto sstore = [&](int buf) {

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <utility>
@@ -182,7 +183,7 @@ struct Tower {
     float eps = 1e-6f;
     std::vector<DevLayer> layers;
     hipStream_t own = nullptr, stream = nullptr;
-    DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid;
+    DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid, rowmap;
     GemmTiming timing;
     // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
     bool attn_f64 = false;
@@ -286,6 +287,21 @@ struct Tower {
         S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
         S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
         S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
+        S2X_TRY(ensure(rowmap, sizeof(int32_t) * (size_t)M, stream));
+        return S2X_OK;
+    }
+
+    // The attention workspace's padding slots (d_head..d_pad of Q / K rows)
+    // must hold zeros; the QKV GEMM epilogue writes real slots only, so the
+    // workspace is cleared whenever its layout or address changes.
+    void *attn_zeroed_at = nullptr;
+    int64_t attn_zeroed_key[3] = {-1, -1, -1};
+    int attn_ws_ready(const AttnLayout &AL) {
+        const int64_t key[3] = {AL.n_seg, AL.len_pad, AL.n_head};
+        if (attn_zeroed_at == attn_ws.p && std::equal(key, key + 3, attn_zeroed_key)) return S2X_OK;
+        S2X_HIP_TRY(hipMemsetAsync(attn_ws.p, 0, AL.bytes, stream));
+        attn_zeroed_at = attn_ws.p;
+        std::copy(key, key + 3, attn_zeroed_key);
         return S2X_OK;
     }
 
@@ -298,13 +314,19 @@ struct Tower {
         std::vector<int32_t> tab(2 * n);
         std::memcpy(tab.data(), start.data(), n * 4);
         std::memcpy(tab.data() + n, len.data(), n * 4);
-        if (tab == seg_host && seg_dev_at == seg.p) return S2X_OK;
+        if (tab == seg_host && seg_dev_at == seg.p && rowmap_at == rowmap.p) return S2X_OK;
         S2X_HIP_TRY(hipMemcpyAsync(seg.p, tab.data(), 8 * n, hipMemcpyHostToDevice, stream));
         S2X_HIP_TRY(hipStreamSynchronize(stream));  // `tab` is pageable host memory
+        const int64_t max_len = n ? *std::max_element(len.begin(), len.end()) : 0;
+        hipError_t e = launch_rowmap(seg_start(), seg_len((int64_t)n), (int64_t)n, max_len,
+                                     rowmap.as<int32_t>(), stream);
+        if (e != hipSuccess) return hip_fail(e, "rowmap launch");
         seg_host = std::move(tab);
         seg_dev_at = seg.p;
+        rowmap_at = rowmap.p;
         return S2X_OK;
     }
+    void *rowmap_at = nullptr;
     const int32_t *seg_start() const { return seg.as<int32_t>(); }
     const int32_t *seg_len(int64_t n_seg) const { return seg.as<int32_t>() + n_seg; }
 
@@ -313,10 +335,27 @@ struct Tower {
         const AttnLayout AL = attn_layout(n_seg, max_len, n_head, d_head);
         const float kq_scale = 1.0f / std::sqrt((float)d_head);
         float *xp = x.as<float>();
+        // f16 GEMM + flash attention: the QKV GEMM writes the attention
+        // operands itself (EPI_QKV); otherwise f32 rows and a staging pass
+        const bool fused_qkv = gemm_f16 && !attn_f64;
+        if (fused_qkv) S2X_TRY(attn_ws_ready(AL));
         for (auto &L : layers) {
             S2X_TRY(layernorm_q(xp, M, L.ln1_w, L.ln1_b, nullptr));
-            S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
             hipError_t e;
+            if (fused_qkv) {
+                S2X_TRY(gemm(L.qkv, M, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rowmap.as<int32_t>()), H));
+                e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
+                                att.as<float>(), H, stream);
+                if (e != hipSuccess) return hip_fail(e, "attn launch");
+                S2X_TRY(quantize(att.as<float>(), H, M, H, H));
+                S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
+                S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
+                S2X_TRY(gemm(L.up, M, u.as<float>(), F, EpiParams{EPI_BIAS_GELU, L.up_b, nullptr, 0, 0, 0}, H));
+                S2X_TRY(quantize(u.as<float>(), F, M, F, F_pad));
+                S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F));
+                continue;
+            }
+            S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
             if (attn_f64) {
                 e = launch_attn_f64(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
                                     key_valid, n_seg, max_len, n_head, d_head, kq_scale,

@@ -39,7 +39,10 @@ struct Q81Out {
     int64_t   ldT = 0;
 };
 
-enum EpiKind { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4 };
+enum EpiKind {
+    EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4,
+    EPI_QKV = 5,  // f16 GEMM only: (mm + bias) -> f16 Q / K / V^T in the attention layout
+};
 
 struct EpiParams {
     int          kind;
@@ -48,6 +51,11 @@ struct EpiParams {
     int64_t      ld_resid;
     int64_t      resid_rows;  // 0: row m; >0: row m % resid_rows
     int64_t      dump_kb;     // EPI_DUMP_I: the block whose int32 dot is written
+    // EPI_QKV: output columns [q | k | v] (n_head x d_head each); row m is
+    // position rowmap[m] & 0xffff of segment rowmap[m] >> 16
+    _Float16      *q, *k, *vt;
+    const int32_t *rowmap;
+    int            n_head, d_head, d_pad, dv_pad, len_pad;
 };
 
 // a1: F32 -> Q8_1 into the planes of `out`.
@@ -100,6 +108,11 @@ AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d
 hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                             const int32_t *seg_start, const int32_t *seg_len,
                             const AttnLayout &L, void *ws, hipStream_t stream);
+// Row -> (segment << 16 | position) table of packed segments, for EPI_QKV.
+hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
+                         int64_t max_len, int32_t *rowmap, hipStream_t stream);
+// EPI_QKV destination planes of layout L in workspace ws.
+EpiParams epi_qkv(const AttnLayout &L, void *ws, const float *qkv_bias, const int32_t *rowmap);
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
                        const uint8_t *key_valid, const AttnLayout &L, float scale,
                        float *out, int64_t ld_out, hipStream_t stream);

@@ -321,6 +321,35 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
 
+    if constexpr (EPI == EPI_QKV) {
+        // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad] or
+        // V^T [seg][head][dv_pad][pos]; padding slots are not written
+        const int H = epi.n_head * epi.d_head;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = n0 + wcol0 + b * 32;
+            if (n >= N) continue;
+            const float bias = epi.bias[n];
+            const int part = n / H, hd = n - part * H;
+            const int h = hd / epi.d_head, d = hd - h * epi.d_head;
+            _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    if (m >= M) continue;
+                    const int rm = epi.rowmap[m];
+                    const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                    const int pos = rm & 0xffff;
+                    const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
+                                                 : (sh * epi.dv_pad + d) * epi.len_pad + pos;
+                    dst[off] = f32_to_f16(acc[a][b][r] + bias);
+                }
+        }
+        return;
+    }
+
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -374,6 +403,11 @@ hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT
     case EPI_BIAS: return run<C, EPI_BIAS>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_BIAS_GELU: return run<C, EPI_BIAS_GELU>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_BIAS_RESID: return run<C, EPI_BIAS_RESID>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    case EPI_QKV:
+        if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
+            epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head)
+            return hipErrorInvalidValue;
+        return run<C, EPI_QKV>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     default: return hipErrorInvalidValue;
     }
 }
