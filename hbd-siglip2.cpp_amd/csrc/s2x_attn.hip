@@ -190,101 +190,118 @@ __global__ __launch_bounds__(256) void k_attn(
 
     // global -> registers for one key tile: K 64x80 halves (10240 B contiguous),
     // V^T 96 rows x 64 halves (128 B each)
-    uint4 kr[3], vr[3];
+    struct Tile {
+        uint4 k0, k1, k2, v0, v1, v2;
+    };
+    // 640 K chunks of 16 B; threads past the end re-load the last chunk
+    // (always in bounds) and later rewrite it with the value it already has
+    const int kc0 = tid, kc1 = tid + 256, kc2 = min(tid + 512, FA_KT * FA_DP / 8 - 1);
+    auto vload = [&](int k0, int i) {
+        const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
+        const int r = c >> 3, cc = (c & 7) * 8;
+        uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
+        // keys past the segment hold zeros or stale finite data; zero them so
+        // a stale NaN/Inf can never meet a zero probability
+        const int valid = len - (k0 + cc);
+        if (valid < 8) {
+            const auto keep = [valid](int j) {
+                return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
+            };
+            v = make_uint4(v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3));
+        }
+        return v;
+    };
     auto gload = [&](int t) {
         const int k0 = t * FA_KT;
         const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            // 640 chunks of 16 B; threads past the end re-load the last chunk
-            // (always in bounds) so kr[] stays in registers
-            const int c = min(tid + i * 256, FA_KT * FA_DP / 8 - 1);
-            kr[i] = ks[c];
-        }
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
-            const int r = c >> 3, cc = (c & 7) * 8;
-            uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
-            // keys past the segment hold zeros or stale finite data; zero them
-            // so a stale NaN/Inf can never meet a zero probability
-            const int valid = len - (k0 + cc);
-            if (valid < 8) {
-                uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t keep = (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
-                    w[j] &= keep;
-                }
-                v = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-            vr[i] = v;
-        }
+        Tile g;
+        g.k0 = ks[kc0];
+        g.k1 = ks[kc1];
+        g.k2 = ks[kc2];
+        g.v0 = vload(k0, 0);
+        g.v1 = vload(k0, 1);
+        g.v2 = vload(k0, 2);
+        return g;
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](int buf, const Tile &g) {
         _Float16 *kl = lds + buf * FA_STAGE;
         _Float16 *vl = kl + FA_KT * FA_KP;
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            // same clamp as the load: past-the-end threads rewrite the last
-            // chunk with the value it already has
-            const int c = min(tid + i * 256, FA_KT * FA_DP / 8 - 1);
-            const int r = c / 10, cc = (c % 10) * 8;
-            *reinterpret_cast<uint4 *>(kl + r * FA_KP + cc) = kr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
+        const auto kput = [&](int c, uint4 v) {
+            *reinterpret_cast<uint4 *>(kl + (c / 10) * FA_KP + (c % 10) * 8) = v;
+        };
+        kput(kc0, g.k0);
+        kput(kc1, g.k1);
+        kput(kc2, g.k2);
+        const auto vput = [&](int i, uint4 v) {
             const int c = tid + i * 256;
-            const int r = c >> 3, cc = (c & 7) * 8;
-            uint2 *dst = reinterpret_cast<uint2 *>(vl + r * FA_VP + cc);  // 8-byte aligned
-            dst[0] = make_uint2(vr[i].x, vr[i].y);
-            dst[1] = make_uint2(vr[i].z, vr[i].w);
-        }
+            uint2 *dst = reinterpret_cast<uint2 *>(vl + (c >> 3) * FA_VP + (c & 7) * 8);  // 8-byte aligned
+            dst[0] = make_uint2(v.x, v.y);
+            dst[1] = make_uint2(v.z, v.w);
+        };
+        vput(0, g.v0);
+        vput(1, g.v1);
+        vput(2, g.v2);
     };
 
-    gload(0);
-    sstore(0);
+    sstore(0, gload(0));
     __syncthreads();
 
     for (int t = 0; t < n_tiles; ++t) {
         const int buf = t & 1;
-        if (t + 1 < n_tiles) gload(t + 1);
+        Tile nxt{};
+        if (t + 1 < n_tiles) nxt = gload(t + 1);
         const _Float16 *kl = lds + buf * FA_STAGE;
         const _Float16 *vl = kl + FA_KT * FA_KP;
+        // S^T for the tile's two 32-key halves (raw q.k, unscaled)
+        v16f sc[2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-            const int kbase = t * FA_KT + sub * 32;
-            // S^T (32 keys x 32 queries)
-            v16f s = {};
+            v16f acc = {};
 #pragma unroll
             for (int st = 0; st < 5; ++st) {
                 const v8h kf = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], acc, 0, 0, 0);
             }
-            // scale, mask, tile max
-            float mt = -INFINITY;
+            sc[sub] = acc;
+        }
+        // mask (only the tile holding the segment end, or a key mask), then
+        // the tile max; one softmax rescale per 64 keys
+        const int kbase = t * FA_KT;
+        if (kbase + FA_KT > len || key_valid) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kbase + 8 * (r >> 2) + 4 * lh + (r & 3);
-                bool ok = key < len;
-                if (key_valid) ok = ok && key_valid[row0 + min(key, len - 1)] != 0;
-                const float v = ok ? s[r] * scale_log2 : -INFINITY;
-                s[r] = v;
-                mt = fmaxf(mt, v);
-            }
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float m_new = fmaxf(m_run, mt);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-            m_run = m_new;
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbase + sub * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    bool ok = key < len;
+                    if (key_valid) ok = ok && key_valid[row0 + min(key, len - 1)] != 0;
+                    sc[sub][r] = ok ? sc[sub][r] : -INFINITY;
+                }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[sub][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt);  // in raw score units (scale > 0)
+        const float mc = m_new == -INFINITY ? 0.0f : m_new * scale_log2;
+        const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
+        m_run = m_new;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
+        float ps = 0.0f;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
             // P as f16 for the PV product; with P_SPLIT as an exact pair
             // p = hi + lo (hi = f16(p), lo = f16(p - hi); p - hi is exact in
             // f32), i.e. ~22 significant bits instead of 11.
-            float ps = 0.0f;
             v8h ph0, ph1, pl0, pl1;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
+                const float p = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
                 ps = ps + p;
                 const _Float16 hi = f32_to_f16(p);
                 if (r < 8) ph0[r] = hi; else ph1[r - 8] = hi;
@@ -293,11 +310,6 @@ __global__ __launch_bounds__(256) void k_attn(
                     if (r < 8) pl0[r] = lo; else pl1[r - 8] = lo;
                 }
             }
-            l_run = l_run * alpha + ps;
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
             // O^T += V^T P^T
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
@@ -313,7 +325,8 @@ __global__ __launch_bounds__(256) void k_attn(
                 }
             }
         }
-        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        l_run = l_run * alpha + ps;
+        if (t + 1 < n_tiles) sstore(buf ^ 1, nxt);
         __syncthreads();
     }
 
