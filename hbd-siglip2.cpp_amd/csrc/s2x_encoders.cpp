@@ -184,6 +184,7 @@ struct Tower {
     std::vector<DevLayer> layers;
     hipStream_t own = nullptr, stream = nullptr;
     DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid, rowmap;
+    DevBuf qs2, ds2;  // f16 GEMM: the fc1 epilogue's Q8_1 output (fc2 input)
     GemmTiming timing;
     // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
     bool attn_f64 = false;
@@ -228,14 +229,15 @@ struct Tower {
 
     // GEMM with optional event timing; k_logical excludes the K padding.
     int gemm(const s2x_weight *w, int64_t M, float *y, int64_t ldy, const EpiParams &e,
-             int64_t k_logical) {
+             int64_t k_logical, bool from_qs2 = false) {
         hipEvent_t a = nullptr, b = nullptr;
         if (timing.on) {
             a = timing.get();
             b = timing.get();
             S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, qs.as<_Float16>(), ds.as<uint16_t>(),
+        const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
+        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, xq.as<_Float16>(), xd.as<uint16_t>(),
                                                    mmq16_ld_dx(M), M, y, ldy, e, stream)
                                   : launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y,
                                                ldy, e, stream);
@@ -284,7 +286,11 @@ struct Tower {
         S2X_TRY(ensure(ds, ds_bytes(M, kmax), stream));
         S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
-        S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
+        if (gemm_f16) {
+            S2X_TRY(ensure(qs2, 2 * (size_t)(M * F_pad), stream));
+            S2X_TRY(ensure(ds2, 2 * (size_t)(mmq16_ld_dx(M) * (F_pad / QK_)), stream));
+        }
+        if (!gemm_f16 || attn_f64) S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
         S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
         S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
         S2X_TRY(ensure(rowmap, sizeof(int32_t) * (size_t)M, stream));
@@ -350,9 +356,14 @@ struct Tower {
                 S2X_TRY(quantize(att.as<float>(), H, M, H, H));
                 S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
                 S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
-                S2X_TRY(gemm(L.up, M, u.as<float>(), F, EpiParams{EPI_BIAS_GELU, L.up_b, nullptr, 0, 0, 0}, H));
-                S2X_TRY(quantize(u.as<float>(), F, M, F, F_pad));
-                S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F));
+                EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
+                up.q_out = qs2.as<_Float16>();
+                up.q_dT = ds2.as<uint16_t>();
+                up.q_kpad = F_pad;
+                up.q_ld = mmq16_ld_dx(M);
+                S2X_TRY(gemm(L.up, M, nullptr, 0, up, H));
+                S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F,
+                             true));
                 continue;
             }
             S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));

@@ -41,7 +41,8 @@ struct Q81Out {
 
 enum EpiKind {
     EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4,
-    EPI_QKV = 5,  // f16 GEMM only: (mm + bias) -> f16 Q / K / V^T in the attention layout
+    EPI_QKV = 5,       // f16 GEMM only: (mm + bias) -> f16 Q / K / V^T in the attention layout
+    EPI_GELU_Q81 = 6,  // f16 GEMM only: GELU(mm + bias) quantized to Q8_1 (f16 quants + d^T)
 };
 
 struct EpiParams {
@@ -56,6 +57,11 @@ struct EpiParams {
     _Float16      *q, *k, *vt;
     const int32_t *rowmap;
     int            n_head, d_head, d_pad, dv_pad, len_pad;
+    // EPI_GELU_Q81: quants [M][q_kpad] (columns N..q_kpad-1 quantize zeros)
+    // and transposed scales [q_kpad/32][q_ld]
+    _Float16 *q_out;
+    uint16_t *q_dT;
+    int64_t   q_kpad, q_ld;
 };
 
 // a1: F32 -> Q8_1 into the planes of `out`.

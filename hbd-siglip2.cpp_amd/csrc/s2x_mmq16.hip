@@ -54,7 +54,8 @@ struct Cfg {
     static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
     static constexpr bool PIPE = PIPE_;
     static constexpr int WGM = BM / (32 * TM);          // waves along M (2 along N)
-    static constexpr int NT = WGM * 2 * WAVE;
+    static constexpr int NWAVE = WGM * 2;
+    static constexpr int NT = NWAVE * WAVE;
     static constexpr int XI = BM * 4 / NT;              // X DMA instructions per stage
     static constexpr int WI = BN * 4 / NT;              // W DMA instructions per stage
     static constexpr int X_BYTES = BM * ROWB;
@@ -321,6 +322,55 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
 
+    if constexpr (EPI == EPI_GELU_Q81) {
+        // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over rows of
+        // q_kpad values (columns >= N are zeros).  A wave's 32 x 32 subtile is
+        // one quant block per row: it goes through LDS so that lane pairs own
+        // a row (16 values each); the stage buffers are free after a barrier.
+        constexpr int P = 36;  // floats per scratch row (16-byte aligned rows)
+        static_assert(C::NWAVE * 32 * P * 4 <= C::LDS, "epilogue scratch fits the stages");
+        __syncthreads();
+        float *scr = reinterpret_cast<float *>(lds) + wave * 32 * P;
+        const int row = lane >> 1, half = lane & 1;
+        const int m = m0 + wm * 32 + row;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int nb = n0 + wn * 64 + b * 32;  // first column of this quant block
+            if (nb >= epi.q_kpad) continue;        // wave-uniform
+            const int n = nb + lr;
+            const float bias = n < N ? epi.bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
+                    n < N ? gelu_tanh(acc[0][b][r] + bias) : 0.0f;
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4f t = *reinterpret_cast<const v4f *>(scr + row * P + half * 16 + 4 * j);
+                v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
+            }
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[j]));
+            a = fmaxf(a, __shfl_xor(a, 1));
+            const float d = a / 127.0f;
+            const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+            v8h q0, q1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                q0[j] = (_Float16)q8_round(v[j], inv);
+                q1[j] = (_Float16)q8_round(v[8 + j], inv);
+            }
+            if (m < M) {
+                v8h *dst = reinterpret_cast<v8h *>(epi.q_out + (int64_t)m * epi.q_kpad + nb + half * 16);
+                dst[0] = q0;
+                dst[1] = q1;
+                if (half == 0) epi.q_dT[(int64_t)(nb / QK) * epi.q_ld + m] = f32_to_f16_bits(d);
+            }
+        }
+        return;
+    }
+
     if constexpr (EPI == EPI_QKV) {
         // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad] or
         // V^T [seg][head][dv_pad][pos]; padding slots are not written
@@ -403,6 +453,12 @@ hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT
     case EPI_BIAS: return run<C, EPI_BIAS>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_BIAS_GELU: return run<C, EPI_BIAS_GELU>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_BIAS_RESID: return run<C, EPI_BIAS_RESID>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    case EPI_GELU_Q81:
+        if (C::TM != 1 || !epi.q_out || !epi.q_dT || !epi.bias || epi.q_kpad % QK ||
+            epi.q_kpad < w.N || epi.q_kpad - w.N >= QK || epi.q_ld < mmq16_ld_dx(M) ||
+            (reinterpret_cast<uintptr_t>(epi.q_out) & 15))
+            return hipErrorInvalidValue;
+        return run<C, EPI_GELU_Q81>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_QKV:
         if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
             epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head)
