@@ -31,6 +31,19 @@ KERNELS = {
 }
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mmq16_vision_b32_traffic.json")
+
+
+def traffic_per_launch(gemm):
+    """HBM bytes per GEMM launch of this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated on a copy kernel);
+    None when not measured for this kernel."""
+    if gemm != "f16" or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        return int(json.load(f)["bytes_per_launch"])
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -43,6 +56,9 @@ def main():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--cpu-images", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run one device-to-device copy of BYTES (a plain copy kernel "
+                         "for calibrating HBM byte counters) and exit")
     ap.add_argument("--gemm", choices=["f16", "i8"], default="f16",
                     help="GEMM kernel: f16-MFMA block dots + scale tile (default) or "
                          "int8-MFMA block dots with VALU rescale; same bits")
@@ -55,6 +71,16 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.copy_probe:
+        n = args.copy_probe // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
+        return
 
     import s2x
     from s2x import synth
@@ -148,7 +174,8 @@ def main():
                    "seq_len": n_pos, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+                     "traffic": traffic_per_launch(args.gemm),
                      "kernel": KERNELS[args.gemm],
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "launches": int(launches.value)},
