@@ -147,11 +147,17 @@ __global__ __launch_bounds__(256) void k_layernorm(
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const float *xr = x + row * ldx;
-    float v[LN_MAXIT][4];
-    double s = 0.0;
+    float v[LN_MAXIT][4], wv[LN_MAXIT][4], bv[LN_MAXIT][4];
+    // x, w and b all requested before any use: the row's loads overlap
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[it][j] = 0.0f;
+            wv[it][j] = 1.0f;
+            bv[it][j] = 0.0f;
+        }
         if (c < H) {
             if (vec4 & 1) {
                 const float4 t = *reinterpret_cast<const float4 *>(xr + c);
@@ -160,11 +166,29 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[it][j] = xr[c + j];
             }
-            s = s + (((double)v[it][0] + (double)v[it][1]) + ((double)v[it][2] + (double)v[it][3]));
-        } else {
+            if (vec4 & 4) {
+                if (w) {
+                    const float4 t = *reinterpret_cast<const float4 *>(w + c);
+                    wv[it][0] = t.x; wv[it][1] = t.y; wv[it][2] = t.z; wv[it][3] = t.w;
+                }
+                if (b) {
+                    const float4 t = *reinterpret_cast<const float4 *>(b + c);
+                    bv[it][0] = t.x; bv[it][1] = t.y; bv[it][2] = t.z; bv[it][3] = t.w;
+                }
+            } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
+                for (int j = 0; j < 4; ++j) {
+                    if (w) wv[it][j] = w[c + j];
+                    if (b) bv[it][j] = b[c + j];
+                }
+            }
         }
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int it = 0; it < LN_MAXIT; ++it) {
+        const int64_t c = (int64_t)it * 256 + lane * 4;
+        if (c < H) s = s + (((double)v[it][0] + (double)v[it][1]) + ((double)v[it][2] + (double)v[it][3]));
     }
     // sums in double, as ggml's CPU norm accumulates: the f32 mean and
     // variance then equal the CPU's (the double sum's rounding, whatever
@@ -192,8 +216,8 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float t = (v[it][j] - mean) * scale;
-            if (w) t = t * w[c + j];
-            if (b) t = t + b[c + j];
+            if (w) t = t * wv[it][j];
+            if (b) t = t + bv[it][j];
             o[j] = t;
         }
         if (WRITE_Y) {
@@ -225,6 +249,7 @@ hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
     if (M == 0) return hipSuccess;
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) vec4 |= 4;
     const dim3 grid((unsigned)((M + 3) / 4));
     const bool quant = q != nullptr;
     const Q81Out qo = q ? *q : Q81Out{};
