@@ -49,10 +49,11 @@ constexpr int ROWB = QK * 2;  // one block of f16 quants per row and stage
 constexpr int GM = 8;         // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-template <int BM_, int NS_, bool PIPE_, int TM_ = 2>
+template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true>
 struct Cfg {
     static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
-    static constexpr bool PIPE = PIPE_;
+    static constexpr bool PIPE = PIPE_;  // next block's fragments read during this block's MFMAs
+    static constexpr bool SKEW = SKEW_;  // a subtile's fmas issued after the next one's MFMAs
     static constexpr int WGM = BM / (32 * TM);          // waves along M (2 along N)
     static constexpr int NWAVE = WGM * 2;
     static constexpr int NT = NWAVE * WAVE;
@@ -71,7 +72,7 @@ struct Cfg {
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <int TM>
-struct Frag {
+struct FragTM {
     v8h a[TM][2], b[2][2];   // [subtile][k half]
     uint32_t dx[TM], dw[2];  // fp16 bits of the row / column scales (0 on lanes 32..63)
 };
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
     const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
     int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
     constexpr int BM = C::BM, NS = C::NS, NT = C::NT, TM = C::TM;
-    using Frag = mmq16::Frag<TM>;
+    using Frag = FragTM<TM>;
     extern __shared__ __align__(16) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -236,6 +237,11 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
                 __builtin_bit_cast(v8h, v4i{(int)f.dx[a], 0, 0, 0}),
                 __builtin_bit_cast(v8h, v4i{(int)f.dw[b], 0, 0, 0}), zero, 0, 0, 0);
             I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
+            if constexpr (!C::SKEW) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], S[r], acc[a][b][r]);
+                continue;
+            }
             const int pk = (k + 2 * TM - 1) % (2 * TM), pa = pk >> 1, pb = pk & 1;
             if (k > 0 || pending) {
 #pragma unroll
@@ -319,8 +325,10 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
             }
         }
     }
+    if constexpr (C::SKEW) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
+        for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
+    }
 
     if constexpr (EPI == EPI_GELU_Q81) {
         // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over rows of
@@ -375,6 +383,37 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
         // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad] or
         // V^T [seg][head][dv_pad][pos]; padding slots are not written
         const int H = epi.n_head * epi.d_head;
+        if (TM == 1 && n0 + BN <= 2 * H && H % BN == 0 && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
+            // a Q or K tile (the q|k|v boundaries fall on tile edges): the
+            // wave's 32 x 64 f16 tile goes through LDS so that each 8-column
+            // chunk of a row -- 8 consecutive d of one head -- leaves as one
+            // 16-byte store
+            constexpr int P = 72;  // halves per scratch row (16-byte aligned)
+            static_assert(C::NWAVE * 32 * P * 2 <= C::LDS, "epilogue scratch fits the stages");
+            __syncthreads();
+            _Float16 *scr = reinterpret_cast<_Float16 *>(lds) + wave * 32 * P;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int n = n0 + wcol0 + b * 32;
+                const float bias = n < N ? epi.bias[n] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] = f32_to_f16(acc[0][b][r] + bias);
+            }
+            _Float16 *dst0 = n0 < H ? epi.q : epi.k;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
+                const int m = m0 + wm * 32 + row, n = n0 + wn * 64 + c;
+                if (m >= M || n >= N) continue;
+                const int hd = n % H, h = hd / epi.d_head, d = hd - h * epi.d_head;
+                const int rm = epi.rowmap[m];
+                const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
+                *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
+            }
+            return;
+        }
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int n = n0 + wcol0 + b * 32;
