@@ -2,7 +2,7 @@
 patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
-                    [--cpu-images 1] [--no-cpu]
+                    [--cpu-images 3] [--no-cpu] [--gemm f16|i8]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
@@ -25,7 +25,7 @@ sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
 KERNELS = {
-    "f16": "k_mmq_f16 (Q8_0 x Q8_1 GEMM: exact int8-valued block dots and the dx*dw scale "
+    "f16": "k_mmq16 (Q8_0 x Q8_1 GEMM: exact int8-valued block dots and the dx*dw scale "
            "tile on v_mfma_f32_32x32x16_f16; priced against the int8 peak)",
     "i8": "k_mmq (Q8_0 x Q8_1 GEMM: v_mfma_i32_32x32x32_i8 block dots, VALU rescale)",
 }
@@ -54,7 +54,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=32)
-    ap.add_argument("--cpu-images", type=int, default=1)
+    ap.add_argument("--cpu-images", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (a plain copy kernel "
