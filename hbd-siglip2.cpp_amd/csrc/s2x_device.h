@@ -60,6 +60,51 @@ __device__ __forceinline__ float group_sum(float v) {
     for (int o = W / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, W);
     return v;
 }
+// DPP lane exchanges (VALU, no LDS round trip).  CTRL: quad_perm codes
+// 0x00-0xff, row_half_mirror 0x141 (lane i <-> 7 - i within 8), row_mirror
+// 0x140 (i <-> 15 - i within 16), row_bcast15 0x142 / row_bcast31 0x143
+// (last lane of the previous row / of lanes 0-31 into the rows of ROW_MASK).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL, ROW_MASK>(__builtin_bit_cast(int, v)));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = dpp_i<CTRL, ROW_MASK>((int)b), hi = dpp_i<CTRL, ROW_MASK>((int)(b >> 32));
+    return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+// max / sum over aligned groups of 8 lanes, result in every lane of the group
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int group8_isum(int v) {
+    v = v + dpp_i<0xb1>(v);
+    v = v + dpp_i<0x4e>(v);
+    return v + dpp_i<0x141>(v);
+}
+// Sum over the wave (64 lanes), returned wave-uniform.  The summation order
+// differs from a butterfly; a double sum of f32 terms is exact to ~1e-16
+// relative either way.
+__device__ __forceinline__ double wave_dsum(double v) {
+    v = v + dpp_d<0xb1>(v);
+    v = v + dpp_d<0x4e>(v);
+    v = v + dpp_d<0x141>(v);
+    v = v + dpp_d<0x140>(v);
+    v = v + dpp_d<0x142, 0xa>(v);
+    v = v + dpp_d<0x143, 0xc>(v);
+    const long long b = __builtin_bit_cast(long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, 63);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), 63);
+    return __builtin_bit_cast(double, (long long)(((unsigned long long)hi << 32) | lo));
+}
+
 template <int W>
 __device__ __forceinline__ double group_dsum(double v) {
 #pragma unroll

@@ -360,7 +360,7 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
             float a = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[j]));
-            a = fmaxf(a, __shfl_xor(a, 1));
+            a = fmaxf(a, dpp_f<0xb1>(a));  // partner lane (xor 1)
             const float d = a / 127.0f;
             const float inv = a != 0.0f ? 127.0f / a : 0.0f;
             v8h q0, q1;

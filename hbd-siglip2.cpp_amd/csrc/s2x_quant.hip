@@ -57,13 +57,13 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
         v3 = c + 3 < K ? xr[c + 3] : 0.0f;
     }
     float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-    a = group_max<8>(a);
+    a = group8_max(a);
     const float d = a / 127.0f;
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;
     const int q0 = q8_round(v0, inv), q1 = q8_round(v1, inv);
     const int q2 = q8_round(v2, inv), q3 = q8_round(v3, inv);
     store_q4(o.qs, o.qh, m * K_pad + c, q0, q1, q2, q3);
-    const int s = group_isum<8>(q0 + q1 + q2 + q3);
+    const int s = group8_isum(q0 + q1 + q2 + q3);
     if (sub == 0) store_scales(o, m, kb, KB, d, s);
 }
 
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
     // sums in double, as ggml's CPU norm accumulates: the f32 mean and
     // variance then equal the CPU's (the double sum's rounding, whatever
     // its order, is ~1e-16 relative and vanishes in the f32 conversion)
-    const float mean = (float)(group_dsum<64>(s) / (double)H);
+    const float mean = (float)(wave_dsum(s) / (double)H);
     double s2 = 0.0;
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
             }
         }
     }
-    const float var = (float)(group_dsum<64>(s2) / (double)H);
+    const float var = (float)(wave_dsum(s2) / (double)H);
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int it = 0; it < LN_MAXIT; ++it) {
@@ -231,13 +231,13 @@ __global__ __launch_bounds__(256) void k_layernorm(
         }
         if (QUANT) {
             float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-            a = group_max<8>(a);
+            a = group8_max(a);
             const float d = a / 127.0f;
             const float inv = a != 0.0f ? 127.0f / a : 0.0f;
             const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
             const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
             store_q4(q.qs, q.qh, row * H + c, q0, q1, q2, q3);
-            const int sq = group_isum<8>(q0 + q1 + q2 + q3);
+            const int sq = group8_isum(q0 + q1 + q2 + q3);
             if ((lane & 7) == 0) store_scales(q, row, c / QK, H / QK, d, sq);
         }
     }
