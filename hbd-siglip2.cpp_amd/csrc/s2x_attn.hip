@@ -24,6 +24,8 @@
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
+#include <type_traits>
+
 namespace s2x {
 
 static inline int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
@@ -246,7 +248,9 @@ __global__ __launch_bounds__(256) void k_attn(
     sstore(0, gload(0));
     __syncthreads();
 
-    for (int t = 0; t < n_tiles; ++t) {
+    // one 64-key tile; MASK: the tile holding the segment end, or a key mask
+    auto tile = [&](int t, auto maskc) {
+        constexpr bool MASK = decltype(maskc)::value;
         const int buf = t & 1;
         Tile nxt{};
         if (t + 1 < n_tiles) nxt = gload(t + 1);
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(256) void k_attn(
         // mask (only the tile holding the segment end, or a key mask), then
         // the tile max; one softmax rescale per 64 keys
         const int kbase = t * FA_KT;
-        if (kbase + FA_KT > len || key_valid) {
+        if constexpr (MASK) {
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -288,26 +292,39 @@ __global__ __launch_bounds__(256) void k_attn(
         const float mc = m_new == -INFINITY ? 0.0f : m_new * scale_log2;
         const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
         m_run = m_new;
+        // alpha is exactly 1 where the running max did not move: skip the
+        // rescale when that holds for the whole wave (the common case once
+        // the first tiles have set the max)
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j)
+            for (int j = 0; j < 3; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
+                for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
+        }
         float ps = 0.0f;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-            // P as f16 for the PV product; with P_SPLIT as an exact pair
-            // p = hi + lo (hi = f16(p), lo = f16(p - hi); p - hi is exact in
-            // f32), i.e. ~22 significant bits instead of 11.
-            v8h ph0, ph1, pl0, pl1;
+            // P as f16 for the PV product; with P_SPLIT as a pair p ~ hi + lo
+            // (hi = f16(p), lo = f16(p - hi), p - hi exact in f32): ~22
+            // significant bits instead of 11.  Pairs of values convert in
+            // one v_cvt_pkrtz_f16_f32; truncation of hi is harmless since lo
+            // carries the remainder.
+            float pv[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
-                ps = ps + p;
-                const _Float16 hi = f32_to_f16(p);
-                if (r < 8) ph0[r] = hi; else ph1[r - 8] = hi;
+                pv[r] = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
+                ps = ps + pv[r];
+            }
+            v8h ph0, ph1, pl0, pl1;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[r], pv[r + 1]);
+                const _Float16 h0 = (_Float16)h2[0], h1 = (_Float16)h2[1];
+                if (r < 8) { ph0[r] = h0; ph0[r + 1] = h1; } else { ph1[r - 8] = h0; ph1[r - 7] = h1; }
                 if (P_SPLIT) {
-                    const _Float16 lo = f32_to_f16(p - (float)hi);
-                    if (r < 8) pl0[r] = lo; else pl1[r - 8] = lo;
+                    const auto l2 = __builtin_amdgcn_cvt_pkrtz(pv[r] - (float)h0, pv[r + 1] - (float)h1);
+                    const _Float16 l0 = (_Float16)l2[0], l1 = (_Float16)l2[1];
+                    if (r < 8) { pl0[r] = l0; pl0[r + 1] = l1; } else { pl1[r - 8] = l0; pl1[r - 7] = l1; }
                 }
             }
             // O^T += V^T P^T
@@ -328,7 +345,11 @@ __global__ __launch_bounds__(256) void k_attn(
         l_run = l_run * alpha + ps;
         if (t + 1 < n_tiles) sstore(buf ^ 1, nxt);
         __syncthreads();
-    }
+    };
+    // whole tiles without a key mask take the unmasked instance
+    const int n_plain = key_valid ? 0 : len / FA_KT;
+    for (int t = 0; t < n_plain; ++t) tile(t, std::false_type{});
+    for (int t = n_plain; t < n_tiles; ++t) tile(t, std::true_type{});
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv = 1.0f / l_tot;
@@ -491,13 +512,29 @@ __global__ __launch_bounds__(256) void k_attn_1q(
     const int len = seg_len[sg];
     const int64_t row0 = seg_start[sg];
     const int H = n_head * d_head;
+    __shared__ float qf[128];
     const float *qh = q + h * d_head;
+    if (threadIdx.x < d_head) qf[threadIdx.x] = (float)f32_to_f16(qh[threadIdx.x]);
+    __syncthreads();
+    // one key per thread; with d_head % 4 == 0 and 16-byte aligned rows the
+    // row is read as float4 (same fma order over d)
+    const bool v4 = (d_head % 4 == 0) && (ld % 4 == 0) &&
+                    ((reinterpret_cast<uintptr_t>(k) & 15) == 0);
     float mx = -INFINITY;
     for (int j = threadIdx.x; j < len; j += 256) {
         const float *kr = k + (row0 + j) * ld + h * d_head;
         float acc = 0.0f;
-        for (int d = 0; d < d_head; ++d)
-            acc = fmaf((float)f32_to_f16(qh[d]), (float)f32_to_f16(kr[d]), acc);
+        if (v4) {
+            for (int d = 0; d < d_head; d += 4) {
+                const float4 t = *reinterpret_cast<const float4 *>(kr + d);
+                acc = fmaf(qf[d], (float)f32_to_f16(t.x), acc);
+                acc = fmaf(qf[d + 1], (float)f32_to_f16(t.y), acc);
+                acc = fmaf(qf[d + 2], (float)f32_to_f16(t.z), acc);
+                acc = fmaf(qf[d + 3], (float)f32_to_f16(t.w), acc);
+            }
+        } else {
+            for (int d = 0; d < d_head; ++d) acc = fmaf(qf[d], (float)f32_to_f16(kr[d]), acc);
+        }
         const float s = acc * scale;
         p[j] = s;
         mx = fmaxf(mx, s);
