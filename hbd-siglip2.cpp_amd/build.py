@@ -27,6 +27,7 @@ SOURCES = [
     "s2x_misc.hip",
     "s2x_abi.cpp",
     "s2x_encoders.cpp",
+    "s2x_gguf.cpp",
     "siglip2_api.cpp",
 ]
 

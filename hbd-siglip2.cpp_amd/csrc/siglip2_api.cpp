@@ -6,8 +6,22 @@
 
 namespace siglip2 {
 
-static const char *kNoGguf =
-    "GGUF loading is not part of libs2x; pass the tensors to load_weights()";
+// Read a GGUF file's tower weights (host mapping) and upload them; the
+// mapping is released once the encoder holds its device copies.
+template <class W, class Bind, class Load>
+static bool load_gguf(const std::string &path, Bind bind, Load load, std::string &err) {
+    s2x_gguf *g = nullptr;
+    if (s2x_gguf_open(path.c_str(), &g) != S2X_OK) {
+        err = s2x_last_error();
+        return false;
+    }
+    W w{};
+    bool ok = bind(g, &w) == S2X_OK;
+    if (!ok) err = s2x_last_error();
+    if (ok) ok = load(w);
+    s2x_gguf_close(g);
+    return ok;
+}
 
 VisionEncoder::VisionEncoder() = default;
 VisionEncoder::~VisionEncoder() { close(); }
@@ -17,10 +31,11 @@ void VisionEncoder::close() {
     v_ = nullptr;
 }
 
-bool VisionEncoder::load(const std::string &, bool) {
+bool VisionEncoder::load(const std::string &gguf_path, bool) {
     close();
-    error_msg_ = kNoGguf;
-    return false;
+    return load_gguf<s2x_vision_weights>(
+        gguf_path, s2x_gguf_vision_weights,
+        [this](const s2x_vision_weights &w) { return load_weights(w); }, error_msg_);
 }
 
 bool VisionEncoder::load_weights(const s2x_vision_weights &w) {
@@ -83,10 +98,11 @@ void TextEncoder::close() {
     t_ = nullptr;
 }
 
-bool TextEncoder::load(const std::string &, bool) {
+bool TextEncoder::load(const std::string &gguf_path, bool) {
     close();
-    error_msg_ = kNoGguf;
-    return false;
+    return load_gguf<s2x_text_weights>(
+        gguf_path, s2x_gguf_text_weights,
+        [this](const s2x_text_weights &w) { return load_weights(w); }, error_msg_);
 }
 
 bool TextEncoder::load_weights(const s2x_text_weights &w) {

@@ -120,6 +120,10 @@ _sig("s2x_vision_encode_ragged_dev", [_p, _p, _p, _i32, _i32, _i32, _p])
 _sig("s2x_vision_gemm_timing", [_p, ctypes.c_int])
 _sig("s2x_vision_gemm_stats", [_p, ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64), ctypes.c_int])
+_sig("s2x_gguf_open", [ctypes.c_char_p, ctypes.POINTER(_p)])
+_sig("s2x_gguf_close", [_p], None)
+_sig("s2x_gguf_vision_weights", [_p, ctypes.POINTER(VisionWeights)])
+_sig("s2x_gguf_text_weights", [_p, ctypes.POINTER(TextWeights)])
 _sig("s2x_text_create", [ctypes.POINTER(TextWeights), ctypes.POINTER(_p)])
 _sig("s2x_text_destroy", [_p], None)
 _sig("s2x_text_set_stream", [_p, _p])

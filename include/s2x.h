@@ -246,6 +246,24 @@ typedef struct {
     const s2x_layer_weights *layers;
 } s2x_text_weights;
 
+/* ------------------------------------------------------------------------ */
+/* GGUF weight files (replaces the reference's loader path into the          */
+/* encoders, src/gguf_loader.cpp:205-337 and the tensor binding of           */
+/* VisionEncoder::load / TextEncoder::load, src/siglip2_vision.cpp:424-560,  */
+/* src/siglip2_text.cpp:424-540).  Host only: the file is mapped read-only, */
+/* tensors are bound by the converter's names                                 */
+/* (scripts/convert_siglip2_to_gguf.py:7-35) and the siglip2.vision.* /      */
+/* siglip2.text.* metadata.  Q8_0 and F32 tensors are used in place, F16    */
+/* vectors are widened, F16 / F32 matrices are quantized to Q8_0 on load     */
+/* (K zero-padded to a multiple of 32).  The filled struct points into the   */
+/* handle and stays valid until s2x_gguf_close.                               */
+/* ------------------------------------------------------------------------ */
+typedef struct s2x_gguf s2x_gguf;
+int s2x_gguf_open(const char *path, s2x_gguf **out);
+void s2x_gguf_close(s2x_gguf *g);
+int s2x_gguf_vision_weights(s2x_gguf *g, s2x_vision_weights *out);
+int s2x_gguf_text_weights(s2x_gguf *g, s2x_text_weights *out);
+
 typedef struct s2x_vision s2x_vision;
 typedef struct s2x_text s2x_text;
 

@@ -1,9 +1,9 @@
 // siglip2_text.h -- drop-in siglip2::TextEncoder over the s2x C-ABI.
 //
 // Same class and method signatures as the reference (src/siglip2_text.h:
-// 9-75), running on libs2x.so's gfx950 kernels.  Weights arrive through
-// load_weights() (s2x_text_weights); load(gguf_path) reports that GGUF
-// reading is not part of this library.
+// 9-75), running on libs2x.so's gfx950 kernels.  Weights come from a
+// siglip2 GGUF file (load) or from host tensors (load_weights,
+// s2x_text_weights).
 #pragma once
 
 #include <cstdint>

@@ -2,9 +2,8 @@
 //
 // Same class, enum and method signatures as the reference
 // (src/siglip2_vision.h:9-68); the encoder runs on the gfx950 kernels of
-// libs2x.so.  Weights arrive through load_weights() (raw Q8_0 blocks and f32
-// tensors in host memory, s2x_vision_weights); load(gguf_path) reports that
-// GGUF reading is not part of this library.
+// libs2x.so.  Weights come from a siglip2 GGUF file (load) or from host
+// tensors (load_weights: raw Q8_0 blocks and f32, s2x_vision_weights).
 #pragma once
 
 #include <cstdint>
@@ -38,8 +37,9 @@ public:
     VisionEncoder(const VisionEncoder &) = delete;
     VisionEncoder &operator=(const VisionEncoder &) = delete;
 
-    // Reference entry point: GGUF files are not read by this library; returns
-    // false with last_error() explaining so.  Use load_weights().
+    // Reference entry point: read the vision tower of a siglip2 GGUF file
+    // (s2x_gguf_*) and upload it.  private_backend is accepted and ignored
+    // (the encoder always owns its HIP stream).
     bool load(const std::string &gguf_path, bool private_backend = false);
     // Upload + repack the weights onto the current HIP device.
     bool load_weights(const s2x_vision_weights &w);

@@ -1,0 +1,157 @@
+"""GGUF reader (host only): a synthetic tower written to a GGUF v3 file under
+the converter's names must come back as the same weight struct -- every
+tensor byte for byte, F16 vectors widened exactly, F16 / F32 matrices
+quantized to Q8_0 by ggml's rule with K zero-padded -- and malformed files
+must be rejected with an error, never read past their end."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import s2x
+from s2x import synth
+from gguf_util import T_F16, text_tensors, vision_tensors, write_gguf
+
+SMALL_V = synth.VisionConfig(hidden=288, inter=1076, n_head=4, n_layer=2)
+SMALL_T = synth.TextConfig(hidden=288, inter=1076, n_head=4, n_layer=2, vocab=1000, max_pos=64,
+                           proj=288)
+
+
+def _open(path):
+    g = ctypes.c_void_p()
+    st = s2x.lib.s2x_gguf_open(str(path).encode(), ctypes.byref(g))
+    return st, g
+
+
+def _bytes(p, n):
+    return ctypes.string_at(p, n)
+
+
+def _q8_bytes(k_pad, n):
+    return n * (k_pad // 32) * 34
+
+
+def _check_layers(ws, hm, H, F, Fp):
+    for i, L in enumerate(hm.layers):
+        lw = ws.layers[i]
+        for key, n in (("ln1_w", 4 * H), ("ln1_b", 4 * H), ("qkv_b", 12 * H), ("o_b", 4 * H),
+                       ("ln2_w", 4 * H), ("ln2_b", 4 * H), ("up_b", 4 * F), ("down_b", 4 * H),
+                       ("qkv_w", _q8_bytes(H, 3 * H)), ("o_w", _q8_bytes(H, H)),
+                       ("up_w", _q8_bytes(H, F)), ("down_w", _q8_bytes(Fp, H))):
+            assert _bytes(getattr(lw, key), n) == L[key].tobytes(), (i, key)
+
+
+def test_gguf_vision_roundtrip(tmp_path):
+    hm = synth.vision_model(SMALL_V, seed=31)
+    kv, ts = vision_tensors(hm)
+    path = tmp_path / "v.gguf"
+    write_gguf(path, kv, ts)
+    st, g = _open(path)
+    assert st == 0, s2x.lib.s2x_last_error()
+    try:
+        w = s2x.VisionWeights()
+        s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+        c = SMALL_V
+        H, F, Fp = c.hidden, c.inter, c.inter_pad
+        assert (w.hidden, w.inter, w.inter_pad, w.n_head, w.n_layer, w.patch_dim, w.n_side) == (
+            H, F, Fp, c.n_head, c.n_layer, c.patch_dim, c.n_side)
+        assert w.eps == np.float32(c.eps)
+        t = hm.tensors
+        for key, n in (("patch_w", _q8_bytes(c.patch_dim, H)), ("patch_b", 4 * H),
+                       ("pos_embd", 4 * H * c.n_side ** 2), ("post_ln_w", 4 * H),
+                       ("post_ln_b", 4 * H), ("probe", 4 * H), ("hq_w", _q8_bytes(H, H)),
+                       ("hk_w", _q8_bytes(H, H)), ("hv_w", _q8_bytes(H, H)),
+                       ("ho_w", _q8_bytes(H, H)), ("hq_b", 4 * H), ("hk_b", 4 * H),
+                       ("hv_b", 4 * H), ("ho_b", 4 * H), ("hln_w", 4 * H), ("hln_b", 4 * H),
+                       ("hup_w", _q8_bytes(H, F)), ("hup_b", 4 * F),
+                       ("hdown_w", _q8_bytes(Fp, H)), ("hdown_b", 4 * H)):
+            assert _bytes(getattr(w, key), n) == t[key].tobytes(), key
+        _check_layers(w, hm, H, F, Fp)
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_text_roundtrip(tmp_path):
+    hm = synth.text_model(SMALL_T, seed=32)
+    kv, ts = text_tensors(hm)
+    path = tmp_path / "t.gguf"
+    write_gguf(path, kv, ts)
+    st, g = _open(path)
+    assert st == 0, s2x.lib.s2x_last_error()
+    try:
+        w = s2x.TextWeights()
+        s2x.call("s2x_gguf_text_weights", g, ctypes.byref(w))
+        c = SMALL_T
+        H = c.hidden
+        assert (w.hidden, w.inter, w.inter_pad, w.n_head, w.n_layer, w.vocab, w.max_pos, w.proj) == (
+            H, c.inter, c.inter_pad, c.n_head, c.n_layer, c.vocab, c.max_pos, c.proj)
+        t = hm.tensors
+        assert _bytes(w.tok_embd, _q8_bytes(H, c.vocab)) == t["tok_embd"].tobytes()
+        assert _bytes(w.pos_embd, 4 * H * c.max_pos) == t["pos_embd"].tobytes()
+        assert _bytes(w.head_w, _q8_bytes(H, c.proj)) == t["head_w"].tobytes()
+        assert _bytes(w.head_b, 4 * c.proj) == t["head_b"].tobytes()
+        _check_layers(w, hm, H, c.inter, c.inter_pad)
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_f16_tensors_converted(tmp_path):
+    """An F16 ffn_down (K = F, unpadded) is quantized on load with ggml's Q8_0
+    rule and K zero-padded to F_pad; an F16 LayerNorm weight is widened."""
+    hm = synth.vision_model(SMALL_V, seed=33)
+    kv, ts = vision_tensors(hm)
+    c = SMALL_V
+    H, F, Fp = c.hidden, c.inter, c.inter_pad
+    rng = np.random.default_rng(5)
+    w16 = (rng.standard_normal((H, F)) * 0.02).astype(np.float16)
+    w16[0, :32] = 0                      # an all-zero block: d = 0, q = 0
+    w16[1, 5] = np.float16(65504.0)      # the largest fp16
+    ln16 = (1 + 0.02 * rng.standard_normal(H)).astype(np.float16)
+    for i, (name, t, ne, data) in enumerate(ts):
+        if name == "v.blk.0.ffn_down.weight":
+            ts[i] = (name, T_F16, [F, H], w16.tobytes())
+        if name == "v.blk.1.ln1.weight":
+            ts[i] = (name, T_F16, [H], ln16.tobytes())
+    path = tmp_path / "v16.gguf"
+    write_gguf(path, kv, ts)
+    st, g = _open(path)
+    assert st == 0, s2x.lib.s2x_last_error()
+    try:
+        w = s2x.VisionWeights()
+        s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+        want = synth.quantize_q8_0(w16.astype(np.float32), Fp)
+        assert _bytes(w.layers[0].down_w, want.nbytes) == want.tobytes()
+        got = np.frombuffer(_bytes(w.layers[1].ln1_w, 4 * H), np.float32)
+        assert np.array_equal(got, ln16.astype(np.float32))
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_rejects_bad_files(tmp_path):
+    hm = synth.vision_model(SMALL_V, seed=34)
+    kv, ts = vision_tensors(hm)
+    good = tmp_path / "good.gguf"
+    write_gguf(good, kv, ts)
+    raw = good.read_bytes()
+
+    bad_magic = tmp_path / "magic.gguf"
+    bad_magic.write_bytes(b"GGUX" + raw[4:])
+    assert _open(bad_magic)[0] != 0
+
+    truncated = tmp_path / "trunc.gguf"
+    truncated.write_bytes(raw[: len(raw) // 2])  # tensor data past the end
+    assert _open(truncated)[0] != 0
+    assert b"past the end" in s2x.lib.s2x_last_error()
+
+    missing = tmp_path / "missing.gguf"
+    write_gguf(missing, kv, [t for t in ts if t[0] != "v.blk.1.attn_o.weight"])
+    st, g = _open(missing)
+    assert st == 0
+    try:
+        w = s2x.VisionWeights()
+        assert s2x.lib.s2x_gguf_vision_weights(g, ctypes.byref(w)) != 0
+        assert b"v.blk.1.attn_o.weight" in s2x.lib.s2x_last_error()
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+    assert _open(tmp_path / "does-not-exist.gguf")[0] != 0

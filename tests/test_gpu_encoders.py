@@ -241,3 +241,55 @@ def test_so400m_text_5x64_vs_oracle(orc):
             assert c >= 0.9999
     finally:
         t.close()
+
+
+def test_small_towers_from_gguf_same_bits(tmp_path, small_vision):
+    """Encoders created from a GGUF file (s2x_gguf_*) equal the ones created
+    from the host structs, bit for bit."""
+    from gguf_util import text_tensors, vision_tensors, write_gguf
+    v, _ = small_vision
+    path = tmp_path / "v.gguf"
+    write_gguf(path, *vision_tensors(v.host))
+    g = ctypes.c_void_p()
+    s2x.call("s2x_gguf_open", str(path).encode(), ctypes.byref(g))
+    try:
+        w = s2x.VisionWeights()
+        s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+        h = ctypes.c_void_p()
+        s2x.call("s2x_vision_create", ctypes.byref(w), ctypes.byref(h))
+    finally:
+        s2x.lib.s2x_gguf_close(g)  # the encoder holds device copies
+    try:
+        px = synth.pixels(2, 16 * 20, seed=91)
+        pd = dev(px)
+        out = empty((2, v.host.cfg.hidden), torch.float32)
+        s2x.call("s2x_vision_encode_batch_dev", h, ptr(pd), 2, 16, 20, s2x.POOL_PROBE, ptr(out))
+        assert np.array_equal(host(out), v.batch(px, 2, 16, 20, s2x.POOL_PROBE))
+    finally:
+        s2x.lib.s2x_vision_destroy(h)
+
+    hm = synth.text_model(SMALL_T, seed=23)
+    tpath = tmp_path / "t.gguf"
+    write_gguf(tpath, *text_tensors(hm))
+    ids, _ = synth.text_tokens(3, 64, vocab=SMALL_T.vocab, seed=9)
+    outs = []
+    for src in ("struct", "gguf"):
+        h = ctypes.c_void_p()
+        if src == "struct":
+            s2x.call("s2x_text_create", ctypes.byref(hm.struct), ctypes.byref(h))
+        else:
+            s2x.call("s2x_gguf_open", str(tpath).encode(), ctypes.byref(g))
+            try:
+                w = s2x.TextWeights()
+                s2x.call("s2x_gguf_text_weights", g, ctypes.byref(w))
+                s2x.call("s2x_text_create", ctypes.byref(w), ctypes.byref(h))
+            finally:
+                s2x.lib.s2x_gguf_close(g)
+        try:
+            o = np.empty((3, SMALL_T.proj), np.float32)
+            ids32 = np.ascontiguousarray(ids, np.int32)
+            s2x.call("s2x_text_encode_batch", h, ids32.ctypes.data, 64, 3, o.ctypes.data)
+            outs.append(o)
+        finally:
+            s2x.lib.s2x_text_destroy(h)
+    assert np.array_equal(outs[0], outs[1])
