@@ -9,13 +9,16 @@
 // budget.  Here the quants are stored as f16 (exact integers, |q| <= 128):
 //   * two v_mfma_f32_32x32x16_f16 give the block dot I as an exact f32
 //     (products are integers < 2^14, partial sums integers < 2^20);
-//   * the scale tile s[i][j] = dx[i] * dw[j] is one more f16 MFMA: A holds
-//     dx[row] in every k slot, B holds dw[col] in k slot 0 and zeros
-//     elsewhere, so each output is one exact f16 x f16 product in f32;
+//   * the scale tile s[i][j] = dx[i] * dw[j] is one v_mfma_f32_32x32x8_f16
+//     (two-register operands): A holds dx[row] and B holds dw[col] in k
+//     slot 0, every other slot is zero, so each output is one exact
+//     f16 x f16 product in f32.  The zero slots live in registers that are
+//     cleared once; only the scale half-word is reloaded per block;
 //   * the VALU does acc = fmaf(I, s, acc) -- the CPU's operation, one
 //     instruction.
-// Per 32x32 subtile and block: 3 MFMAs (96 cycles) against 16 VALU fmas
-// (64 cycles): the matrix pipe bounds the kernel at 1/3 of the int8 peak.
+// Per 32x32 subtile and block: two 32-cycle MFMAs and the half-rate scale
+// MFMA against 16 VALU fmas (64 cycles): the matrix pipe bounds the kernel
+// at about 2/5 of the int8 peak.
 //
 // Tile: BM x 128 outputs per workgroup of BM/64 x 2 waves, each wave 64 x 64
 // (2 x 2 subtiles).  One pipeline stage is one 32-value block of K: BM X rows
@@ -73,8 +76,16 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 template <int TM>
 struct FragTM {
-    v8h a[TM][2], b[2][2];   // [subtile][k half]
-    uint32_t dx[TM], dw[2];  // fp16 bits of the row / column scales (0 on lanes 32..63)
+    v8h a[TM][2], b[2][2];  // [subtile][k half]
+    // scale-tile operands (32x32x8 f16 MFMA, k slots 0..3 on lanes 0..31):
+    // dword 0 holds the fp16 bits of the row / column scale (0 on lanes
+    // 32..63), dword 1 stays zero for the whole loop, so only dword 0 is
+    // reloaded per block
+    v2i sx[TM], sw[2];
+    __device__ void zero_scales() {
+        for (int a = 0; a < TM; ++a) sx[a] = v2i{0, 0};
+        for (int b = 0; b < 2; ++b) sw[b] = v2i{0, 0};
+    }
 };
 
 // 16 bytes per lane from buffer r at voffset + soffset into LDS at
@@ -117,7 +128,7 @@ __device__ __forceinline__ void wait_stage(bool scale_wave, int after) {
 }
 
 template <class C, int EPI>
-__global__ __launch_bounds__(C::NT) void k_mmq16(
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 512 ? 4 : 2))) void k_mmq16(
     const _Float16 *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
     const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
     int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
@@ -209,15 +220,15 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
             f.a[a][0] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c0);
             f.a[a][1] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c1);
         }
-        f.dx[0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
-        if constexpr (TM == 2) f.dx[1] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
+        f.sx[0][0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
+        if constexpr (TM == 2) f.sx[1][0] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             f.b[b][0] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c0);
             f.b[b][1] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c1);
         }
-        f.dw[0] = *reinterpret_cast<const uint16_t *>(sb + dwo0);
-        f.dw[1] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
+        f.sw[0][0] = *reinterpret_cast<const uint16_t *>(sb + dwo0);
+        f.sw[1][0] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
     };
 
     // One block of K.  Subtile k = 2a + b gets I (two MFMAs) and the scale
@@ -233,9 +244,8 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
         for (int k = 0; k < 2 * TM; ++k) {
             const int a = k >> 1, b = k & 1;
             v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][0], f.b[b][0], zero, 0, 0, 0);
-            const v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                __builtin_bit_cast(v8h, v4i{(int)f.dx[a], 0, 0, 0}),
-                __builtin_bit_cast(v8h, v4i{(int)f.dw[b], 0, 0, 0}), zero, 0, 0, 0);
+            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(
+                __builtin_bit_cast(v4h, f.sx[a]), __builtin_bit_cast(v4h, f.sw[b]), zero, 0, 0, 0);
             I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
             if constexpr (!C::SKEW) {
 #pragma unroll
@@ -270,6 +280,7 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
         const int npro = min(NS - 1, KB);
         for (int s = 0; s < npro; ++s) issue(s, s);
         Frag F;
+        F.zero_scales();
         auto step = [&](int s, auto bufc) {
             constexpr int buf = decltype(bufc)::value;
             wait_stage<C>(scale_wave, min(NS - 2, KB - 1 - s));
@@ -298,6 +309,8 @@ __global__ __launch_bounds__(C::NT) void k_mmq16(
         wait_stage<C>(scale_wave, npro - 1);
         block_sync_lds();
         Frag F0, F1;
+        F0.zero_scales();
+        F1.zero_scales();
         load_frag(lds, F0);
         auto step = [&](int s, auto bufc, Frag &cur, Frag &nxt) {
             constexpr int buf = decltype(bufc)::value;  // buffer of block s
