@@ -16,9 +16,9 @@
 //     cleared once; only the scale half-word is reloaded per block;
 //   * the VALU does acc = fmaf(I, s, acc) -- the CPU's operation, one
 //     instruction.
-// Per 32x32 subtile and block: two 32-cycle MFMAs and the half-rate scale
-// MFMA against 16 VALU fmas (64 cycles): the matrix pipe bounds the kernel
-// at about 2/5 of the int8 peak.
+// Per 32x32 subtile and block: 3 MFMAs of 32 cycles each (96 cycles; the
+// 32x32x8 form issues at the same rate as 32x32x16) against 16 VALU fmas
+// (64 cycles): the matrix pipe bounds the kernel at 1/3 of the int8 peak.
 //
 // Tile: BM x 128 outputs per workgroup of BM/64 x 2 waves, each wave 64 x 64
 // (2 x 2 subtiles).  One pipeline stage is one 32-value block of K: BM X rows
