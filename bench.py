@@ -2,7 +2,7 @@
 patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
-                    [--cpu-images 3] [--no-cpu] [--gemm f16|i8]
+                    [--cpu-images 3] [--no-cpu] [--gemm f16|i8] [--lanes N]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
@@ -62,6 +62,9 @@ def main():
     ap.add_argument("--gemm", choices=["f16", "i8"], default="f16",
                     help="GEMM kernel: f16-MFMA block dots + scale tile (default) or "
                          "int8-MFMA block dots with VALU rescale; same bits")
+    ap.add_argument("--lanes", type=int, default=0,
+                    help="row ranges (whole images) run concurrently on their own streams "
+                         "(1..4; default: the library's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (the tower "
@@ -94,6 +97,8 @@ def main():
     s2x.call("s2x_vision_create", ctypes.byref(hm.struct), ctypes.byref(v))
     s2x.call("s2x_vision_set_gemm_variant", v,
              s2x.GEMM_F16_MFMA if args.gemm == "f16" else s2x.GEMM_I8_MFMA)
+    if args.lanes:
+        s2x.call("s2x_vision_set_lanes", v, args.lanes)
     stream = torch.cuda.ExternalStream  # noqa: F841 (the encoder owns its stream)
     px = synth.pixels(B, n_pos, seed=1234)
     pd = torch.from_numpy(px).to("cuda:0")

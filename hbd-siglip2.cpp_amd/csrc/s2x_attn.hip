@@ -48,6 +48,19 @@ AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d
     return L;
 }
 
+// Segments [s0, s1) of layout L as a layout of their own: the same plane
+// geometry with the Q / K / V^T bases moved to segment s0.
+AttnLayout attn_sublayout(const AttnLayout &L, int64_t s0, int64_t s1) {
+    AttnLayout S = L;
+    const size_t qk_seg = (size_t)(L.n_head * L.len_pad * L.d_pad) * 2;
+    const size_t vt_seg = (size_t)(L.n_head * L.dv_pad * L.len_pad) * 2;
+    S.n_seg = s1 - s0;
+    S.q_off = L.q_off + (size_t)s0 * qk_seg;
+    S.k_off = L.k_off + (size_t)s0 * qk_seg;
+    S.vt_off = L.vt_off + (size_t)s0 * vt_seg;
+    return S;
+}
+
 // ---------------------------------------------------------------------------
 // staging: one workgroup per (64-position tile, head, segment)
 // ---------------------------------------------------------------------------

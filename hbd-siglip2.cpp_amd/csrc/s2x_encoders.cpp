@@ -193,15 +193,36 @@ struct Tower {
     // holds the transposed fp16 scales [KB][mmq16_ld_dx(M)] or the
     // block_q8_1 scale words [M][KB].
     bool gemm_f16 = true;
+    // The encoder blocks of a batch run as up to MAX_LANES independent row
+    // ranges (whole segments), each on a stream of its own: while one
+    // lane's GEMM drains its last, partly filled round of tiles, the other
+    // lanes' kernels occupy the idle CUs.  Lanes fork from `stream` and
+    // join back into it, so callers see one ordered stream.
+    static constexpr int MAX_LANES = 4;
+    int n_lanes = 1;
+    hipStream_t lane_s[MAX_LANES] = {};
+    hipEvent_t ev_fork = nullptr, ev_join[MAX_LANES] = {}, ev_phase[MAX_LANES] = {};
 
     ~Tower() {
         for (auto &L : layers) L.release();
+        for (int i = 0; i < MAX_LANES; ++i) {
+            if (lane_s[i]) (void)hipStreamDestroy(lane_s[i]);
+            if (ev_join[i]) (void)hipEventDestroy(ev_join[i]);
+            if (ev_phase[i]) (void)hipEventDestroy(ev_phase[i]);
+        }
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (own) (void)hipStreamDestroy(own);
     }
 
     int init_stream() {
         S2X_HIP_TRY(hipStreamCreateWithFlags(&own, hipStreamNonBlocking));
         stream = own;
+        S2X_HIP_TRY(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+        for (int i = 0; i < MAX_LANES; ++i) {
+            S2X_HIP_TRY(hipStreamCreateWithFlags(&lane_s[i], hipStreamNonBlocking));
+            S2X_HIP_TRY(hipEventCreateWithFlags(&ev_join[i], hipEventDisableTiming));
+            S2X_HIP_TRY(hipEventCreateWithFlags(&ev_phase[i], hipEventDisableTiming));
+        }
         return S2X_OK;
     }
 
@@ -230,20 +251,36 @@ struct Tower {
     // GEMM with optional event timing; k_logical excludes the K padding.
     int gemm(const s2x_weight *w, int64_t M, float *y, int64_t ldy, const EpiParams &e,
              int64_t k_logical, bool from_qs2 = false) {
+        if (gemm_f16) {
+            const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
+            return gemm_rows(w, xq.as<_Float16>(), xd.as<uint16_t>(), mmq16_ld_dx(M), M, y, ldy,
+                             e, k_logical, stream);
+        }
+        return timed(w, M, k_logical, stream, [&] {
+            return launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y, ldy, e, stream);
+        });
+    }
+    // f16 GEMM over rows whose quants start at xh and transposed scales at
+    // xdT (row stride ld_dx of the whole batch), on stream st.
+    int gemm_rows(const s2x_weight *w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+                  int64_t M, float *y, int64_t ldy, const EpiParams &e, int64_t k_logical,
+                  hipStream_t st) {
+        return timed(w, M, k_logical, st, [&] {
+            return launch_mmq_f16(w->view, xh, xdT, ld_dx, M, y, ldy, e, st);
+        });
+    }
+    template <class Launch>
+    int timed(const s2x_weight *w, int64_t M, int64_t k_logical, hipStream_t st, Launch &&launch) {
         hipEvent_t a = nullptr, b = nullptr;
         if (timing.on) {
             a = timing.get();
             b = timing.get();
-            S2X_HIP_TRY(hipEventRecord(a, stream));
+            S2X_HIP_TRY(hipEventRecord(a, st));
         }
-        const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
-        hipError_t err = gemm_f16 ? launch_mmq_f16(w->view, xq.as<_Float16>(), xd.as<uint16_t>(),
-                                                   mmq16_ld_dx(M), M, y, ldy, e, stream)
-                                  : launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y,
-                                               ldy, e, stream);
+        const hipError_t err = launch();
         if (err != hipSuccess) return hip_fail(err, "mmq launch");
         if (timing.on) {
-            S2X_HIP_TRY(hipEventRecord(b, stream));
+            S2X_HIP_TRY(hipEventRecord(b, st));
             timing.pending.push_back({a, b, 2.0 * (double)M * (double)w->view.N * (double)k_logical});
         }
         return S2X_OK;
@@ -336,36 +373,96 @@ struct Tower {
     const int32_t *seg_start() const { return seg.as<int32_t>(); }
     const int32_t *seg_len(int64_t n_seg) const { return seg.as<int32_t>() + n_seg; }
 
+    // Lane boundaries: segment indices b[0] = 0 < b[1] < ... < b[n] = n_seg
+    // splitting the rows as evenly as whole segments allow.  A lane's first
+    // row must be a multiple of 8 (16-byte aligned transposed scales).
+    std::vector<int64_t> lane_bounds(int64_t M, int64_t n_seg) const {
+        std::vector<int64_t> b{0};
+        const int64_t n = std::min<int64_t>(n_lanes, MAX_LANES);
+        const int32_t *start = seg_host.data();
+        for (int64_t i = 1; i < n && (int64_t)seg_host.size() == 2 * n_seg; ++i) {
+            const int64_t target = M * i / n;
+            int64_t best = -1;
+            for (int64_t s = b.back() + 1; s < n_seg; ++s)
+                if (start[s] % 8 == 0 &&
+                    (best < 0 || std::llabs(start[s] - target) < std::llabs(start[best] - target)))
+                    best = s;
+            if (best > 0) b.push_back(best);
+        }
+        b.push_back(n_seg);
+        return b;
+    }
+
+    // Encoder blocks, f16 GEMM + flash attention path, for rows [r0, r1)
+    // = segments [s0, s1) of an M-row batch, on stream st.  The QKV GEMM
+    // writes the attention operands itself (EPI_QKV); every buffer is
+    // addressed by absolute row / segment, so lanes touch disjoint parts.
+    int run_rows(hipStream_t st, int64_t r0, int64_t r1, int64_t s0, int64_t s1, int64_t M,
+                 const AttnLayout &AL, float kq_scale, const uint8_t *key_valid,
+                 hipEvent_t phase = nullptr) {
+        const int64_t Mp = r1 - r0, ld = mmq16_ld_dx(M);
+        if (Mp == 0) return S2X_OK;
+        float *xp = x.as<float>() + r0 * H;
+        _Float16 *q1 = qs.as<_Float16>() + r0 * H, *q2 = qs2.as<_Float16>() + r0 * F_pad;
+        uint16_t *d1 = ds.as<uint16_t>() + r0, *d2 = ds2.as<uint16_t>() + r0;
+        Q81Out qa;
+        qa.qh = q1;
+        qa.dT = d1;
+        qa.ldT = ld;
+        const AttnLayout ALs = attn_sublayout(AL, s0, s1);
+        const int32_t *rm = rowmap.as<int32_t>() + r0;
+        hipError_t e;
+        for (auto &L : layers) {
+            e = launch_layernorm(xp, H, Mp, H, L.ln1_w, L.ln1_b, eps, &qa, nullptr, H, st);
+            if (e != hipSuccess) return hip_fail(e, "layernorm launch");
+            S2X_TRY(gemm_rows(L.qkv, q1, d1, ld, Mp, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rm), H, st));
+            e = launch_attn(attn_ws.p, seg_start() + s0, seg.as<int32_t>() + AL.n_seg + s0,
+                            key_valid, ALs, kq_scale, att.as<float>(), H, st);
+            if (e != hipSuccess) return hip_fail(e, "attn launch");
+            if (phase && &L == &layers[0]) S2X_HIP_TRY(hipEventRecord(phase, st));
+            e = launch_quantize_q8_1(att.as<float>() + r0 * H, H, Mp, H, H, qa, st);
+            if (e != hipSuccess) return hip_fail(e, "quantize launch");
+            S2X_TRY(gemm_rows(L.o, q1, d1, ld, Mp, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H, st));
+            e = launch_layernorm(xp, H, Mp, H, L.ln2_w, L.ln2_b, eps, &qa, nullptr, H, st);
+            if (e != hipSuccess) return hip_fail(e, "layernorm launch");
+            EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
+            up.q_out = q2;
+            up.q_dT = d2;
+            up.q_kpad = F_pad;
+            up.q_ld = ld;
+            S2X_TRY(gemm_rows(L.up, q1, d1, ld, Mp, nullptr, 0, up, H, st));
+            S2X_TRY(gemm_rows(L.down, q2, d2, ld, Mp, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F, st));
+        }
+        return S2X_OK;
+    }
+
     // The 27 encoder blocks in place on x (M packed rows).
     int run_layers(int64_t M, int64_t n_seg, int64_t max_len, const uint8_t *key_valid) {
         const AttnLayout AL = attn_layout(n_seg, max_len, n_head, d_head);
         const float kq_scale = 1.0f / std::sqrt((float)d_head);
         float *xp = x.as<float>();
-        // f16 GEMM + flash attention: the QKV GEMM writes the attention
-        // operands itself (EPI_QKV); otherwise f32 rows and a staging pass
-        const bool fused_qkv = gemm_f16 && !attn_f64;
-        if (fused_qkv) S2X_TRY(attn_ws_ready(AL));
+        if (gemm_f16 && !attn_f64) {
+            S2X_TRY(attn_ws_ready(AL));
+            const std::vector<int64_t> b = lane_bounds(M, n_seg);
+            const int nl = (int)b.size() - 1;
+            if (nl == 1) return run_rows(stream, 0, M, 0, n_seg, M, AL, kq_scale, key_valid);
+            const int32_t *start = seg_host.data();
+            S2X_HIP_TRY(hipEventRecord(ev_fork, stream));
+            for (int i = 0; i < nl; ++i) {
+                const int64_t r0 = start[b[i]], r1 = b[i + 1] < n_seg ? start[b[i + 1]] : M;
+                // each lane starts when the previous one has reached its first
+                // attention, so the lanes' GEMM tails fall at different times
+                S2X_HIP_TRY(hipStreamWaitEvent(lane_s[i], i ? ev_phase[i - 1] : ev_fork, 0));
+                S2X_TRY(run_rows(lane_s[i], r0, r1, b[i], b[i + 1], M, AL, kq_scale, key_valid,
+                                 i + 1 < nl ? ev_phase[i] : nullptr));
+                S2X_HIP_TRY(hipEventRecord(ev_join[i], lane_s[i]));
+            }
+            for (int i = 0; i < nl; ++i) S2X_HIP_TRY(hipStreamWaitEvent(stream, ev_join[i], 0));
+            return S2X_OK;
+        }
         for (auto &L : layers) {
             S2X_TRY(layernorm_q(xp, M, L.ln1_w, L.ln1_b, nullptr));
             hipError_t e;
-            if (fused_qkv) {
-                S2X_TRY(gemm(L.qkv, M, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rowmap.as<int32_t>()), H));
-                e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
-                                att.as<float>(), H, stream);
-                if (e != hipSuccess) return hip_fail(e, "attn launch");
-                S2X_TRY(quantize(att.as<float>(), H, M, H, H));
-                S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
-                S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
-                EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
-                up.q_out = qs2.as<_Float16>();
-                up.q_dT = ds2.as<uint16_t>();
-                up.q_kpad = F_pad;
-                up.q_ld = mmq16_ld_dx(M);
-                S2X_TRY(gemm(L.up, M, nullptr, 0, up, H));
-                S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F,
-                             true));
-                continue;
-            }
             S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
             if (attn_f64) {
                 e = launch_attn_f64(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
@@ -609,6 +706,14 @@ int s2x_vision_set_gemm_variant(s2x_vision *v, int variant) {
         return fail(S2X_ERR_INVALID_ARG, "gemm variant %d unknown", variant);
     S2X_HIP_TRY(hipStreamSynchronize(v->t.stream));  // the activation buffer changes format
     v->t.gemm_f16 = variant == S2X_GEMM_F16_MFMA;
+    return S2X_OK;
+}
+
+int s2x_vision_set_lanes(s2x_vision *v, int n) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (n < 1 || n > Tower::MAX_LANES)
+        return fail(S2X_ERR_INVALID_ARG, "lanes %d outside 1..%d", n, Tower::MAX_LANES);
+    v->t.n_lanes = n;
     return S2X_OK;
 }
 

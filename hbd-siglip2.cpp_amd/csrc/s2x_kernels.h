@@ -111,6 +111,7 @@ struct AttnLayout {
     bool p_split = true;
 };
 AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head);
+AttnLayout attn_sublayout(const AttnLayout &L, int64_t s0, int64_t s1);
 hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                             const int32_t *seg_start, const int32_t *seg_len,
                             const AttnLayout &L, void *ws, hipStream_t stream);

@@ -138,7 +138,10 @@ hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t 
 // ---------------------------------------------------------------------------
 constexpr int LN_MAXIT = 8;  // H <= 8 * 256
 
-template <bool QUANT, bool WRITE_Y>
+// NIT = ceil(H / 256) column passes of 4 values per lane; only x stays in
+// registers across the reductions (w and b are read when applied), which
+// keeps the kernel at full occupancy.
+template <bool QUANT, bool WRITE_Y, int NIT>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
     const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
@@ -147,17 +150,12 @@ __global__ __launch_bounds__(256) void k_layernorm(
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const float *xr = x + row * ldx;
-    float v[LN_MAXIT][4], wv[LN_MAXIT][4], bv[LN_MAXIT][4];
-    // x, w and b all requested before any use: the row's loads overlap
+    float v[NIT][4];
 #pragma unroll
-    for (int it = 0; it < LN_MAXIT; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[it][j] = 0.0f;
-            wv[it][j] = 1.0f;
-            bv[it][j] = 0.0f;
-        }
+        for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
         if (c < H) {
             if (vec4 & 1) {
                 const float4 t = *reinterpret_cast<const float4 *>(xr + c);
@@ -166,27 +164,11 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[it][j] = xr[c + j];
             }
-            if (vec4 & 4) {
-                if (w) {
-                    const float4 t = *reinterpret_cast<const float4 *>(w + c);
-                    wv[it][0] = t.x; wv[it][1] = t.y; wv[it][2] = t.z; wv[it][3] = t.w;
-                }
-                if (b) {
-                    const float4 t = *reinterpret_cast<const float4 *>(b + c);
-                    bv[it][0] = t.x; bv[it][1] = t.y; bv[it][2] = t.z; bv[it][3] = t.w;
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (w) wv[it][j] = w[c + j];
-                    if (b) bv[it][j] = b[c + j];
-                }
-            }
         }
     }
     double s = 0.0;
 #pragma unroll
-    for (int it = 0; it < LN_MAXIT; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
         if (c < H) s = s + (((double)v[it][0] + (double)v[it][1]) + ((double)v[it][2] + (double)v[it][3]));
     }
@@ -196,7 +178,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
     const float mean = (float)(wave_dsum(s) / (double)H);
     double s2 = 0.0;
 #pragma unroll
-    for (int it = 0; it < LN_MAXIT; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
         if (c < H) {
 #pragma unroll
@@ -209,15 +191,32 @@ __global__ __launch_bounds__(256) void k_layernorm(
     const float var = (float)(wave_dsum(s2) / (double)H);
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
-    for (int it = 0; it < LN_MAXIT; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
         if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
+        float wv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (vec4 & 4) {
+            if (w) {
+                const float4 t = *reinterpret_cast<const float4 *>(w + c);
+                wv[0] = t.x; wv[1] = t.y; wv[2] = t.z; wv[3] = t.w;
+            }
+            if (b) {
+                const float4 t = *reinterpret_cast<const float4 *>(b + c);
+                bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (w) wv[j] = w[c + j];
+                if (b) bv[j] = b[c + j];
+            }
+        }
         float o[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float t = (v[it][j] - mean) * scale;
-            if (w) t = t * wv[it][j];
-            if (b) t = t + bv[it][j];
+            if (w) t = t * wv[j];
+            if (b) t = t + bv[j];
             o[j] = t;
         }
         if (WRITE_Y) {
@@ -243,6 +242,21 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
 }
 
+template <int NIT>
+void launch_ln_nit(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
+                   const float *b, float eps, bool quant, const Q81Out &qo, float *y,
+                   int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
+    if (quant && y)
+        hipLaunchKernelGGL((k_layernorm<true, true, NIT>), grid, dim3(256), 0, stream, x, H, M,
+                           ldx, w, b, eps, qo, y, ldy, vec4);
+    else if (quant)
+        hipLaunchKernelGGL((k_layernorm<true, false, NIT>), grid, dim3(256), 0, stream, x, H, M,
+                           ldx, w, b, eps, qo, y, ldy, vec4);
+    else
+        hipLaunchKernelGGL((k_layernorm<false, true, NIT>), grid, dim3(256), 0, stream, x, H, M,
+                           ldx, w, b, eps, qo, y, ldy, vec4);
+}
+
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
                             const float *w, const float *b, float eps, const Q81Out *q,
                             float *y, int64_t ldy, hipStream_t stream) {
@@ -250,19 +264,20 @@ hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
     if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) vec4 |= 4;
+    if (H <= 0 || H % QK != 0 || H > LN_MAXIT * 256 || (!q && !y)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((M + 3) / 4));
     const bool quant = q != nullptr;
     const Q81Out qo = q ? *q : Q81Out{};
-    const bool wy = y != nullptr;
-    if (quant && wy)
-        hipLaunchKernelGGL((k_layernorm<true, true>), grid, dim3(256), 0, stream, x, H, M, ldx,
-                           w, b, eps, qo, y, ldy, vec4);
-    else if (quant)
-        hipLaunchKernelGGL((k_layernorm<true, false>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qo, y, ldy, vec4);
-    else
-        hipLaunchKernelGGL((k_layernorm<false, true>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qo, y, ldy, vec4);
+    switch ((H + 255) / 256) {
+    case 1: launch_ln_nit<1>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 2: launch_ln_nit<2>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 3: launch_ln_nit<3>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 4: launch_ln_nit<4>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 5: launch_ln_nit<5>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 6: launch_ln_nit<6>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    case 7: launch_ln_nit<7>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    default: launch_ln_nit<8>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
+    }
     return hipGetLastError();
 }
 

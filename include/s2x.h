@@ -284,6 +284,12 @@ int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
  * give the same bits. */
 enum { S2X_GEMM_F16_MFMA = 0, S2X_GEMM_I8_MFMA = 1 };
 int s2x_vision_set_gemm_variant(s2x_vision *v, int variant);
+/* Concurrency of a batch (f16 GEMM + flash attention path): the encoder
+ * blocks run as n (1..4, default 1) independent row ranges of whole images
+ * on streams of their own, forked from and joined back into the encoder's
+ * stream.  Results do not depend on n.  No counterpart in the reference
+ * (its CPU path runs one image at a time). */
+int s2x_vision_set_lanes(s2x_vision *v, int n);
 
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */

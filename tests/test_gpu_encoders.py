@@ -110,6 +110,27 @@ def test_small_vision_gemm_variants_same_bits(small_vision):
     assert s2x.lib.s2x_vision_set_gemm_variant(v.h, 7) == 1
 
 
+def test_small_vision_lanes_same_bits(small_vision):
+    # the blocks of a batch split into 1..4 row ranges of whole images on
+    # streams of their own: every lane count must give the same bits, and
+    # the same as the int8 GEMM path, which never splits
+    v, _ = small_vision
+    n_img = 6
+    px = synth.pixels(n_img, 16 * 16, seed=78)
+    s2x.call("s2x_vision_set_gemm_variant", v.h, s2x.GEMM_I8_MFMA)
+    ref = v.batch(px, n_img, 16, 16, s2x.POOL_PROBE)
+    s2x.call("s2x_vision_set_gemm_variant", v.h, s2x.GEMM_F16_MFMA)
+    try:
+        for lanes in (1, 2, 3, 4, 2):
+            s2x.call("s2x_vision_set_lanes", v.h, lanes)
+            got = v.batch(px, n_img, 16, 16, s2x.POOL_PROBE)
+            assert np.array_equal(got, ref), lanes
+    finally:
+        s2x.call("s2x_vision_set_lanes", v.h, 2)
+    assert s2x.lib.s2x_vision_set_lanes(v.h, 0) == 1
+    assert s2x.lib.s2x_vision_set_lanes(v.h, 5) == 1
+
+
 def test_vision_rejects_bad_shapes(small_vision):
     v, _ = small_vision
     px = np.zeros((4, 768), np.float32)
