@@ -165,7 +165,8 @@ constexpr int FA_DP = 80;              // Q/K row length (halves)
 constexpr int FA_DV = 96;              // V^T rows
 constexpr int FA_KT = 64;              // keys per LDS tile
 constexpr int FA_KP = FA_DP + 8;       // K tile pitch (halves): conflict-free 16-byte reads
-constexpr int FA_VP = FA_KT + 4;       // V^T tile pitch (halves): conflict-free 8-byte reads
+constexpr int FA_VP = FA_KT + 8;       // V^T tile pitch (halves): 16-byte rows, conflict-free reads
+constexpr int FA_ONES = 88;            // V^T padding row held at 1.0: O^T row 88 = sum of P
 constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
 
 template <bool P_SPLIT>
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void k_attn(
     for (int j = 0; j < 3; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = -INFINITY;
 
     const int n_tiles = (len + FA_KT - 1) / FA_KT;
 
@@ -211,14 +212,16 @@ __global__ __launch_bounds__(256) void k_attn(
     // 640 K chunks of 16 B; threads past the end re-load the last chunk
     // (always in bounds) and later rewrite it with the value it already has
     const int kc0 = tid, kc1 = tid + 256, kc2 = min(tid + 512, FA_KT * FA_DP / 8 - 1);
-    auto vload = [&](int k0, int i) {
+    auto vload = [&](int k0, int i, auto edgec) {
+        constexpr bool edge = decltype(edgec)::value;
         const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
         const int r = c >> 3, cc = (c & 7) * 8;
         uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
         // keys past the segment hold zeros or stale finite data; zero them so
-        // a stale NaN/Inf can never meet a zero probability
+        // a stale NaN/Inf can never meet a zero probability (only the tile
+        // holding the segment end has such keys)
         const int valid = len - (k0 + cc);
-        if (valid < 8) {
+        if (edge && valid < 8) {
             const auto keep = [valid](int j) {
                 return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
             };
@@ -226,16 +229,17 @@ __global__ __launch_bounds__(256) void k_attn(
         }
         return v;
     };
-    auto gload = [&](int t) {
+    auto gload = [&](int t, auto edgec) {
+        constexpr bool edge = decltype(edgec)::value;
         const int k0 = t * FA_KT;
         const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
         Tile g;
         g.k0 = ks[kc0];
         g.k1 = ks[kc1];
         g.k2 = ks[kc2];
-        g.v0 = vload(k0, 0);
-        g.v1 = vload(k0, 1);
-        g.v2 = vload(k0, 2);
+        g.v0 = vload(k0, 0, edgec);
+        g.v1 = vload(k0, 1, edgec);
+        g.v2 = vload(k0, 2, edgec);
         return g;
     };
     auto sstore = [&](int buf, const Tile &g) {
@@ -247,18 +251,27 @@ __global__ __launch_bounds__(256) void k_attn(
         kput(kc0, g.k0);
         kput(kc1, g.k1);
         kput(kc2, g.k2);
+        // V^T rows keep each 16-key group in the order [0-3, 8-11, 4-7,
+        // 12-15]: the 8 keys a lane feeds to one PV MFMA (4 lh + 0..3 and
+        // 8 + 4 lh + 0..3, the S^T result layout) are then one 16-byte read
         const auto vput = [&](int i, uint4 v) {
             const int c = tid + i * 256;
-            uint2 *dst = reinterpret_cast<uint2 *>(vl + (c >> 3) * FA_VP + (c & 7) * 8);  // 8-byte aligned
-            dst[0] = make_uint2(v.x, v.y);
-            dst[1] = make_uint2(v.z, v.w);
+            const int row = c >> 3, ch = c & 7;
+            if (row == FA_ONES) v = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+            _Float16 *base = vl + row * FA_VP + (ch >> 1) * 16 + (ch & 1) * 4;
+            *reinterpret_cast<uint2 *>(base) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2 *>(base + 8) = make_uint2(v.z, v.w);
         };
         vput(0, g.v0);
         vput(1, g.v1);
         vput(2, g.v2);
     };
 
-    sstore(0, gload(0));
+    const int n_plain = key_valid ? 0 : len / FA_KT;  // whole tiles without a key mask
+    if (n_plain == 0)
+        sstore(0, gload(0, std::true_type{}));
+    else
+        sstore(0, gload(0, std::false_type{}));
     __syncthreads();
 
     // one 64-key tile; MASK: the tile holding the segment end, or a key mask
@@ -266,7 +279,10 @@ __global__ __launch_bounds__(256) void k_attn(
         constexpr bool MASK = decltype(maskc)::value;
         const int buf = t & 1;
         Tile nxt{};
-        if (t + 1 < n_tiles) nxt = gload(t + 1);
+        if (t + 1 < n_plain)
+            nxt = gload(t + 1, std::false_type{});
+        else if (t + 1 < n_tiles)
+            nxt = gload(t + 1, std::true_type{});
         const _Float16 *kl = lds + buf * FA_STAGE;
         const _Float16 *vl = kl + FA_KT * FA_KP;
         // S^T for the tile's two 32-key halves (raw q.k, unscaled)
@@ -314,57 +330,61 @@ __global__ __launch_bounds__(256) void k_attn(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
         }
-        float ps = 0.0f;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             // P as f16 for the PV product; with P_SPLIT as a pair p ~ hi + lo
-            // (hi = f16(p), lo = f16(p - hi), p - hi exact in f32): ~22
-            // significant bits instead of 11.  Pairs of values convert in
-            // one v_cvt_pkrtz_f16_f32; truncation of hi is harmless since lo
-            // carries the remainder.
+            // (hi = f16(p) rounded toward zero, lo = f16(p - hi) with p - hi
+            // exact in f32): ~22 significant bits instead of 11.  Pairs of
+            // values convert in one v_cvt_pkrtz_f16_f32, whose packed words
+            // are the MFMA operand registers as they stand.
             float pv[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                pv[r] = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
-                ps = ps + pv[r];
-            }
-            v8h ph0, ph1, pl0, pl1;
+            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
+            uint32_t hw[8], lw[8];
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
                 const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[r], pv[r + 1]);
-                const _Float16 h0 = (_Float16)h2[0], h1 = (_Float16)h2[1];
-                if (r < 8) { ph0[r] = h0; ph0[r + 1] = h1; } else { ph1[r - 8] = h0; ph1[r - 7] = h1; }
+                hw[r / 2] = __builtin_bit_cast(uint32_t, h2);
                 if (P_SPLIT) {
-                    const auto l2 = __builtin_amdgcn_cvt_pkrtz(pv[r] - (float)h0, pv[r + 1] - (float)h1);
-                    const _Float16 l0 = (_Float16)l2[0], l1 = (_Float16)l2[1];
-                    if (r < 8) { pl0[r] = l0; pl0[r + 1] = l1; } else { pl1[r - 8] = l0; pl1[r - 7] = l1; }
+                    // p - hi in one v_fma_mix_f32 each (hi read as f16 from its
+                    // half of the packed word, -1.0 as f32, p as f32): exact
+                    float l0, l1;
+                    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]"
+                        : "=v"(l0) : "v"(hw[r / 2]), "v"(pv[r]));
+                    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                        : "=v"(l1) : "v"(hw[r / 2]), "v"(pv[r + 1]));
+                    lw[r / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
                 }
             }
-            // O^T += V^T P^T
+            const v8h ph0 = __builtin_bit_cast(v8h, v4u{hw[0], hw[1], hw[2], hw[3]});
+            const v8h ph1 = __builtin_bit_cast(v8h, v4u{hw[4], hw[5], hw[6], hw[7]});
+            v8h pl0 = {}, pl1 = {};
+            if (P_SPLIT) {
+                pl0 = __builtin_bit_cast(v8h, v4u{lw[0], lw[1], lw[2], lw[3]});
+                pl1 = __builtin_bit_cast(v8h, v4u{lw[4], lw[5], lw[6], lw[7]});
+            }
+            // O^T += V^T P^T (row FA_ONES of V^T is 1: O^T row FA_ONES sums P)
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    const _Float16 *vp = vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 4 * lh;
-                    const v4h lo = *reinterpret_cast<const v4h *>(vp);
-                    const v4h hi = *reinterpret_cast<const v4h *>(vp + 8);
-                    const v8h vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const v8h vf = *reinterpret_cast<const v8h *>(vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 8 * lh);
                     o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? ph1 : ph0, o[j], 0, 0, 0);
                     if (P_SPLIT)
                         o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? pl1 : pl0, o[j], 0, 0, 0);
                 }
             }
         }
-        l_run = l_run * alpha + ps;
         if (t + 1 < n_tiles) sstore(buf ^ 1, nxt);
         __syncthreads();
     };
     // whole tiles without a key mask take the unmasked instance
-    const int n_plain = key_valid ? 0 : len / FA_KT;
     for (int t = 0; t < n_plain; ++t) tile(t, std::false_type{});
     for (int t = n_plain; t < n_tiles; ++t) tile(t, std::true_type{});
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    // sum of P: O^T row FA_ONES = 64 + 24 (register 12 of lanes 0..31)
+    static_assert(FA_ONES == 2 * 32 + 8 * 3 && FA_ONES >= FA_DP && FA_ONES < FA_DV, "ones row");
+    const float l_tot = __shfl(o[2][12], lr);
     const float inv = 1.0f / l_tot;
     if (q < len) {
         float *orow = out + (row0 + q) * ld_out + h * d_head;

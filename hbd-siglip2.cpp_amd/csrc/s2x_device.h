@@ -17,6 +17,7 @@ constexpr int QK = 32;           // Q8_0 / Q8_1 block length
 constexpr int WAVE = 64;         // CDNA wavefront
 
 typedef int      v2i  __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u  __attribute__((ext_vector_type(4)));
 typedef int      v4i  __attribute__((ext_vector_type(4)));
 typedef int      v16i __attribute__((ext_vector_type(16)));
 typedef float    v4f  __attribute__((ext_vector_type(4)));
