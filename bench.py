@@ -2,7 +2,7 @@
 patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
-                    [--cpu-images 3] [--no-cpu] [--gemm f16|i8] [--lanes N]
+                    [--cpu-images 3] [--no-cpu] [--gemm i8|f16] [--lanes N]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
@@ -25,22 +25,28 @@ sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
 KERNELS = {
-    "f16": "k_mmq16 (Q8_0 x Q8_1 GEMM: exact int8-valued block dots and the dx*dw scale "
-           "tile on v_mfma_f32_32x32x16_f16; priced against the int8 peak)",
-    "i8": "k_mmq (Q8_0 x Q8_1 GEMM: v_mfma_i32_32x32x32_i8 block dots, VALU rescale)",
+    "i8": "k_mmq16<int8> (Q8_0 x Q8_1 GEMM: int8 quants by LDS DMA, v_mfma_i32_32x32x32_i8 "
+          "block dots, dx*dw scale tile on v_mfma_f32_32x32x8_f16, one convert + fma per "
+          "element and block; priced against the int8 peak)",
+    "f16": "k_mmq16<f16> (Q8_0 x Q8_1 GEMM: f16-coded quants, block dots on two "
+           "v_mfma_f32_32x32x16_f16, scale tile on v_mfma_f32_32x32x8_f16; priced against "
+           "the int8 peak)",
 }
 
-
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mmq16_vision_b32_traffic.json")
+TRAFFIC_FILES = {
+    "i8": os.path.join(ROOT, "profiles", "mmq_i8_vision_b32_traffic.json"),
+    "f16": os.path.join(ROOT, "profiles", "mmq16_vision_b32_traffic.json"),
+}
 
 
 def traffic_per_launch(gemm):
     """HBM bytes per GEMM launch of this workload, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated on a copy kernel);
     None when not measured for this kernel."""
-    if gemm != "f16" or not os.path.exists(TRAFFIC_FILE):
+    path = TRAFFIC_FILES.get(gemm)
+    if not path or not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         return int(json.load(f)["bytes_per_launch"])
 
 
@@ -59,9 +65,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (a plain copy kernel "
                          "for calibrating HBM byte counters) and exit")
-    ap.add_argument("--gemm", choices=["f16", "i8"], default="f16",
-                    help="GEMM kernel: f16-MFMA block dots + scale tile (default) or "
-                         "int8-MFMA block dots with VALU rescale; same bits")
+    ap.add_argument("--gemm", choices=["i8", "f16"], default="i8",
+                    help="GEMM quant format: int8 quants on the int8 MFMA (default) or "
+                         "f16-coded quants on the f16 MFMA; same bits")
     ap.add_argument("--lanes", type=int, default=0,
                     help="row ranges (whole images) run concurrently on their own streams "
                          "(1..4; default: the library's)")

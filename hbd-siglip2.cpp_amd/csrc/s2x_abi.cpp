@@ -204,13 +204,13 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
     hipError_t e = repack_into(w_raw, wv, s);
     if (e != hipSuccess) return hip_fail(e, "repack launch");
     Q81Out o;
-    o.qh = (_Float16 *)(ws + L.qh_off);
+    o.qs = (int8_t *)(ws + L.xq_off);
     o.dT = (uint16_t *)(ws + L.dT_off);
     o.ldT = mmq16_ld_dx(M);
     e = launch_quantize_q8_1(x, K, M, ldx, K_pad, o, s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
-    e = launch_mmq_f16(wv, o.qh, o.dT, o.ldT, M, y, N, p, s);
+    e = launch_mmq_i8(wv, o.qs, o.dT, o.ldT, M, y, N, p, s);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
 }
 

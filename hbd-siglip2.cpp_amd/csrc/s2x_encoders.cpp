@@ -184,15 +184,16 @@ struct Tower {
     std::vector<DevLayer> layers;
     hipStream_t own = nullptr, stream = nullptr;
     DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid, rowmap;
-    DevBuf qs2, ds2;  // f16 GEMM: the fc1 epilogue's Q8_1 output (fc2 input)
+    DevBuf qs2, ds2;  // the fc1 epilogue's Q8_1 output (fc2 input)
     GemmTiming timing;
     // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
     bool attn_f64 = false;
-    // GEMM variant: f16-coded operands on f16 MFMA (true) or int8 MFMA.  The
-    // quantized activations in `qs` are f16 or int8 accordingly, and `ds`
-    // holds the transposed fp16 scales [KB][mmq16_ld_dx(M)] or the
-    // block_q8_1 scale words [M][KB].
-    bool gemm_f16 = true;
+    // GEMM variant: int8 quants on v_mfma_i32_32x32x32_i8 (true, default) or
+    // f16-coded quants on v_mfma_f32_32x32x16_f16; same bits.  The quantized
+    // activations in `qs` / `qs2` are int8 or f16 accordingly; `ds` / `ds2`
+    // hold the transposed fp16 scales [KB][mmq16_ld_dx(M)].
+    bool gemm_i8 = true;
+    int64_t qbytes() const { return gemm_i8 ? 1 : 2; }
     // The encoder blocks of a batch run as up to MAX_LANES independent row
     // ranges (whole segments), each on a stream of its own: while one
     // lane's GEMM drains its last, partly filled round of tiles, the other
@@ -251,23 +252,32 @@ struct Tower {
     // GEMM with optional event timing; k_logical excludes the K padding.
     int gemm(const s2x_weight *w, int64_t M, float *y, int64_t ldy, const EpiParams &e,
              int64_t k_logical, bool from_qs2 = false) {
-        if (gemm_f16) {
-            const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
-            return gemm_rows(w, xq.as<_Float16>(), xd.as<uint16_t>(), mmq16_ld_dx(M), M, y, ldy,
-                             e, k_logical, stream);
-        }
-        return timed(w, M, k_logical, stream, [&] {
-            return launch_mmq(w->view, qs.as<int8_t>(), ds.as<uint32_t>(), M, y, ldy, e, stream);
-        });
+        const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
+        return gemm_rows(w, xq.as<uint8_t>(), xd.as<uint16_t>(), mmq16_ld_dx(M), M, y, ldy, e,
+                         k_logical, stream);
     }
-    // f16 GEMM over rows whose quants start at xh and transposed scales at
-    // xdT (row stride ld_dx of the whole batch), on stream st.
-    int gemm_rows(const s2x_weight *w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+    // GEMM over rows whose quants start at xq and transposed scales at xdT
+    // (row stride ld_dx of the whole batch), on stream st.
+    int gemm_rows(const s2x_weight *w, const uint8_t *xq, const uint16_t *xdT, int64_t ld_dx,
                   int64_t M, float *y, int64_t ldy, const EpiParams &e, int64_t k_logical,
                   hipStream_t st) {
         return timed(w, M, k_logical, st, [&] {
-            return launch_mmq_f16(w->view, xh, xdT, ld_dx, M, y, ldy, e, st);
+            return gemm_i8 ? launch_mmq_i8(w->view, reinterpret_cast<const int8_t *>(xq), xdT,
+                                           ld_dx, M, y, ldy, e, st)
+                           : launch_mmq_f16(w->view, reinterpret_cast<const _Float16 *>(xq), xdT,
+                                            ld_dx, M, y, ldy, e, st);
         });
+    }
+    // Q8_1 planes of rows starting at quant bytes q and scale column d.
+    Q81Out qplanes(uint8_t *q, uint16_t *d, int64_t ld) const {
+        Q81Out o;
+        if (gemm_i8)
+            o.qs = reinterpret_cast<int8_t *>(q);
+        else
+            o.qh = reinterpret_cast<_Float16 *>(q);
+        o.dT = d;
+        o.ldT = ld;
+        return o;
     }
     template <class Launch>
     int timed(const s2x_weight *w, int64_t M, int64_t k_logical, hipStream_t st, Launch &&launch) {
@@ -287,22 +297,9 @@ struct Tower {
     }
 
     // Quantized-activation planes for a GEMM over M rows.
-    Q81Out qout(int64_t M) {
-        Q81Out o;
-        if (gemm_f16) {
-            o.qh = qs.as<_Float16>();
-            o.dT = ds.as<uint16_t>();
-            o.ldT = mmq16_ld_dx(M);
-        } else {
-            o.qs = qs.as<int8_t>();
-            o.ds = ds.as<uint32_t>();
-        }
-        return o;
-    }
+    Q81Out qout(int64_t M) { return qplanes(qs.as<uint8_t>(), ds.as<uint16_t>(), mmq16_ld_dx(M)); }
     static size_t ds_bytes(int64_t M, int64_t kmax) {
-        const size_t words = sizeof(uint32_t) * (size_t)(M * (kmax / QK_));
-        const size_t trans = sizeof(uint16_t) * (size_t)(mmq16_ld_dx(M) * (kmax / QK_));
-        return words > trans ? words : trans;
+        return sizeof(uint16_t) * (size_t)(mmq16_ld_dx(M) * (kmax / QK_));
     }
 
     int quantize(const float *src, int64_t K, int64_t M, int64_t ldx, int64_t K_pad) {
@@ -319,15 +316,16 @@ struct Tower {
     int reserve(int64_t M, int64_t n_seg, int64_t max_len) {
         const int64_t kmax = F_pad > H ? F_pad : H;
         S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
-        S2X_TRY(ensure(qs, 2 * (size_t)(M * kmax), stream));  // f16 or int8 quants
+        S2X_TRY(ensure(qs, 2 * (size_t)(M * kmax), stream));  // int8 or f16 quants
         S2X_TRY(ensure(ds, ds_bytes(M, kmax), stream));
         S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
-        if (gemm_f16) {
+        if (!attn_f64) {
             S2X_TRY(ensure(qs2, 2 * (size_t)(M * F_pad), stream));
-            S2X_TRY(ensure(ds2, 2 * (size_t)(mmq16_ld_dx(M) * (F_pad / QK_)), stream));
+            S2X_TRY(ensure(ds2, ds_bytes(M, F_pad), stream));
+        } else {
+            S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
         }
-        if (!gemm_f16 || attn_f64) S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
         S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
         S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
         S2X_TRY(ensure(rowmap, sizeof(int32_t) * (size_t)M, stream));
@@ -403,12 +401,9 @@ struct Tower {
         const int64_t Mp = r1 - r0, ld = mmq16_ld_dx(M);
         if (Mp == 0) return S2X_OK;
         float *xp = x.as<float>() + r0 * H;
-        _Float16 *q1 = qs.as<_Float16>() + r0 * H, *q2 = qs2.as<_Float16>() + r0 * F_pad;
+        uint8_t *q1 = qs.as<uint8_t>() + r0 * H * qbytes(), *q2 = qs2.as<uint8_t>() + r0 * F_pad * qbytes();
         uint16_t *d1 = ds.as<uint16_t>() + r0, *d2 = ds2.as<uint16_t>() + r0;
-        Q81Out qa;
-        qa.qh = q1;
-        qa.dT = d1;
-        qa.ldT = ld;
+        const Q81Out qa = qplanes(q1, d1, ld);
         const AttnLayout ALs = attn_sublayout(AL, s0, s1);
         const int32_t *rm = rowmap.as<int32_t>() + r0;
         hipError_t e;
@@ -426,7 +421,10 @@ struct Tower {
             e = launch_layernorm(xp, H, Mp, H, L.ln2_w, L.ln2_b, eps, &qa, nullptr, H, st);
             if (e != hipSuccess) return hip_fail(e, "layernorm launch");
             EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
-            up.q_out = q2;
+            if (gemm_i8)
+                up.q_out8 = reinterpret_cast<int8_t *>(q2);
+            else
+                up.q_out = reinterpret_cast<_Float16 *>(q2);
             up.q_dT = d2;
             up.q_kpad = F_pad;
             up.q_ld = ld;
@@ -441,7 +439,7 @@ struct Tower {
         const AttnLayout AL = attn_layout(n_seg, max_len, n_head, d_head);
         const float kq_scale = 1.0f / std::sqrt((float)d_head);
         float *xp = x.as<float>();
-        if (gemm_f16 && !attn_f64) {
+        if (!attn_f64) {
             S2X_TRY(attn_ws_ready(AL));
             const std::vector<int64_t> b = lane_bounds(M, n_seg);
             const int nl = (int)b.size() - 1;
@@ -705,7 +703,7 @@ int s2x_vision_set_gemm_variant(s2x_vision *v, int variant) {
     if (variant != S2X_GEMM_F16_MFMA && variant != S2X_GEMM_I8_MFMA)
         return fail(S2X_ERR_INVALID_ARG, "gemm variant %d unknown", variant);
     S2X_HIP_TRY(hipStreamSynchronize(v->t.stream));  // the activation buffer changes format
-    v->t.gemm_f16 = variant == S2X_GEMM_F16_MFMA;
+    v->t.gemm_i8 = variant == S2X_GEMM_I8_MFMA;
     return S2X_OK;
 }
 

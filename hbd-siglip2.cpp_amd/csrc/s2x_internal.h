@@ -63,16 +63,16 @@ inline hipError_t repack_into(const void *raw, const WeightView &v, hipStream_t 
                               const_cast<uint16_t *>(v.dT), v.ldT, s);
 }
 
-// Workspace of the drop-in MUL_MAT: repacked W, then X as f16-coded Q8_1
+// Workspace of the drop-in MUL_MAT: repacked W, then X as int8 Q8_1
 // (quants [M][K_pad] and transposed scales [KB][mmq16_ld_dx(M)]).
 struct MulMatWs {
-    size_t w_off, qh_off, dT_off, total;
+    size_t w_off, xq_off, dT_off, total;
 };
 inline MulMatWs mul_mat_ws_layout(int64_t K_pad, int64_t N, int64_t M) {
     MulMatWs L;
     L.w_off = 0;
-    L.qh_off = weight_planes_bytes(K_pad, N);
-    L.dT_off = L.qh_off + (size_t)round_up_i(M * K_pad * 2, 256);
+    L.xq_off = weight_planes_bytes(K_pad, N);
+    L.dT_off = L.xq_off + (size_t)round_up_i(M * K_pad, 256);  // int8 quants
     L.total = L.dT_off + (size_t)round_up_i((K_pad / QK_) * mmq16_ld_dx(M) * 2, 256);
     return L;
 }

@@ -57,9 +57,11 @@ struct EpiParams {
     _Float16      *q, *k, *vt;
     const int32_t *rowmap;
     int            n_head, d_head, d_pad, dv_pad, len_pad;
-    // EPI_GELU_Q81: quants [M][q_kpad] (columns N..q_kpad-1 quantize zeros)
-    // and transposed scales [q_kpad/32][q_ld]
+    // EPI_GELU_Q81: quants [M][q_kpad] (columns N..q_kpad-1 quantize zeros),
+    // f16 (q_out, f16 GEMM) or int8 (q_out8, int8 GEMM), and transposed
+    // scales [q_kpad/32][q_ld]
     _Float16 *q_out;
+    int8_t   *q_out8;
     uint16_t *q_dT;
     int64_t   q_kpad, q_ld;
 };
@@ -86,6 +88,12 @@ hipError_t launch_mmq(const WeightView &w, const int8_t *xq, const uint32_t *xds
 hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
                           int64_t ld_dx, int64_t M, float *y, int64_t ldy,
                           const EpiParams &epi, hipStream_t stream);
+// The same kernel over int8 quants (w.qs, xq [M][K_pad]): one
+// v_mfma_i32_32x32x32_i8 per block dot, then (float) I in the fma.  Same
+// bits as launch_mmq_f16 and launch_mmq.
+hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *xdT,
+                         int64_t ld_dx, int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                         hipStream_t stream);
 
 // a4: LayerNorm (+ Q8_1).  q may be null (no quantized output), y may be
 // null (no f32 output); at least one is set.

@@ -48,35 +48,44 @@ namespace s2x {
 namespace mmq16 {
 
 constexpr int BN = (int)MMQ16_BN;
-constexpr int ROWB = QK * 2;  // one block of f16 quants per row and stage
 constexpr int GM = 8;         // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true>
+template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true, bool I8_ = false>
 struct Cfg {
     static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
+    static constexpr bool I8 = I8_;      // int8 quants, v_mfma_i32_32x32x32_i8 block dots
+    static constexpr int ROWB = QK * (I8 ? 1 : 2);  // bytes of one block of one row
+    static constexpr int CH = ROWB / 16;            // 16-byte chunks per row and block
     static constexpr bool PIPE = PIPE_;  // next block's fragments read during this block's MFMAs
     static constexpr bool SKEW = SKEW_;  // a subtile's fmas issued after the next one's MFMAs
     static constexpr int WGM = BM / (32 * TM);          // waves along M (2 along N)
     static constexpr int NWAVE = WGM * 2;
     static constexpr int NT = NWAVE * WAVE;
-    static constexpr int XI = BM * 4 / NT;              // X DMA instructions per stage
-    static constexpr int WI = BN * 4 / NT;              // W DMA instructions per stage
+    // quant DMA instructions per thread and stage: the stage's X chunks
+    // then its W chunks, NT per instruction (each wave's 64 are all X or all W)
+    static constexpr int QI = (BM + BN) * CH / NT;
     static constexpr int X_BYTES = BM * ROWB;
     static constexpr int DX_OFF = X_BYTES + BN * ROWB;  // BM fp16 X scales
     static constexpr int DW_OFF = DX_OFF + BM * 2;      // BN fp16 W scales
     static constexpr int Z_OFF = DW_OFF + BN * 2;       // 16 zero bytes
     static constexpr int STAGE = Z_OFF + 16;
-    static constexpr int LDS = NS * STAGE;
-    static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && XI >= 1 && WI >= 1 && BM / 8 <= WAVE && BN / 8 <= WAVE, "config");
+    // the stage ring, or the epilogues' 32 x 144-byte scratch rows per wave
+    static constexpr int LDS = NS * STAGE > NWAVE * 32 * 144 ? NS * STAGE : NWAVE * 32 * 144;
+    static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && QI >= 1 &&
+                      (BM + BN) * CH == QI * NT && (BM * CH) % WAVE == 0 && BM / 8 <= WAVE &&
+                      BN / 8 <= WAVE && (!I8 || TM == 1),
+                  "config");
     static_assert(NS >= 2 && NS <= 4, "wait table / unroll");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int TM>
+template <int TM, bool I8>
 struct FragTM {
-    v8h a[TM][2], b[2][2];  // [subtile][k half]
+    // quant operands: f16 [subtile][k half] (two 32x32x16 MFMAs per block)
+    // or int8 [subtile] (one 32x32x32 MFMA per block)
+    std::conditional_t<I8, v4i, v8h> a[TM][I8 ? 1 : 2], b[2][I8 ? 1 : 2];
     // scale-tile operands (32x32x8 f16 MFMA, k slots 0..3 on lanes 0..31):
     // dword 0 holds the fp16 bits of the row / column scale (0 on lanes
     // 32..63), dword 1 stays zero for the whole loop, so only dword 0 is
@@ -122,18 +131,18 @@ __device__ __forceinline__ void wait_after(int after) {
 template <class C>
 __device__ __forceinline__ void wait_stage(bool scale_wave, int after) {
     if (scale_wave)
-        wait_after<C::XI + C::WI + 1>(after);
+        wait_after<C::QI + 1>(after);
     else
-        wait_after<C::XI + C::WI>(after);
+        wait_after<C::QI>(after);
 }
 
 template <class C, int EPI>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 512 ? 4 : 2))) void k_mmq16(
-    const _Float16 *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
-    const _Float16 *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
+    const uint8_t *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
+    const uint8_t *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
     int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
-    constexpr int BM = C::BM, NS = C::NS, NT = C::NT, TM = C::TM;
-    using Frag = FragTM<TM>;
+    constexpr int BM = C::BM, NS = C::NS, NT = C::NT, TM = C::TM, ROWB = C::ROWB, CH = C::CH;
+    using Frag = FragTM<TM, C::I8>;
     extern __shared__ __align__(16) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -145,28 +154,24 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     tile_coords<GM>(blockIdx.x, gridDim.x, m_tiles, n_tiles, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const int64_t K_pad = (int64_t)KB * QK;
-    const uint32_t row_bytes = (uint32_t)(K_pad * 2);
+    const int64_t row_bytes = K_pad * (C::I8 ? 1 : 2);
 
     // Buffers over this tile's rows: rows past M / N read as zeros (their
-    // outputs are never stored).  Position p (16-byte unit) of a stage's
-    // quant rows holds chunk (p & 3) ^ ((row >> 2) & 3) of row p >> 2.
+    // outputs are never stored).  Position p (16-byte unit) of a stage's X
+    // (then W) rows holds chunk (p % CH) ^ ((row >> 2) & (CH - 1)) of row
+    // p / CH.
     const auto clip = [](int64_t bytes) { return (int)min(bytes, (int64_t)0x7fffffff); };
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(xq + (int64_t)m0 * K_pad), (short)0, clip((int64_t)(M - m0) * K_pad * 2), BUF_DW3);
+        (void *)(xq + (int64_t)m0 * row_bytes), (short)0, clip((int64_t)(M - m0) * row_bytes), BUF_DW3);
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(wq + (int64_t)n0 * K_pad), (short)0, clip((int64_t)(N - n0) * K_pad * 2), BUF_DW3);
-    uint32_t xv[C::XI], wv[C::WI];
+        (void *)(wq + (int64_t)n0 * row_bytes), (short)0, clip((int64_t)(N - n0) * row_bytes), BUF_DW3);
+    uint32_t qv[C::QI];
 #pragma unroll
-    for (int i = 0; i < C::XI; ++i) {
+    for (int i = 0; i < C::QI; ++i) {
         const int p = i * NT + tid;
-        const int row = p >> 2, chunk = (p & 3) ^ ((row >> 2) & 3);
-        xv[i] = (uint32_t)row * row_bytes + (uint32_t)chunk * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < C::WI; ++i) {
-        const int p = i * NT + tid;
-        const int row = p >> 2, chunk = (p & 3) ^ ((row >> 2) & 3);
-        wv[i] = (uint32_t)row * row_bytes + (uint32_t)chunk * 16;
+        const int pr = p < BM * CH ? p : p - BM * CH;  // position within X or W
+        const int row = pr / CH, chunk = (pr % CH) ^ ((row >> 2) & (CH - 1));
+        qv[i] = (uint32_t)(row * row_bytes) + (uint32_t)chunk * 16;
     }
     // wave 0: X scales (BM/8 lanes x 8), wave 1: W scales (BN/8 lanes x 8)
     const bool scale_wave = wave < 2;
@@ -185,10 +190,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
         uint8_t *sb = lds + buf * C::STAGE;
         const uint32_t koff = (uint32_t)kb * ROWB;
 #pragma unroll
-        for (int i = 0; i < C::XI; ++i) dma16(xr, xv[i], koff, sb + (i * NT + wave * 64) * 16);
-#pragma unroll
-        for (int i = 0; i < C::WI; ++i)
-            dma16(wr, wv[i], koff, sb + C::X_BYTES + (i * NT + wave * 64) * 16);
+        for (int i = 0; i < C::QI; ++i) {
+            const int p0 = i * NT + wave * 64;  // wave-uniform: the 64 chunks are X or W
+            dma16(p0 < BM * CH ? xr : wr, qv[i], koff, sb + p0 * 16);
+        }
         if (scale_wave && s_lane) dma16(sr, (uint32_t)lane * 16, (uint32_t)kb * s_stride, sb + s_dst);
     };
 
@@ -204,7 +209,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
     const int lr = lane & 31, lh = lane >> 5;
-    const int sw = (lr >> 2) & 3;  // chunk permutation of the rows this lane reads
+    const int sw = (lr >> 2) & (CH - 1);  // chunk permutation of the rows this lane reads
+    // k slots 8 lh .. 8 lh + 7 (f16: of each 16-value half) / 16 lh .. +15 (int8)
     const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
     const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 64 + lr;
     const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
@@ -217,57 +223,84 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     auto load_frag = [&](const uint8_t *sb, Frag &f) {
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
-            f.a[a][0] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c0);
-            f.a[a][1] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c1);
+            if constexpr (C::I8) {
+                f.a[a][0] = *reinterpret_cast<const v4i *>(sb + xo + a * 32 * ROWB + c0);
+            } else {
+                f.a[a][0] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c0);
+                f.a[a][1] = *reinterpret_cast<const v8h *>(sb + xo + a * 32 * ROWB + c1);
+            }
         }
         f.sx[0][0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
         if constexpr (TM == 2) f.sx[1][0] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            f.b[b][0] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c0);
-            f.b[b][1] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c1);
+            if constexpr (C::I8) {
+                f.b[b][0] = *reinterpret_cast<const v4i *>(sb + wo + b * 32 * ROWB + c0);
+            } else {
+                f.b[b][0] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c0);
+                f.b[b][1] = *reinterpret_cast<const v8h *>(sb + wo + b * 32 * ROWB + c1);
+            }
         }
         f.sw[0][0] = *reinterpret_cast<const uint16_t *>(sb + dwo0);
         f.sw[1][0] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
     };
 
-    // One block of K.  Subtile k = 2a + b gets I (two MFMAs) and the scale
-    // tile (one MFMA); acc = fmaf(I, s, acc) for subtile k runs after subtile
-    // k+1's MFMAs are issued, and subtile 3's in the next block, so the VALU
-    // work overlaps the matrix pipe.  Each acc element still receives its
-    // fmas in block order.
-    v16f Ip, Sp;
+    // One block of K.  Subtile k = 2a + b gets I (f16: two MFMAs, exact f32;
+    // int8: one MFMA, exact int32) and the scale tile (one MFMA);
+    // acc = fmaf(I, s, acc) for subtile k runs after subtile k+1's MFMAs are
+    // issued, and subtile 3's in the next block, so the VALU work overlaps
+    // the matrix pipe.  Each acc element still receives its fmas in block
+    // order.
+    using IT = std::conditional_t<C::I8, v16i, v16f>;
+    IT Ip;
+    v16f Sp;
     bool pending = false;
     auto mma = [&](const Frag &f) {
         const v16f zero = {};
+        const v16i zero_i = {};
 #pragma unroll
         for (int k = 0; k < 2 * TM; ++k) {
             const int a = k >> 1, b = k & 1;
-            v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][0], f.b[b][0], zero, 0, 0, 0);
-            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(
-                __builtin_bit_cast(v4h, f.sx[a]), __builtin_bit_cast(v4h, f.sw[b]), zero, 0, 0, 0);
-            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
+            IT I;
+            v16f S;
+            if constexpr (C::I8) {
+                I = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a][0], f.b[b][0], zero_i, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x8f16(
+                    __builtin_bit_cast(v4h, f.sx[a]), __builtin_bit_cast(v4h, f.sw[b]), zero, 0, 0, 0);
+            } else {
+                I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][0], f.b[b][0], zero, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x8f16(
+                    __builtin_bit_cast(v4h, f.sx[a]), __builtin_bit_cast(v4h, f.sw[b]), zero, 0, 0, 0);
+                I = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[a][1], f.b[b][1], I, 0, 0, 0);
+            }
             if constexpr (!C::SKEW) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], S[r], acc[a][b][r]);
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf((float)I[r], S[r], acc[a][b][r]);
                 continue;
             }
             const int pk = (k + 2 * TM - 1) % (2 * TM), pa = pk >> 1, pb = pk & 1;
             if (k > 0 || pending) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf(Ip[r], Sp[r], acc[pa][pb][r]);
+                for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf((float)Ip[r], Sp[r], acc[pa][pb][r]);
             }
             Ip = I;
             Sp = S;
-            // issue order: each MFMA followed by a third of the previous
-            // subtile's fmas, so a wave alone keeps the matrix pipe fed
+            // issue order: each MFMA followed by its share of the previous
+            // subtile's VALU work, so a wave alone keeps the matrix pipe fed
             if (k > 0 || pending) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                if constexpr (C::I8) {  // 2 MFMAs, 16 converts + 16 fmas
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                } else {  // 3 MFMAs, 16 fmas
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
             }
         }
         pending = true;
@@ -340,7 +373,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     }
     if constexpr (C::SKEW) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf(Ip[r], Sp[r], acc[TM - 1][1][r]);
+        for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf((float)Ip[r], Sp[r], acc[TM - 1][1][r]);
     }
 
     if constexpr (EPI == EPI_GELU_Q81) {
@@ -376,16 +409,27 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
             a = fmaxf(a, dpp_f<0xb1>(a));  // partner lane (xor 1)
             const float d = a / 127.0f;
             const float inv = a != 0.0f ? 127.0f / a : 0.0f;
-            v8h q0, q1;
+            int qi[16];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                q0[j] = (_Float16)q8_round(v[j], inv);
-                q1[j] = (_Float16)q8_round(v[8 + j], inv);
-            }
+            for (int j = 0; j < 16; ++j) qi[j] = q8_round(v[j], inv);
             if (m < M) {
-                v8h *dst = reinterpret_cast<v8h *>(epi.q_out + (int64_t)m * epi.q_kpad + nb + half * 16);
-                dst[0] = q0;
-                dst[1] = q1;
+                const int64_t off = (int64_t)m * epi.q_kpad + nb + half * 16;
+                if constexpr (C::I8) {
+                    *reinterpret_cast<uint4 *>(epi.q_out8 + off) =
+                        make_uint4(pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7]),
+                                   pack4_i8(qi[8], qi[9], qi[10], qi[11]),
+                                   pack4_i8(qi[12], qi[13], qi[14], qi[15]));
+                } else {
+                    v8h q0, q1;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        q0[j] = (_Float16)qi[j];
+                        q1[j] = (_Float16)qi[8 + j];
+                    }
+                    v8h *dst = reinterpret_cast<v8h *>(epi.q_out + off);
+                    dst[0] = q0;
+                    dst[1] = q1;
+                }
                 if (half == 0) epi.q_dT[(int64_t)(nb / QK) * epi.q_ld + m] = f32_to_f16_bits(d);
             }
         }
@@ -479,7 +523,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
 }
 
 template <class C, int EPI>
-hipError_t run(const WeightView &w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+hipError_t run(const WeightView &w, const void *xq, const uint16_t *xdT, int64_t ld_dx,
                int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
     const int m_tiles = (int)((M + C::BM - 1) / C::BM), n_tiles = (int)((w.N + BN - 1) / BN);
     auto kern = k_mmq16<C, EPI>;
@@ -491,14 +535,16 @@ hipError_t run(const WeightView &w, const _Float16 *xh, const uint16_t *xdT, int
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(m_tiles * n_tiles), dim3(C::NT), C::LDS, stream, xh, xdT,
-                       ld_dx, w.qh, w.dT, w.ldT, (int)M, (int)w.N, (int)(w.K_pad / QK), y, ldy,
-                       epi);
+    const void *wq = C::I8 ? (const void *)w.qs : (const void *)w.qh;
+    hipLaunchKernelGGL(kern, dim3(m_tiles * n_tiles), dim3(C::NT), C::LDS, stream,
+                       reinterpret_cast<const uint8_t *>(xq), xdT, ld_dx,
+                       reinterpret_cast<const uint8_t *>(wq), w.dT, w.ldT, (int)M, (int)w.N,
+                       (int)(w.K_pad / QK), y, ldy, epi);
     return hipGetLastError();
 }
 
 template <class C>
-hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT, int64_t ld_dx,
+hipError_t dispatch(const WeightView &w, const void *xh, const uint16_t *xdT, int64_t ld_dx,
                     int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
     switch (epi.kind) {
     case EPI_NONE: return run<C, EPI_NONE>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
@@ -506,9 +552,9 @@ hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT
     case EPI_BIAS_GELU: return run<C, EPI_BIAS_GELU>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_BIAS_RESID: return run<C, EPI_BIAS_RESID>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_GELU_Q81:
-        if (C::TM != 1 || !epi.q_out || !epi.q_dT || !epi.bias || epi.q_kpad % QK ||
+        if (C::TM != 1 || !(C::I8 ? (void *)epi.q_out8 : (void *)epi.q_out) || !epi.q_dT || !epi.bias || epi.q_kpad % QK ||
             epi.q_kpad < w.N || epi.q_kpad - w.N >= QK || epi.q_ld < mmq16_ld_dx(M) ||
-            (reinterpret_cast<uintptr_t>(epi.q_out) & 15))
+            (reinterpret_cast<uintptr_t>(C::I8 ? (void *)epi.q_out8 : (void *)epi.q_out) & 15))
             return hipErrorInvalidValue;
         return run<C, EPI_GELU_Q81>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_QKV:
@@ -522,14 +568,28 @@ hipError_t dispatch(const WeightView &w, const _Float16 *xh, const uint16_t *xdT
 
 }  // namespace mmq16
 
+static bool mmq_args_ok(const WeightView &w, const void *xq, const uint16_t *xdT, int64_t ld_dx,
+                        int64_t M) {
+    return w.dT && xq && xdT && ld_dx >= mmq16_ld_dx(M) && !(ld_dx & 7) &&
+           w.ldT >= mmq16_ld_dw(w.N) && !(w.ldT & 7) && !(w.K_pad % QK) && w.K_pad != 0 &&
+           !(reinterpret_cast<uintptr_t>(xq) & 15) && !(reinterpret_cast<uintptr_t>(xdT) & 15);
+}
+
 hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
                           int64_t ld_dx, int64_t M, float *y, int64_t ldy,
                           const EpiParams &epi, hipStream_t stream) {
     if (M == 0 || w.N == 0) return hipSuccess;
-    if (!w.qh || !w.dT || !xh || !xdT || ld_dx < mmq16_ld_dx(M) || (ld_dx & 7) ||
-        w.ldT < mmq16_ld_dw(w.N) || (w.ldT & 7) || (w.K_pad % QK) || w.K_pad == 0)
-        return hipErrorInvalidValue;
+    if (!w.qh || !mmq_args_ok(w, xh, xdT, ld_dx, M)) return hipErrorInvalidValue;
     return mmq16::dispatch<mmq16::Cfg<128, 3, false, 1>>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+}
+
+hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *xdT,
+                         int64_t ld_dx, int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                         hipStream_t stream) {
+    if (M == 0 || w.N == 0) return hipSuccess;
+    if (!w.qs || !mmq_args_ok(w, xq, xdT, ld_dx, M)) return hipErrorInvalidValue;
+    return mmq16::dispatch<mmq16::Cfg<128, 3, false, 1, true, true>>(w, xq, xdT, ld_dx, M, y, ldy,
+                                                                     epi, stream);
 }
 
 }  // namespace s2x

@@ -278,10 +278,11 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream);
 /* Attention precision: 0 (default) = f16-MFMA flash attention with f32
  * softmax and an exact f16 hi/lo split of P; 1 = s2x_attn_fp64. */
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
-/* GEMM kernel: S2X_GEMM_F16_MFMA (default; block dots and the dx*dw scale
- * tile on f16 MFMA, one VALU fma per element and block) or S2X_GEMM_I8_MFMA
- * (v_mfma_i32_32x32x32_i8 block dots, VALU convert + scale + fma).  Both
- * give the same bits. */
+/* GEMM kernel of the towers: S2X_GEMM_I8_MFMA (default; int8 quants,
+ * v_mfma_i32_32x32x32_i8 block dots, the dx*dw scale tile on an f16 MFMA,
+ * one VALU convert + fma per element and block) or S2X_GEMM_F16_MFMA (the
+ * same kernel over f16-coded quants: block dots on two f16 MFMAs, one VALU
+ * fma).  Both give the same bits. */
 enum { S2X_GEMM_F16_MFMA = 0, S2X_GEMM_I8_MFMA = 1 };
 int s2x_vision_set_gemm_variant(s2x_vision *v, int variant);
 /* Concurrency of a batch (f16 GEMM + flash attention path): the encoder
