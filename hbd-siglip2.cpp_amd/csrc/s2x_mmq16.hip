@@ -47,13 +47,15 @@
 namespace s2x {
 namespace mmq16 {
 
-constexpr int BN = (int)MMQ16_BN;
 constexpr int GM = 8;         // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true, bool I8_ = false>
+template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true, bool I8_ = false,
+          int TN_ = 2>
 struct Cfg {
     static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
+    static constexpr int TN = TN_;                      // TN: 32-column subtiles per wave
+    static constexpr int BN = 2 * 32 * TN;              // two waves along N
     static constexpr bool I8 = I8_;      // int8 quants, v_mfma_i32_32x32x32_i8 block dots
     static constexpr int ROWB = QK * (I8 ? 1 : 2);  // bytes of one block of one row
     static constexpr int CH = ROWB / 16;            // 16-byte chunks per row and block
@@ -72,7 +74,7 @@ struct Cfg {
     static constexpr int STAGE = Z_OFF + 16;
     // the stage ring, or the epilogues' 32 x 144-byte scratch rows per wave
     static constexpr int LDS = NS * STAGE > NWAVE * 32 * 144 ? NS * STAGE : NWAVE * 32 * 144;
-    static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && QI >= 1 &&
+    static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && (TN == 1 || TN == 2) && QI >= 1 &&
                       (BM + BN) * CH == QI * NT && (BM * CH) % WAVE == 0 && BM / 8 <= WAVE &&
                       BN / 8 <= WAVE && (!I8 || TM == 1),
                   "config");
@@ -81,19 +83,19 @@ struct Cfg {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int TM, bool I8>
+template <int TM, int TN, bool I8>
 struct FragTM {
     // quant operands: f16 [subtile][k half] (two 32x32x16 MFMAs per block)
     // or int8 [subtile] (one 32x32x32 MFMA per block)
-    std::conditional_t<I8, v4i, v8h> a[TM][I8 ? 1 : 2], b[2][I8 ? 1 : 2];
+    std::conditional_t<I8, v4i, v8h> a[TM][I8 ? 1 : 2], b[TN][I8 ? 1 : 2];
     // scale-tile operands (32x32x8 f16 MFMA, k slots 0..3 on lanes 0..31):
     // dword 0 holds the fp16 bits of the row / column scale (0 on lanes
     // 32..63), dword 1 stays zero for the whole loop, so only dword 0 is
     // reloaded per block
-    v2i sx[TM], sw[2];
+    v2i sx[TM], sw[TN];
     __device__ void zero_scales() {
         for (int a = 0; a < TM; ++a) sx[a] = v2i{0, 0};
-        for (int b = 0; b < 2; ++b) sw[b] = v2i{0, 0};
+        for (int b = 0; b < TN; ++b) sw[b] = v2i{0, 0};
     }
 };
 
@@ -137,12 +139,13 @@ __device__ __forceinline__ void wait_stage(bool scale_wave, int after) {
 }
 
 template <class C, int EPI>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 512 ? 4 : 2))) void k_mmq16(
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 1 ? 4 : 2))) void k_mmq16(
     const uint8_t *__restrict__ xq, const uint16_t *__restrict__ xdT, int64_t ld_dx,
     const uint8_t *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ld_dw, int M,
     int N, int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
-    constexpr int BM = C::BM, NS = C::NS, NT = C::NT, TM = C::TM, ROWB = C::ROWB, CH = C::CH;
-    using Frag = FragTM<TM, C::I8>;
+    constexpr int BM = C::BM, BN = C::BN, NS = C::NS, NT = C::NT, TM = C::TM, TN = C::TN;
+    constexpr int ROWB = C::ROWB, CH = C::CH;
+    using Frag = FragTM<TM, TN, C::I8>;
     extern __shared__ __align__(16) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -200,11 +203,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     // the zero words read by lanes 32..63 for the scale operands
     if (tid < NS) *reinterpret_cast<v4i *>(lds + tid * C::STAGE + C::Z_OFF) = v4i{0, 0, 0, 0};
 
-    float acc[TM][2][16];
+    float acc[TM][TN][16];
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < TN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
@@ -212,13 +215,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     const int sw = (lr >> 2) & (CH - 1);  // chunk permutation of the rows this lane reads
     // k slots 8 lh .. 8 lh + 7 (f16: of each 16-value half) / 16 lh .. +15 (int8)
     const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
-    const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 64 + lr;
+    const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 32 * TN + lr;
     const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
     // scale operands: k slot 0 (lanes 0..31) holds the scale, the rest zeros
     const int dxo0 = lh ? C::Z_OFF : C::DX_OFF + xrow0 * 2;
     const int dxo1 = lh ? C::Z_OFF : C::DX_OFF + (xrow0 + 32 * (TM - 1)) * 2;
     const int dwo0 = lh ? C::Z_OFF : C::DW_OFF + wcol0 * 2;
-    const int dwo1 = lh ? C::Z_OFF : C::DW_OFF + (wcol0 + 32) * 2;
+    const int dwo1 = lh ? C::Z_OFF : C::DW_OFF + (wcol0 + 32 * (TN - 1)) * 2;
 
     auto load_frag = [&](const uint8_t *sb, Frag &f) {
 #pragma unroll
@@ -233,7 +236,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
         f.sx[0][0] = *reinterpret_cast<const uint16_t *>(sb + dxo0);
         if constexpr (TM == 2) f.sx[1][0] = *reinterpret_cast<const uint16_t *>(sb + dxo1);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < TN; ++b) {
             if constexpr (C::I8) {
                 f.b[b][0] = *reinterpret_cast<const v4i *>(sb + wo + b * 32 * ROWB + c0);
             } else {
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
             }
         }
         f.sw[0][0] = *reinterpret_cast<const uint16_t *>(sb + dwo0);
-        f.sw[1][0] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
+        if constexpr (TN == 2) f.sw[1][0] = *reinterpret_cast<const uint16_t *>(sb + dwo1);
     };
 
     // One block of K.  Subtile k = 2a + b gets I (f16: two MFMAs, exact f32;
@@ -259,8 +262,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
         const v16f zero = {};
         const v16i zero_i = {};
 #pragma unroll
-        for (int k = 0; k < 2 * TM; ++k) {
-            const int a = k >> 1, b = k & 1;
+        for (int k = 0; k < TM * TN; ++k) {
+            const int a = k / TN, b = k % TN;
             IT I;
             v16f S;
             if constexpr (C::I8) {
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf((float)I[r], S[r], acc[a][b][r]);
                 continue;
             }
-            const int pk = (k + 2 * TM - 1) % (2 * TM), pa = pk >> 1, pb = pk & 1;
+            const int pk = (k + TM * TN - 1) % (TM * TN), pa = pk / TN, pb = pk % TN;
             if (k > 0 || pending) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf((float)Ip[r], Sp[r], acc[pa][pb][r]);
@@ -373,7 +376,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
     }
     if constexpr (C::SKEW) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[TM - 1][1][r] = fmaf((float)Ip[r], Sp[r], acc[TM - 1][1][r]);
+        for (int r = 0; r < 16; ++r) acc[TM - 1][TN - 1][r] = fmaf((float)Ip[r], Sp[r], acc[TM - 1][TN - 1][r]);
     }
 
     if constexpr (EPI == EPI_GELU_Q81) {
@@ -388,8 +391,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
         const int row = lane >> 1, half = lane & 1;
         const int m = m0 + wm * 32 + row;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int nb = n0 + wn * 64 + b * 32;  // first column of this quant block
+        for (int b = 0; b < TN; ++b) {
+            const int nb = n0 + wn * 32 * TN + b * 32;  // first column of this quant block
             if (nb >= epi.q_kpad) continue;        // wave-uniform
             const int n = nb + lr;
             const float bias = n < N ? epi.bias[n] : 0.0f;
@@ -440,7 +443,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
         // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad] or
         // V^T [seg][head][dv_pad][pos]; padding slots are not written
         const int H = epi.n_head * epi.d_head;
-        if (TM == 1 && n0 + BN <= 2 * H && H % BN == 0 && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
+        if constexpr (TM == 1 && TN == 2) {
+        if (n0 + BN <= 2 * H && H % BN == 0 && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
             // a Q or K tile (the q|k|v boundaries fall on tile edges): the
             // wave's 32 x 64 f16 tile goes through LDS so that each 8-column
             // chunk of a row -- 8 consecutive d of one head -- leaves as one
@@ -471,8 +475,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
             }
             return;
         }
+        }
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < TN; ++b) {
             const int n = n0 + wcol0 + b * 32;
             if (n >= N) continue;
             const float bias = epi.bias[n];
@@ -499,7 +504,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < TN; ++b) {
             const int n = n0 + wcol0 + b * 32;
             if (n >= N) continue;
             float bias = 0.0f;
@@ -525,7 +530,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NT >= 
 template <class C, int EPI>
 hipError_t run(const WeightView &w, const void *xq, const uint16_t *xdT, int64_t ld_dx,
                int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
-    const int m_tiles = (int)((M + C::BM - 1) / C::BM), n_tiles = (int)((w.N + BN - 1) / BN);
+    const int m_tiles = (int)((M + C::BM - 1) / C::BM), n_tiles = (int)((w.N + C::BN - 1) / C::BN);
     auto kern = k_mmq16<C, EPI>;
     static bool attr_set = false;  // idempotent; a racing second call repeats it harmlessly
     if (!attr_set) {
@@ -575,12 +580,87 @@ static bool mmq_args_ok(const WeightView &w, const void *xq, const uint16_t *xdT
            !(reinterpret_cast<uintptr_t>(xq) & 15) && !(reinterpret_cast<uintptr_t>(xdT) & 15);
 }
 
+namespace mmq16 {
+
+// Workgroups of config C resident at once on the current device.
+template <class C>
+int64_t resident_tiles() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cached[dev]) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(k_mmq16<C, EPI_NONE>), C::NT, C::LDS) !=
+                hipSuccess)
+            return 0;
+        cached[dev] = cus * per_cu;
+    }
+    return cached[dev];
+}
+
+// The epilogue of rows [r, ...) of a GEMM as a GEMM of its own; false when
+// the row shift cannot be expressed (a residual read modulo resid_rows).
+inline bool shift_rows(const EpiParams &e, int64_t r, float *&y, int64_t ldy, EpiParams &out) {
+    out = e;
+    if (y) y += r * ldy;
+    switch (e.kind) {
+    case EPI_BIAS_RESID:
+        if (e.resid_rows > 0) return r % e.resid_rows == 0;
+        out.resid = e.resid + r * e.ld_resid;
+        return true;
+    case EPI_QKV: out.rowmap = e.rowmap + r; return true;
+    case EPI_GELU_Q81:
+        if (e.q_out) out.q_out = e.q_out + r * e.q_kpad;
+        if (e.q_out8) out.q_out8 = e.q_out8 + r * e.q_kpad;
+        out.q_dT = e.q_dT + r;
+        return true;
+    default: return true;
+    }
+}
+
+// A grid of Big tiles fills the chip in whole rounds of resident
+// workgroups.  When its last round would be less than a fifth full, the
+// rows of that round go to a second launch of Small tiles (a quarter of
+// the work each, so about four times as many run at once); each output
+// tile still accumulates all of K in block order, so the bits are
+// unchanged.  (Measured: a last round that is fuller already runs faster
+// than a full one, and the second launch's own gap and per-block latency
+// then cost more than the split saves.)
+template <class Big, class Small>
+hipError_t launch_tail_split(const WeightView &w, const uint8_t *xq, int64_t row_bytes,
+                             const uint16_t *xdT, int64_t ld_dx, int64_t M, float *y,
+                             int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    const int64_t n_tiles = (w.N + Big::BN - 1) / Big::BN;
+    const int64_t m_tiles = (M + Big::BM - 1) / Big::BM;
+    const int64_t T = m_tiles * n_tiles, S = resident_tiles<Big>();
+    int64_t rows_main = M;
+    if (S > 0 && T > S && T % S != 0 && 5 * (T % S) < S) {
+        const int64_t m_main = (T / S) * S / n_tiles;  // whole Big row tiles in full rounds
+        rows_main = m_main * Big::BM;
+    }
+    EpiParams tail;
+    float *yt = y;
+    if (rows_main >= M || !shift_rows(epi, rows_main, yt, ldy, tail))
+        return dispatch<Big>(w, xq, xdT, ld_dx, M, y, ldy, epi, stream);
+    hipError_t e = dispatch<Big>(w, xq, xdT, ld_dx, rows_main, y, ldy, epi, stream);
+    if (e != hipSuccess) return e;
+    return dispatch<Small>(w, xq + rows_main * row_bytes, xdT + rows_main, ld_dx, M - rows_main,
+                           yt, ldy, tail, stream);
+}
+
+}  // namespace mmq16
+
 hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
                           int64_t ld_dx, int64_t M, float *y, int64_t ldy,
                           const EpiParams &epi, hipStream_t stream) {
     if (M == 0 || w.N == 0) return hipSuccess;
     if (!w.qh || !mmq_args_ok(w, xh, xdT, ld_dx, M)) return hipErrorInvalidValue;
-    return mmq16::dispatch<mmq16::Cfg<128, 3, false, 1>>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
+    using Big = mmq16::Cfg<128, 3, false, 1, true, false, 2>;
+    using Small = mmq16::Cfg<64, 3, false, 1, true, false, 1>;
+    return mmq16::launch_tail_split<Big, Small>(w, reinterpret_cast<const uint8_t *>(xh),
+                                                w.K_pad * 2, xdT, ld_dx, M, y, ldy, epi, stream);
 }
 
 hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *xdT,
@@ -588,8 +668,10 @@ hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *
                          hipStream_t stream) {
     if (M == 0 || w.N == 0) return hipSuccess;
     if (!w.qs || !mmq_args_ok(w, xq, xdT, ld_dx, M)) return hipErrorInvalidValue;
-    return mmq16::dispatch<mmq16::Cfg<128, 3, false, 1, true, true>>(w, xq, xdT, ld_dx, M, y, ldy,
-                                                                     epi, stream);
+    using Big = mmq16::Cfg<128, 3, false, 1, true, true, 2>;
+    using Small = mmq16::Cfg<64, 3, false, 1, true, true, 1>;
+    return mmq16::launch_tail_split<Big, Small>(w, reinterpret_cast<const uint8_t *>(xq), w.K_pad,
+                                                xdT, ld_dx, M, y, ldy, epi, stream);
 }
 
 }  // namespace s2x

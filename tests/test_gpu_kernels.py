@@ -181,12 +181,16 @@ def test_gemm_large_m_batch_invariant(orc, gemm_data):
     assert np.array_equal(orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd), yg[rows])
 
 
-def test_drop_in_large_m(orc, gemm_data):
-    # batch-32 row count through the drop-in (f16-MFMA) GEMM: partial last
-    # row tile (23328 = 91 * 256 + 32) and column tile (4304 = 33 * 128 + 80)
-    raw, N, K, K_pad = gemm_data["fc1"]
+@pytest.mark.parametrize("label", ["fc1", "out"])
+def test_drop_in_large_m(orc, gemm_data, label):
+    # batch-32 row count through the drop-in (int8) GEMM: partial last row
+    # tile (23328 = 182 * 128 + 32), partial column tile for fc1 (4304 =
+    # 33 * 128 + 80); for fc1 the rows past the last full round of 128 x 128
+    # tiles (the last 288) come from the second, 64 x 64-tile launch.  The
+    # checked rows include the last 40
+    raw, N, K, K_pad = gemm_data[label]
     M = 23328
-    say("drop-in fc1 M=23328")
+    say(f"drop-in {label} M=23328")
     x = np.random.default_rng(8).standard_normal((M, K)).astype(np.float32)
     wd, xd = dev(raw), dev(x)
     y = empty((M, N), torch.float32)
@@ -197,12 +201,12 @@ def test_drop_in_large_m(orc, gemm_data):
     yg = host(y)
     rows = np.concatenate([np.arange(M - 40, M), np.random.default_rng(9).choice(M - 40, 40,
                                                                                    replace=False)])
-    assert_same(yg[rows], orc.mul_mat_q8_0_f32(raw, K_pad, N, x[rows]), "drop-in M=23328")
+    assert_same(yg[rows], orc.mul_mat_q8_0_f32(raw, K_pad, N, x[rows]), f"drop-in {label} M=23328")
 
 
 @pytest.mark.parametrize("label", [s[0] for s in SHAPES])
 def test_drop_in_mul_mat_f32(orc, gemm_data, label):
-    # the drop-in op runs the f16-MFMA GEMM; rows 0-7 carry tiny values so
+    # the drop-in op runs the int8 GEMM; rows 0-7 carry tiny values so
     # their activation scales are fp16 subnormals (amax/127 < 6.1e-5)
     raw, N, K, K_pad = gemm_data[label]
     M = 333
