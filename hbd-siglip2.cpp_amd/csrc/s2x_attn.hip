@@ -190,6 +190,7 @@ __global__ __launch_bounds__(256) void k_attn(
 
     // Q^T fragments (B operand): lane holds query q, d = 16 t + 8 lh + s
     const int q = qt * 128 + wave * 32 + lr;
+    const bool active = __builtin_amdgcn_readfirstlane(qt * 128 + wave * 32) < len;
     v8h qf[5];
 #pragma unroll
     for (int t = 0; t < 5; ++t)
@@ -285,6 +286,9 @@ __global__ __launch_bounds__(256) void k_attn(
             nxt = gload(t + 1, std::true_type{});
         const _Float16 *kl = lds + buf * FA_STAGE;
         const _Float16 *vl = kl + FA_KT * FA_KP;
+        // a wave whose 32 queries all lie past the segment end only stages
+        // tiles for the others
+        if (active) {
         // S^T for the tile's two 32-key halves (raw q.k, unscaled)
         v16f sc[2];
 #pragma unroll
@@ -374,6 +378,7 @@ __global__ __launch_bounds__(256) void k_attn(
                         o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? pl1 : pl0, o[j], 0, 0, 0);
                 }
             }
+        }
         }
         if (t + 1 < n_tiles) sstore(buf ^ 1, nxt);
         __syncthreads();
