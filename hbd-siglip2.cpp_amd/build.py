@@ -25,10 +25,12 @@ SOURCES = [
     "s2x_mmq16.hip",
     "s2x_attn.hip",
     "s2x_misc.hip",
+    "s2x_naflex.hip",
     "s2x_abi.cpp",
     "s2x_encoders.cpp",
     "s2x_gguf.cpp",
     "siglip2_api.cpp",
+    "siglip2_preproc.cpp",
 ]
 
 COMMON = [

@@ -368,6 +368,63 @@ int s2x_resize_pos_embed(const float *pos, int64_t n_side, int64_t H, int64_t ou
     return e == hipSuccess ? S2X_OK : hip_fail(e, "resize launch");
 }
 
+// ---------------------------------------------------------------------------
+// NaFlex front end
+// ---------------------------------------------------------------------------
+static int check_nf(int32_t h, int32_t w, int32_t patch, int32_t max_num_patches,
+                    const char *who) {
+    if (h <= 0 || w <= 0 || patch <= 0 || max_num_patches <= 0 || h > 65535 || w > 65535 ||
+        patch > 256 || max_num_patches > (1 << 20))
+        return fail(S2X_ERR_INVALID_ARG, "%s: bad size %dx%d, patch %d, max_num_patches %d", who,
+                    h, w, patch, max_num_patches);
+    return S2X_OK;
+}
+
+int s2x_nf_target_size(int32_t h, int32_t w, int32_t patch, int32_t max_num_patches,
+                       int32_t *target_h, int32_t *target_w) {
+    if (int st = check_nf(h, w, patch, max_num_patches, "nf_target_size")) return st;
+    if (!target_h || !target_w) return fail(S2X_ERR_INVALID_ARG, "nf_target_size: null output");
+    int th = 0, tw = 0;
+    nf_target_size(h, w, patch, max_num_patches, &th, &tw);
+    *target_h = th;
+    *target_w = tw;
+    return S2X_OK;
+}
+
+size_t s2x_nf_workspace_size(int32_t h, int32_t w, int32_t patch, int32_t max_num_patches) {
+    if (h <= 0 || w <= 0 || patch <= 0 || max_num_patches <= 0 || h > 65535 || w > 65535 ||
+        patch > 256 || max_num_patches > (1 << 20))
+        return 0;
+    return nf_workspace_bytes(h, w, patch, max_num_patches);
+}
+
+int s2x_nf_preprocess_rgb_dev(const uint8_t *rgb, int32_t h, int32_t w, int32_t max_num_patches,
+                              int32_t patch, float rescale, const float *mean, const float *std_,
+                              float *out, int64_t out_cap, int32_t *n_h, int32_t *n_w,
+                              void *workspace, size_t ws_bytes, void *stream) {
+    if (int st = check_nf(h, w, patch, max_num_patches, "nf_preprocess_rgb_dev")) return st;
+    if (!rgb || !mean || !std_ || !out || !n_h || !n_w || !workspace)
+        return fail(S2X_ERR_INVALID_ARG, "nf_preprocess_rgb_dev: null pointer");
+    const size_t need = nf_workspace_bytes(h, w, patch, max_num_patches);
+    if (ws_bytes < need)
+        return fail(S2X_ERR_WORKSPACE, "nf_preprocess_rgb_dev: workspace %zu < %zu bytes", ws_bytes,
+                    need);
+    int32_t th = 0, tw = 0;
+    nf_target_size(h, w, patch, max_num_patches, &th, &tw);
+    const int64_t need_out = (int64_t)(th / patch) * (tw / patch) * 3 * patch * patch;
+    if (out_cap < need_out)
+        return fail(S2X_ERR_INVALID_ARG, "nf_preprocess_rgb_dev: out_cap %lld < %lld floats",
+                    (long long)out_cap, (long long)need_out);
+    int nh = 0, nw = 0;
+    hipError_t e = launch_nf_preprocess(rgb, h, w, max_num_patches, patch, rescale, mean, std_,
+                                        out, out_cap, &nh, &nw, workspace, ws_bytes,
+                                        (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "nf_preprocess launch");
+    *n_h = nh;
+    *n_w = nw;
+    return S2X_OK;
+}
+
 int s2x_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows_table, const int32_t *ids,
                       int64_t n_ids, const float *add, int64_t add_rows, float *out,
                       void *stream) {

@@ -171,4 +171,13 @@ hipError_t launch_pack_rows(const float *padded, int64_t row_len, int64_t max_ro
 hipError_t launch_add(const float *a, const float *b, float *y, int64_t n,
                       hipStream_t stream);
 
+// NaFlex front end (s2x_naflex.hip): target grid, anti-aliased resize,
+// rescale + normalise + patchify of one RGB u8 image (device pointers).
+void nf_target_size(int h, int w, int p, int max_patches, int *out_h, int *out_w);
+size_t nf_workspace_bytes(int h, int w, int p, int max_patches);
+hipError_t launch_nf_preprocess(const uint8_t *rgb, int h, int w, int max_patches, int p,
+                                float rescale, const float mean[3], const float stdv[3],
+                                float *out, int64_t out_cap, int *n_h, int *n_w, void *ws,
+                                size_t ws_bytes, hipStream_t stream);
+
 }  // namespace s2x

@@ -197,6 +197,27 @@ int s2x_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
                          void *stream);
 
 /* ------------------------------------------------------------------------ */
+/* NaFlex front end (replaces siglip2::preprocess_image_rgb,                   */
+/* src/siglip2_preproc.h:44-55 / src/siglip2_preproc.cpp:209-244, on the GPU; */
+/* same grid, anti-aliased resize, rounding and normalisation, bit for bit    */
+/* with the reference's release build).                                       */
+/* s2x_nf_target_size: the (target_h, target_w) the image is resized to, both */
+/* multiples of patch (host function, no GPU).                                */
+/* s2x_nf_preprocess_rgb_dev: rgb = h*w*3 u8 channel-last (device); out =     */
+/* n_h*n_w rows of 3*patch*patch floats (device, out_cap floats available);   */
+/* mean / std: 3 floats each (host); workspace: device memory of              */
+/* s2x_nf_workspace_size() bytes.  n_h / n_w (host) receive the grid.         */
+/* ------------------------------------------------------------------------ */
+int s2x_nf_target_size(int32_t h, int32_t w, int32_t patch, int32_t max_num_patches,
+                       int32_t *target_h, int32_t *target_w);
+size_t s2x_nf_workspace_size(int32_t h, int32_t w, int32_t patch, int32_t max_num_patches);
+int s2x_nf_preprocess_rgb_dev(const uint8_t *rgb, int32_t h, int32_t w,
+                              int32_t max_num_patches, int32_t patch, float rescale,
+                              const float *mean, const float *std_, float *out,
+                              int64_t out_cap, int32_t *n_h, int32_t *n_w,
+                              void *workspace, size_t ws_bytes, void *stream);
+
+/* ------------------------------------------------------------------------ */
 /* a11  Q8_0 get_rows (replaces ggml_get_rows on the Q8_0 token table,        */
 /* src/siglip2_text.cpp:649-658): out[i] = dequant(table row ids[i]) (+ add  */
 /* row i % add_rows of `add` when add != NULL).                               */

@@ -452,6 +452,116 @@ void orc_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
 }
 
 /* ------------------------------------------------------------------------ */
+/* NaFlex front end (src/siglip2_preproc.cpp)                                */
+/* ------------------------------------------------------------------------ */
+
+/* a scaled side rounded up to whole patches, at least one (:20-24) */
+static int nf_scaled(double scale, int size, int p) {
+    const double v = (double)size * scale;
+    const int r = (int)ceil(v / (double)p) * p;
+    return r > p ? r : p;
+}
+
+/* largest scale whose grid fits max_patches, bisection to 1e-5 (:28-53) */
+void orc_nf_target_size(int h, int w, int p, int max_patches, int *out_h, int *out_w) {
+    const double eps = 1e-5;
+    double lo = eps / 10.0, hi = 100.0;
+    while (hi - lo >= eps) {
+        const double mid = 0.5 * (lo + hi);
+        const long long n = (long long)(nf_scaled(mid, h, p) / p) * (long long)(nf_scaled(mid, w, p) / p);
+        if (n <= (long long)max_patches)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    *out_h = nf_scaled(lo, h, p);
+    *out_w = nf_scaled(lo, w, p);
+}
+
+/* triangle filter of support max(src/dst, 1) around each output centre,
+ * weights normalised to sum 1 (:76-107) */
+int orc_nf_filter(int src, int dst, int fused, int *first, int *taps, float *weights, int cap) {
+    const double scale = (double)src / (double)dst;
+    const double r = scale > 1.0 ? scale : 1.0;
+    const int mt = (int)ceil(2.0 * r) + 2;
+    if (mt > cap) return -1;
+    for (int i = 0; i < dst; ++i) {
+        const double center = fused ? fma((double)i + 0.5, scale, -0.5) : ((double)i + 0.5) * scale - 0.5;
+        const int k0 = (int)ceil(center - r), k1 = (int)floor(center + r);
+        const int n = k1 - k0 + 1;
+        double sum = 0.0;
+        for (int t = 0; t < mt; ++t) weights[(int64_t)i * mt + t] = 0.0f;
+        for (int t = 0; t < n; ++t) {
+            const double d = ((double)(k0 + t) - center) / r;
+            const double wv = 1.0 - fabs(d) > 0.0 ? 1.0 - fabs(d) : 0.0;
+            weights[(int64_t)i * mt + t] = (float)wv;
+            sum += wv;
+        }
+        const float inv = (float)(1.0 / sum);
+        for (int t = 0; t < n; ++t) weights[(int64_t)i * mt + t] *= inv;
+        first[i] = k0;
+        taps[i] = n;
+    }
+    return mt;
+}
+
+int orc_nf_preprocess_rgb(const uint8_t *rgb, int h, int w, int max_patches, int p,
+                          float rescale, const float mean[3], const float std_[3], int fused,
+                          float *out, int64_t out_cap, int *n_h, int *n_w) {
+    if (!rgb || h <= 0 || w <= 0 || p <= 0 || max_patches <= 0) return -1;
+    int th, tw;
+    orc_nf_target_size(h, w, p, max_patches, &th, &tw);
+    const int nh = th / p, nw = tw / p, feat = 3 * p * p;
+    if ((int64_t)nh * nw * feat > out_cap) return -1;
+    const int cap_y = (int)ceil(2.0 * ((double)h / th > 1.0 ? (double)h / th : 1.0)) + 2;
+    const int cap_x = (int)ceil(2.0 * ((double)w / tw > 1.0 ? (double)w / tw : 1.0)) + 2;
+    int *fy0 = (int *)malloc(sizeof(int) * (size_t)th), *fyn = (int *)malloc(sizeof(int) * (size_t)th);
+    int *fx0 = (int *)malloc(sizeof(int) * (size_t)tw), *fxn = (int *)malloc(sizeof(int) * (size_t)tw);
+    float *wy = (float *)malloc(sizeof(float) * (size_t)th * cap_y);
+    float *wx = (float *)malloc(sizeof(float) * (size_t)tw * cap_x);
+    const int mty = orc_nf_filter(h, th, fused, fy0, fyn, wy, cap_y);
+    const int mtx = orc_nf_filter(w, tw, fused, fx0, fxn, wx, cap_x);
+    /* pass 1, along the height: (th, w, 3) floats (:120-139) */
+    float *tmp = (float *)malloc(sizeof(float) * (size_t)th * w * 3);
+    for (int y = 0; y < th; ++y)
+        for (int x = 0; x < w; ++x)
+            for (int c = 0; c < 3; ++c) {
+                float a = 0.0f;
+                for (int t = 0; t < fyn[y]; ++t) {
+                    int sy = fy0[y] + t;
+                    sy = sy < 0 ? 0 : sy >= h ? h - 1 : sy;
+                    const float wt = wy[(int64_t)y * mty + t], v = (float)rgb[((int64_t)sy * w + x) * 3 + c];
+                    a = fused ? fmaf(wt, v, a) : a + wt * v;
+                }
+                tmp[((int64_t)y * w + x) * 3 + c] = a;
+            }
+    /* pass 2, along the width, rounded to u8 (:141-166); then rescale,
+     * normalise and the patch layout (:176-207) */
+    for (int y = 0; y < th; ++y)
+        for (int x = 0; x < tw; ++x)
+            for (int c = 0; c < 3; ++c) {
+                float a = 0.0f;
+                for (int t = 0; t < fxn[x]; ++t) {
+                    int sx = fx0[x] + t;
+                    sx = sx < 0 ? 0 : sx >= w ? w - 1 : sx;
+                    const float wt = wx[(int64_t)x * mtx + t], v = tmp[((int64_t)y * w + sx) * 3 + c];
+                    a = fused ? fmaf(wt, v, a) : a + wt * v;
+                }
+                int iv = (int)lrintf(a);
+                iv = iv < 0 ? 0 : iv > 255 ? 255 : iv;
+                const float u = (float)iv;
+                const float sv = fused ? fmaf(u, rescale, -mean[c]) : u * rescale - mean[c];
+                const int ph = y / p, py = y % p, pw = x / p, px = x % p;
+                out[((int64_t)ph * nw + pw) * feat + ((int64_t)py * p + px) * 3 + c] = sv / std_[c];
+            }
+    free(tmp);
+    free(fy0); free(fyn); free(fx0); free(fxn); free(wy); free(wx);
+    *n_h = nh;
+    *n_w = nw;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* model                                                                     */
 /* ------------------------------------------------------------------------ */
 

@@ -141,6 +141,25 @@ void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
 void orc_resize_pos_embed(const float *pos, int64_t n_side, int64_t H,
                           int64_t out_h, int64_t out_w, float *out);
 
+/* ---- NaFlex front end ----------------------------------------------------- */
+/* src/siglip2_preproc.cpp: target grid by binary search over the scale
+ * (:20-53), separable anti-aliased bilinear resize of RGB u8 with a float
+ * intermediate and lrintf rounding (:68-167), rescale + normalise +
+ * patchify to (n_h*n_w, p*p*3) channel-last patches (:169-207).
+ * `fused` = 1 restates the reference as its release build compiles it
+ * (GCC -O3 -march=native, default -ffp-contract=fast: every a*b+c of the
+ * file is one fused multiply-add, in double for the filter centres and in
+ * float for the filter passes and the rescale); 0 rounds each product. */
+void orc_nf_target_size(int h, int w, int p, int max_patches, int *out_h, int *out_w);
+/* Filter of one axis: first source index, tap count and max_taps weights per
+ * output pixel; returns max_taps (<= cap) or -1. */
+int orc_nf_filter(int src, int dst, int fused, int *first, int *taps, float *weights, int cap);
+/* Returns 0 and fills out (n_h*n_w*3*p*p floats, <= out_cap) and n_h, n_w;
+ * -1 on bad arguments or a too small out_cap. */
+int orc_nf_preprocess_rgb(const uint8_t *rgb, int h, int w, int max_patches, int p,
+                          float rescale, const float mean[3], const float std_[3], int fused,
+                          float *out, int64_t out_cap, int *n_h, int *n_w);
+
 /* ---- model ---------------------------------------------------------------- */
 typedef struct {
     const float *ln1_w, *ln1_b;

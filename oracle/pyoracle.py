@@ -66,6 +66,9 @@ def lib():
             "orc_tanh_f32": ([_f32], _f32),
             "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
             "orc_resize_pos_embed": ([_p, _i64, _i64, _i64, _i64, _p], None),
+            "orc_nf_target_size": ([_i32, _i32, _i32, _i32, _p, _p], None),
+            "orc_nf_preprocess_rgb": ([_p, _i32, _i32, _i32, _i32, _f32, _p, _p, ctypes.c_int,
+                                       _p, _i64, _p, _p], ctypes.c_int),
             "orc_vision_encode": ([ctypes.POINTER(OrcVision), _p, _i32, _i32, _i32, _p, _p,
                                    ctypes.c_int], None),
             "orc_text_encode": ([ctypes.POINTER(OrcText), _p, _i32, _p, _p, ctypes.c_int], None),
@@ -182,6 +185,57 @@ def resize_pos_embed(pos, n_side, out_h, out_w):
     out = np.empty((out_h * out_w, H), np.float32)
     lib().orc_resize_pos_embed(_ptr(pos), n_side, H, out_h, out_w, _ptr(out))
     return out
+
+
+def nf_target_size(h, w, p, max_patches):
+    th, tw = ctypes.c_int32(), ctypes.c_int32()
+    lib().orc_nf_target_size(h, w, p, max_patches, ctypes.byref(th), ctypes.byref(tw))
+    return th.value, tw.value
+
+
+NF_MEAN = np.array([0.5, 0.5, 0.5], np.float32)
+NF_STD = np.array([0.5, 0.5, 0.5], np.float32)
+
+
+def _nf_call(fn, rgb, max_patches, p, rescale, mean, std, extra=()):
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    h, w = rgb.shape[:2]
+    mean = np.ascontiguousarray(mean, np.float32)
+    std = np.ascontiguousarray(std, np.float32)
+    cap = max_patches * 3 * p * p
+    out = np.empty(cap, np.float32)
+    nh, nw = ctypes.c_int32(), ctypes.c_int32()
+    st = fn(_ptr(rgb), h, w, max_patches, p, ctypes.c_float(rescale), _ptr(mean), _ptr(std), *extra,
+            _ptr(out), cap, ctypes.byref(nh), ctypes.byref(nw))
+    if st != 0:
+        raise ValueError("preprocess failed")
+    return out[: nh.value * nw.value * 3 * p * p].reshape(nh.value * nw.value, 3 * p * p), nh.value, nw.value
+
+
+def nf_preprocess_rgb(rgb, max_patches, p=16, rescale=1.0 / 255.0, mean=NF_MEAN, std=NF_STD, fused=1):
+    """NaFlex preprocessing of an (h, w, 3) uint8 image -> (patches, n_h, n_w)."""
+    return _nf_call(lib().orc_nf_preprocess_rgb, rgb, max_patches, p, rescale, mean, std,
+                    (ctypes.c_int(fused),))
+
+
+REF_PREPROC_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_ref", "libref_preproc.so")
+_ref = None
+
+
+def ref_preprocess_lib():
+    """The reference's own preprocessing (oracle/_ref, built by `make -C
+    oracle ref` where the reference tree exists), or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PREPROC_PATH):
+        L = ctypes.CDLL(REF_PREPROC_PATH)
+        L.ref_nf_preprocess_rgb.argtypes = [_p, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _i64, _p, _p]
+        L.ref_nf_preprocess_rgb.restype = ctypes.c_int
+        _ref = L
+    return _ref
+
+
+def ref_preprocess_rgb(rgb, max_patches, p=16, rescale=1.0 / 255.0, mean=NF_MEAN, std=NF_STD):
+    return _nf_call(ref_preprocess_lib().ref_nf_preprocess_rgb, rgb, max_patches, p, rescale, mean, std)
 
 
 LAYER_KEYS = [f[0] for f in OrcLayer._fields_]
