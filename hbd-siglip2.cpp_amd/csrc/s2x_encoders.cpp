@@ -515,7 +515,7 @@ struct s2x_vision {
     float *probe_q = nullptr, *hkv_b = nullptr, *ho_b = nullptr, *hln_w = nullptr,
           *hln_b = nullptr, *hup_b = nullptr, *hdown_b = nullptr;
     std::vector<std::pair<std::pair<int, int>, float *>> pos_cache;  // LRU of resized grids
-    DevBuf pix, pos_packed, kv, hq, ha, hu, hout, hid;
+    DevBuf pix, pos_packed, kv, hq, ha, hu, hout, hid, nf_ws;
 
     ~s2x_vision() {
         for (s2x_weight *w : {patch, hkv, ho, hup, hdown}) s2x_weight_destroy(w);
@@ -784,6 +784,66 @@ int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
     for (int i = 0; i < n_img; ++i) {
         const float *pos = nullptr;
         S2X_TRY(v->pos_for(shapes_host[2 * i], shapes_host[2 * i + 1], &pos));
+        S2X_HIP_TRY(hipMemcpyAsync(v->pos_packed.as<float>() + (int64_t)st[(size_t)i] * t.H, pos,
+                                   sizeof(float) * (size_t)(ln[(size_t)i] * t.H),
+                                   hipMemcpyDeviceToDevice, t.stream));
+    }
+    S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
+    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                   EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
+                   v->patch_dim));
+    return v->tail(M, n_img, max_len, pooling, out_dev);
+}
+
+int s2x_vision_encode_rgb_batch_dev(s2x_vision *v, const uint8_t *const *rgb_dev,
+                                    const int32_t *hw_host, int32_t n_img,
+                                    int32_t max_num_patches, float rescale, const float *mean,
+                                    const float *std_, int32_t pooling, float *out_dev) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    if (n_img <= 0 || max_num_patches <= 0 || !rgb_dev || !hw_host || !mean || !std_ ||
+        !out_dev || (pooling != S2X_POOL_MEAN && pooling != S2X_POOL_PROBE))
+        return fail(S2X_ERR_INVALID_ARG, "vision_encode_rgb_batch: bad arguments");
+    if (max_num_patches > MAX_SEG_LEN)
+        return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
+    int p = 1;
+    while (3 * p * p < v->patch_dim) ++p;
+    if (3 * p * p != v->patch_dim)
+        return fail(S2X_ERR_UNSUPPORTED, "vision_encode_rgb_batch: patch_dim %lld is not 3*p*p",
+                    (long long)v->patch_dim);
+    Tower &t = v->t;
+    std::vector<int32_t> st((size_t)n_img), ln((size_t)n_img), shp(2 * (size_t)n_img);
+    int64_t M = 0, max_len = 0;
+    size_t ws_bytes = 0;
+    for (int i = 0; i < n_img; ++i) {
+        const int32_t h = hw_host[2 * i], w = hw_host[2 * i + 1];
+        if (h <= 0 || w <= 0 || h > 65535 || w > 65535 || !rgb_dev[i])
+            return fail(S2X_ERR_INVALID_ARG, "vision_encode_rgb_batch: image %d (%dx%d) invalid", i, h, w);
+        int th = 0, tw = 0;
+        nf_target_size(h, w, p, max_num_patches, &th, &tw);
+        shp[2 * (size_t)i] = th / p;
+        shp[2 * (size_t)i + 1] = tw / p;
+        st[(size_t)i] = (int32_t)M;
+        ln[(size_t)i] = (th / p) * (tw / p);
+        M += ln[(size_t)i];
+        max_len = std::max<int64_t>(max_len, ln[(size_t)i]);
+        ws_bytes = std::max(ws_bytes, nf_workspace_bytes(h, w, p, max_num_patches));
+    }
+    if (max_len > MAX_SEG_LEN) return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
+    S2X_TRY(t.reserve(M, n_img, max_len));
+    S2X_TRY(t.set_segments(st, ln));
+    S2X_TRY(ensure(v->pix, sizeof(float) * (size_t)(M * v->patch_dim), t.stream));
+    S2X_TRY(ensure(v->pos_packed, sizeof(float) * (size_t)(M * t.H), t.stream));
+    S2X_TRY(ensure(v->nf_ws, ws_bytes, t.stream));
+    // each image's patches land straight in its packed row range
+    for (int i = 0; i < n_img; ++i) {
+        int nh = 0, nw = 0;
+        hipError_t e = launch_nf_preprocess(
+            rgb_dev[i], hw_host[2 * i], hw_host[2 * i + 1], max_num_patches, p, rescale, mean,
+            std_, v->pix.as<float>() + (int64_t)st[(size_t)i] * v->patch_dim,
+            (int64_t)ln[(size_t)i] * v->patch_dim, &nh, &nw, v->nf_ws.p, ws_bytes, t.stream);
+        if (e != hipSuccess) return hip_fail(e, "nf_preprocess launch");
+        const float *pos = nullptr;
+        S2X_TRY(v->pos_for(nh, nw, &pos));
         S2X_HIP_TRY(hipMemcpyAsync(v->pos_packed.as<float>() + (int64_t)st[(size_t)i] * t.H, pos,
                                    sizeof(float) * (size_t)(ln[(size_t)i] * t.H),
                                    hipMemcpyDeviceToDevice, t.stream));

@@ -117,6 +117,7 @@ _sig("s2x_vision_set_stream", [_p, _p])
 _sig("s2x_vision_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_vision_set_gemm_variant", [_p, ctypes.c_int])
 _sig("s2x_vision_set_lanes", [_p, ctypes.c_int])
+_sig("s2x_vision_encode_rgb_batch_dev", [_p, _p, _p, _i32, _i32, _f32, _p, _p, _i32, _p])
 GEMM_F16_MFMA, GEMM_I8_MFMA = 0, 1
 _sig("s2x_text_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_vision_encode", [_p, _p, _i32, _i32, _i32, _p])

@@ -336,6 +336,20 @@ int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
                                  int32_t max_patches, int32_t pooling,
                                  float *out_dev);
 
+/* Raw images to embeddings on the device (the reference server's
+ * preprocess_image_rgb + VisionEncoder::encode per image,
+ * src/siglip2_server.cpp:336-366, as one batch): rgb_dev[i] = image i as
+ * h*w*3 u8 channel-last (device), hw_host[i] = (h, w).  Each image goes
+ * through the NaFlex front end (s2x_nf_preprocess_rgb_dev semantics,
+ * max_num_patches, rescale, mean[3], std[3] on the host) straight into
+ * the packed rows of the ragged batch.  out_dev [n_img, hidden].
+ * Asynchronous. */
+int s2x_vision_encode_rgb_batch_dev(s2x_vision *v, const uint8_t *const *rgb_dev,
+                                    const int32_t *hw_host, int32_t n_img,
+                                    int32_t max_num_patches, float rescale,
+                                    const float *mean, const float *std_,
+                                    int32_t pooling, float *out_dev);
+
 /* Per-kernel GPU timing of the MFMA GEMM launches (HIP events on the
  * encoder's stream) for roofline reporting.  enable != 0 turns recording
  * on; s2x_vision_gemm_stats returns the summed milliseconds and op count

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+import pyoracle
 import s2x
 from s2x import synth
 from gpu_util import cos, dev, empty, host, ptr, say
@@ -95,6 +96,34 @@ def test_small_vision_ragged_equals_per_image(small_vision, pooling):
     out = v.ragged(padded.reshape(-1, 768), shapes, maxp, pooling)
     for i in range(len(shapes)):
         assert np.array_equal(out[i], singles[i]), shapes[i]
+
+
+@pytest.mark.parametrize("pooling", [s2x.POOL_PROBE, s2x.POOL_MEAN])
+def test_small_vision_rgb_batch_equals_preprocessed(small_vision, pooling):
+    # raw RGB images of assorted sizes through the GPU NaFlex front end and
+    # the tower in one call == the oracle's preprocessing (the reference's
+    # bits) fed to the ragged encode
+    v, _ = small_vision
+    sizes = [(480, 640), (300, 1000), (432, 432), (37, 53)]
+    maxp, p = 576, 16
+    rng = np.random.default_rng(91)
+    imgs = [rng.integers(0, 256, (h, w, 3), dtype=np.uint8) for h, w in sizes]
+    padded = np.zeros((len(sizes), maxp, 3 * p * p), np.float32)
+    shapes = []
+    for i, img in enumerate(imgs):
+        pre, nh, nw = pyoracle.nf_preprocess_rgb(img, maxp, p=p, fused=1)
+        padded[i, :nh * nw] = pre
+        shapes.append((nh, nw))
+    want = v.ragged(padded.reshape(-1, 3 * p * p), shapes, maxp, pooling)
+    dimgs = [dev(np.ascontiguousarray(im)) for im in imgs]
+    ptrs = (ctypes.c_void_p * len(imgs))(*[ptr(d) for d in dimgs])
+    hw = np.array(sizes, np.int32)
+    mean = np.array([0.5, 0.5, 0.5], np.float32)
+    std = np.array([0.5, 0.5, 0.5], np.float32)
+    out = empty((len(imgs), v.host.cfg.hidden), torch.float32)
+    s2x.call("s2x_vision_encode_rgb_batch_dev", v.h, ptrs, hw.ctypes.data, len(imgs), maxp,
+             ctypes.c_float(1.0 / 255.0), mean.ctypes.data, std.ctypes.data, pooling, ptr(out))
+    assert np.array_equal(host(out), want)
 
 
 def test_small_vision_gemm_variants_same_bits(small_vision):
