@@ -68,6 +68,9 @@ def main():
     ap.add_argument("--gemm", choices=["i8", "f16"], default="i8",
                     help="GEMM quant format: int8 quants on the int8 MFMA (default) or "
                          "f16-coded quants on the f16 MFMA; same bits")
+    ap.add_argument("--preproc", action="store_true",
+                    help="instead of the tower: time the NaFlex front end (GPU resize + "
+                         "patchify of a batch of RGB images) and print its own JSON line")
     ap.add_argument("--lanes", type=int, default=0,
                     help="row ranges (whole images) run concurrently on their own streams "
                          "(1..4; default: the library's)")
@@ -93,6 +96,10 @@ def main():
 
     import s2x
     from s2x import synth
+
+    if args.preproc:
+        bench_preproc(args, np, torch, s2x)
+        return
 
     cfg = synth.SO400M_VISION
     B, gh, gw = args.batch, 27, 27
@@ -190,6 +197,82 @@ def main():
                      "kernel": KERNELS[args.gemm],
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "launches": int(launches.value)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def bench_preproc(args, np, torch, s2x):
+    """The NaFlex front end on its own: B RGB images of 640 x 480 resized to
+    at most 729 patches of 16 x 16 and patchified (s2x_nf_preprocess_rgb_dev
+    per image, images already in HBM).  Roofline: HBM, algorithmic bytes =
+    the u8 image read + the f32 patch rows written."""
+    B, H, W, MP, P = args.batch, 480, 640, 729, 16
+    rng = np.random.default_rng(7)
+    imgs = [torch.from_numpy(rng.integers(0, 256, (H, W, 3), dtype=np.uint8)).to("cuda:0")
+            for _ in range(B)]
+    th, tw = ctypes.c_int32(), ctypes.c_int32()
+    s2x.call("s2x_nf_target_size", H, W, P, MP, ctypes.byref(th), ctypes.byref(tw))
+    n_rows = (th.value // P) * (tw.value // P)
+    feat = 3 * P * P
+    out = torch.empty((B, n_rows * feat), dtype=torch.float32, device="cuda:0")
+    wsb = s2x.lib.s2x_nf_workspace_size(H, W, P, MP)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device="cuda:0")
+    mean = np.array([0.5, 0.5, 0.5], np.float32)
+    std = np.array([0.5, 0.5, 0.5], np.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    nh, nw = ctypes.c_int32(), ctypes.c_int32()
+
+    def step():
+        for i in range(B):
+            s2x.call("s2x_nf_preprocess_rgb_dev", ctypes.c_void_p(imgs[i].data_ptr()), H, W, MP, P,
+                     ctypes.c_float(1.0 / 255.0), mean.ctypes.data, std.ctypes.data,
+                     ctypes.c_void_p(out[i].data_ptr()), n_rows * feat, ctypes.byref(nh),
+                     ctypes.byref(nw), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(wsb),
+                     ctypes.c_void_p(stream))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    gpu_ms = e0.elapsed_time(e1) / args.steps
+    ms_step = (t1 - t0) * 1000.0 / args.steps
+    ips = B / (ms_step / 1000.0)
+    alg_bytes = B * (H * W * 3 + n_rows * feat * 4)
+    gbs = alg_bytes / (gpu_ms / 1000.0) / 1e9
+    log(f"preproc: {ms_step:.3f} ms/step wall, {gpu_ms:.3f} ms/step GPU, {ips:.0f} images/s, "
+        f"{gbs:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle
+        host_imgs = [im.cpu().numpy() for im in imgs[:8]]
+        c0 = time.perf_counter()
+        for im in host_imgs:
+            pyoracle.nf_preprocess_rgb(im, MP, p=P, fused=1)
+        c1 = time.perf_counter()
+        cpu = {"value": round(len(host_imgs) / (c1 - c0), 2), "unit": "images/s", "cores": 1,
+               "kind": "port", "sample": f"{len(host_imgs)} images of the same 640x480 -> "
+                                         f"{n_rows}-patch workload, {c1 - c0:.2f} s"}
+    rec = {
+        "metric": f"images/sec NaFlex preprocessing 640x480 RGB -> {n_rows} patches of 16x16",
+        "value": round(ips, 1), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded uniform u8 RGB images)",
+        "config": {"workload": f"NaFlex front end, batch {B} x 640x480 RGB, max 729 patches",
+                   "global_batch": B, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbs / 8000.0, 4), "traffic": None,
+                     "kernel": "k_nf_vpass + k_nf_hpass (per image)",
+                     "avg_launch_ms": round(gpu_ms / B, 4), "launches": 2 * B * args.steps},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
