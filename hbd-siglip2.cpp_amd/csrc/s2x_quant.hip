@@ -6,6 +6,8 @@
 // Mapping: one 32-value block = 8 consecutive lanes x 4 floats, so a wave
 // reads 1 KiB contiguous per instruction and the block amax is a 3-step
 // butterfly inside the 8-lane group.
+#include <algorithm>
+
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
@@ -136,27 +138,20 @@ hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t 
 // (src/siglip2_vision.cpp:79-88 graph; ggml_norm's two-pass variance), then
 // the 32-blocks of y quantized by 8-lane groups exactly as k_quantize_q8_1.
 // ---------------------------------------------------------------------------
-constexpr int LN_MAXIT = 8;  // H <= 8 * 256
+constexpr int LN_MAXIT = 8;        // H <= 8 * 256
+constexpr int LN_MAX_BLOCKS = 3072;  // resident-size grid; blocks stride over the rows
 
-// NIT = ceil(H / 256) column passes of 4 values per lane; only x stays in
-// registers across the reductions (w and b are read when applied), which
-// keeps the kernel at full occupancy.
-template <bool QUANT, bool WRITE_Y, int NIT>
-__global__ __launch_bounds__(256) void k_layernorm(
-    const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
-    const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
-    float *__restrict__ y, int64_t ldy, int vec4) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const float *xr = x + row * ldx;
-    float v[NIT][4];
+// 4 columns per lane per 256-column pass; a missing row (ok false) or a
+// column past H reads as zeros
+template <int NIT>
+__device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr, int64_t H,
+                                            int lane, bool ok, int vec4) {
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int64_t c = (int64_t)it * 256 + lane * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
-        if (c < H) {
+        if (ok && c < H) {
             if (vec4 & 1) {
                 const float4 t = *reinterpret_cast<const float4 *>(xr + c);
                 v[it][0] = t.x; v[it][1] = t.y; v[it][2] = t.z; v[it][3] = t.w;
@@ -166,79 +161,97 @@ __global__ __launch_bounds__(256) void k_layernorm(
             }
         }
     }
-    double s = 0.0;
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int64_t c = (int64_t)it * 256 + lane * 4;
-        if (c < H) s = s + (((double)v[it][0] + (double)v[it][1]) + ((double)v[it][2] + (double)v[it][3]));
+}
+
+// NIT = ceil(H / 256) column passes.  w and b are staged once per block in
+// LDS; each wave walks rows row, row + 4 * gridDim.x, ... and loads its next
+// row before reducing the current one, so HBM reads overlap the reductions.
+template <bool QUANT, bool WRITE_Y, int NIT>
+__global__ __launch_bounds__(256) void k_layernorm(
+    const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
+    const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
+    float *__restrict__ y, int64_t ldy, int vec4) {
+    __shared__ __align__(16) float sw[NIT * 256], sb[NIT * 256];
+    for (int i = threadIdx.x; i < H; i += 256) {
+        sw[i] = w ? w[i] : 1.0f;
+        sb[i] = b ? b[i] : 0.0f;
     }
-    // sums in double, as ggml's CPU norm accumulates: the f32 mean and
-    // variance then equal the CPU's (the double sum's rounding, whatever
-    // its order, is ~1e-16 relative and vanishes in the f32 conversion)
-    const float mean = (float)(wave_dsum(s) / (double)H);
-    double s2 = 0.0;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * 4;
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    float v[NIT][4];
+    ln_load_row<NIT>(v, x + row * ldx, H, lane, row < M, vec4);
+    for (; row < M; row += stride) {  // wave-uniform
+        float vn[NIT][4];
+        const int64_t next = row + stride;
+        ln_load_row<NIT>(vn, x + next * ldx, H, lane, next < M, vec4);
+        // sums in double, as ggml's CPU norm accumulates: the f32 mean and
+        // variance then equal the CPU's (the double sum's rounding, whatever
+        // its order, is ~1e-16 relative and vanishes in the f32 conversion)
+        double s = 0.0;
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int64_t c = (int64_t)it * 256 + lane * 4;
-        if (c < H) {
+        for (int it = 0; it < NIT; ++it) {
+            const int64_t c = (int64_t)it * 256 + lane * 4;
+            if (c < H)
+                s = s + (((double)v[it][0] + (double)v[it][1]) +
+                         ((double)v[it][2] + (double)v[it][3]));
+        }
+        const float mean = (float)(wave_dsum(s) / (double)H);
+        double s2 = 0.0;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int64_t c = (int64_t)it * 256 + lane * 4;
+            if (c < H) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float t = v[it][j] - mean;
+                    s2 = s2 + (double)(t * t);
+                }
+            }
+        }
+        const float var = (float)(wave_dsum(s2) / (double)H);
+        const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int64_t c = (int64_t)it * 256 + lane * 4;
+            if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
+            const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
+            const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
+            const float wa[4] = {wv.x, wv.y, wv.z, wv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
+            float o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float t = v[it][j] - mean;
-                s2 = s2 + (double)(t * t);
+                float t = (v[it][j] - mean) * scale;
+                if (w) t = t * wa[j];
+                if (b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
+                o[j] = t;
             }
-        }
-    }
-    const float var = (float)(wave_dsum(s2) / (double)H);
-    const float scale = 1.0f / sqrtf(var + eps);
+            if (WRITE_Y) {
+                float *yr = y + row * ldy + c;
+                if (vec4 & 2) {
+                    *reinterpret_cast<float4 *>(yr) = make_float4(o[0], o[1], o[2], o[3]);
+                } else {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int64_t c = (int64_t)it * 256 + lane * 4;
-        if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
-        float wv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (vec4 & 4) {
-            if (w) {
-                const float4 t = *reinterpret_cast<const float4 *>(w + c);
-                wv[0] = t.x; wv[1] = t.y; wv[2] = t.z; wv[3] = t.w;
+                    for (int j = 0; j < 4; ++j) yr[j] = o[j];
+                }
             }
-            if (b) {
-                const float4 t = *reinterpret_cast<const float4 *>(b + c);
-                bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+            if (QUANT) {
+                float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+                a = group8_max(a);
+                const float d = a / 127.0f;
+                const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+                const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
+                const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
+                store_q4(q.qs, q.qh, row * H + c, q0, q1, q2, q3);
+                const int sq = group8_isum(q0 + q1 + q2 + q3);
+                if ((lane & 7) == 0) store_scales(q, row, c / QK, H / QK, d, sq);
             }
-        } else {
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (w) wv[j] = w[c + j];
-                if (b) bv[j] = b[c + j];
-            }
-        }
-        float o[4];
+        for (int it = 0; it < NIT; ++it)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float t = (v[it][j] - mean) * scale;
-            if (w) t = t * wv[j];
-            if (b) t = t + bv[j];
-            o[j] = t;
-        }
-        if (WRITE_Y) {
-            float *yr = y + row * ldy + c;
-            if (vec4 & 2) {
-                *reinterpret_cast<float4 *>(yr) = make_float4(o[0], o[1], o[2], o[3]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) yr[j] = o[j];
-            }
-        }
-        if (QUANT) {
-            float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-            a = group8_max(a);
-            const float d = a / 127.0f;
-            const float inv = a != 0.0f ? 127.0f / a : 0.0f;
-            const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
-            const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
-            store_q4(q.qs, q.qh, row * H + c, q0, q1, q2, q3);
-            const int sq = group8_isum(q0 + q1 + q2 + q3);
-            if ((lane & 7) == 0) store_scales(q, row, c / QK, H / QK, d, sq);
-        }
+            for (int j = 0; j < 4; ++j) v[it][j] = vn[it][j];
     }
 }
 
@@ -263,9 +276,8 @@ hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
     if (M == 0) return hipSuccess;
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
-    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) vec4 |= 4;
     if (H <= 0 || H % QK != 0 || H > LN_MAXIT * 256 || (!q && !y)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((M + 3) / 4));
+    const dim3 grid((unsigned)std::min<int64_t>((M + 3) / 4, LN_MAX_BLOCKS));
     const bool quant = q != nullptr;
     const Q81Out qo = q ? *q : Q81Out{};
     switch ((H + 255) / 256) {

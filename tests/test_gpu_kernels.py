@@ -56,17 +56,29 @@ def test_quantize_strided_input(orc):
     assert np.array_equal(host(qs), rq) and np.array_equal(host(ds).view(np.uint16), rd)
 
 
-def test_layernorm_quantize(orc):
-    rng = np.random.default_rng(2)
-    M, H = 729, 1152
-    x = (rng.standard_normal((M, H)) * 2 + 0.3).astype(np.float32)
-    w = rng.normal(1, 0.02, H).astype(np.float32)
-    b = rng.normal(0, 0.02, H).astype(np.float32)
-    xd, wd, bd = dev(x), dev(w), dev(b)
+# (M, H, ldx, affine w, affine b): 13001 rows exceed one pass of the
+# row-striding grid (4 x 3072 rows); ldx = H + 1 takes the unaligned loads
+LN_CASES = [(729, 1152, 1152, True, True), (13001, 1152, 1152, True, True),
+            (37, 768, 769, True, False), (5, 96, 96, False, True), (3, 2048, 2048, False, False)]
+
+
+@pytest.mark.parametrize("M,H,ldx,has_w,has_b", LN_CASES)
+def test_layernorm_quantize(orc, M, H, ldx, has_w, has_b):
+    say(f"layernorm M={M} H={H} ldx={ldx} w={has_w} b={has_b}")
+    rng = np.random.default_rng(2 + M)
+    xs = (rng.standard_normal((M, ldx)) * 2 + 0.3).astype(np.float32)
+    x = np.ascontiguousarray(xs[:, :H])
+    w = rng.normal(1, 0.02, H).astype(np.float32) if has_w else None
+    b = rng.normal(0, 0.02, H).astype(np.float32) if has_b else None
+    xd = dev(xs)
+    wd = dev(w) if has_w else None
+    bd = dev(b) if has_b else None
+    wp = ptr(wd) if has_w else None
+    bp = ptr(bd) if has_b else None
     qs = empty((M, H), torch.int8)
     ds = empty((M, H // 32, 2), torch.int16)
     y = empty((M, H), torch.float32)
-    s2x.call("s2x_layernorm_quantize_q8_1", ptr(xd), H, M, H, ptr(wd), ptr(bd), ctypes.c_float(1e-6),
+    s2x.call("s2x_layernorm_quantize_q8_1", ptr(xd), H, M, ldx, wp, bp, ctypes.c_float(1e-6),
              ptr(qs), ptr(ds), ptr(y), H, stream())
     yg = host(y)
     ref = orc.layernorm(x, w, b, 1e-6)
@@ -78,7 +90,7 @@ def test_layernorm_quantize(orc):
     assert_same(host(ds).view(np.uint16), rd, "ln ds")
     # LN alone
     y2 = empty((M, H), torch.float32)
-    s2x.call("s2x_layernorm", ptr(xd), H, M, H, ptr(wd), ptr(bd), ctypes.c_float(1e-6), ptr(y2), H,
+    s2x.call("s2x_layernorm", ptr(xd), H, M, ldx, wp, bp, ctypes.c_float(1e-6), ptr(y2), H,
              stream())
     assert np.array_equal(host(y2), yg)
 
