@@ -78,7 +78,7 @@ struct Cfg {
                       (BM + BN) * CH == QI * NT && (BM * CH) % WAVE == 0 && BM / 8 <= WAVE &&
                       BN / 8 <= WAVE && (!I8 || TM == 1),
                   "config");
-    static_assert(NS >= 2 && NS <= 4, "wait table / unroll");
+    static_assert(NS >= 2 && NS <= (PIPE ? 4 : 8), "wait table / unroll");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -125,7 +125,19 @@ __device__ __forceinline__ void wait_after(int after) {
     case 0: wait_vm<0>(); break;
     case 1: wait_vm<L>(); break;
     case 2: wait_vm<2 * L>(); break;
-    default: wait_vm<3 * L>(); break;
+    case 3: wait_vm<3 * L>(); break;
+    case 4: wait_vm<4 * L>(); break;
+    case 5: wait_vm<5 * L>(); break;
+    default: wait_vm<6 * L>(); break;
+    }
+}
+
+// f(integral_constant<int, J>) for J = J0 .. J1 - 1, in order
+template <int J0, int J1, class F>
+__device__ __forceinline__ void unroll_const(F &&f) {
+    if constexpr (J0 < J1) {
+        f(std::integral_constant<int, J0>{});
+        unroll_const<J0 + 1, J1>(f);
     }
 }
 
@@ -212,10 +224,18 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
     const int lr = lane & 31, lh = lane >> 5;
+    const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 32 * TN + lr;
+    // the epilogue's bias of this lane's columns, fetched before the main
+    // loop so that its latency is hidden (0 past N)
+    float bias_v[TN];
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+        const int n = n0 + wcol0 + b * 32;
+        bias_v[b] = EPI != EPI_NONE && EPI != EPI_DUMP_I && n < N ? epi.bias[n] : 0.0f;
+    }
     const int sw = (lr >> 2) & (CH - 1);  // chunk permutation of the rows this lane reads
     // k slots 8 lh .. 8 lh + 7 (f16: of each 16-value half) / 16 lh .. +15 (int8)
     const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
-    const int xrow0 = wm * 32 * TM + lr, wcol0 = wn * 32 * TN + lr;
     const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
     // scale operands: k slot 0 (lanes 0..31) holds the scale, the rest zeros
     const int dxo0 = lh ? C::Z_OFF : C::DX_OFF + xrow0 * 2;
@@ -326,14 +346,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             mma(F);
         };
         for (int s = 0; s < KB; s += NS) {
-            step(s, std::integral_constant<int, 0>{});
-            if (s + 1 < KB) step(s + 1, std::integral_constant<int, 1 % NS>{});
-            if constexpr (NS > 2) {
-                if (s + 2 < KB) step(s + 2, std::integral_constant<int, 2 % NS>{});
-            }
-            if constexpr (NS > 3) {
-                if (s + 3 < KB) step(s + 3, std::integral_constant<int, 3 % NS>{});
-            }
+            unroll_const<0, NS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (s + j < KB) step(s + j, jc);
+            });
         }
     } else {
         // NS blocks in flight; block s+1's fragments are read from LDS while
@@ -378,6 +394,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[TM - 1][TN - 1][r] = fmaf((float)Ip[r], Sp[r], acc[TM - 1][TN - 1][r]);
     }
+    // The stage loop's waits are inline asm, which the compiler's wait
+    // placement cannot see: this vmcnt(0) (expcnt / lgkmcnt left alone) --
+    // free here, nothing is in flight -- tells it that bias_v has arrived,
+    // so the epilogue's stores are not each preceded by a vmcnt(0).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
 
     if constexpr (EPI == EPI_GELU_Q81) {
         // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over rows of
@@ -395,11 +416,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             const int nb = n0 + wn * 32 * TN + b * 32;  // first column of this quant block
             if (nb >= epi.q_kpad) continue;        // wave-uniform
             const int n = nb + lr;
-            const float bias = n < N ? epi.bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
-                    n < N ? gelu_tanh(acc[0][b][r] + bias) : 0.0f;
+                    n < N ? gelu_tanh(acc[0][b][r] + bias_v[b]) : 0.0f;
             float v[16];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -455,20 +475,23 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             _Float16 *scr = reinterpret_cast<_Float16 *>(lds) + wave * 32 * P;
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int n = n0 + wcol0 + b * 32;
-                const float bias = n < N ? epi.bias[n] : 0.0f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] = f32_to_f16(acc[0][b][r] + bias);
+                    scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] =
+                        f32_to_f16(acc[0][b][r] + bias_v[b]);
             }
             _Float16 *dst0 = n0 < H ? epi.q : epi.k;
+            int rmv[4];  // row map entries, all loaded before the first store
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                rmv[i] = epi.rowmap[min(m0 + wm * 32 + ((lane + 64 * i) >> 3), M - 1)];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
                 const int m = m0 + wm * 32 + row, n = n0 + wn * 64 + c;
                 if (m >= M || n >= N) continue;
                 const int hd = n % H, h = hd / epi.d_head, d = hd - h * epi.d_head;
-                const int rm = epi.rowmap[m];
+                const int rm = rmv[i];
                 const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                 const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
                 *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
@@ -476,11 +499,19 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             return;
         }
         }
+        // the row map of this lane's rows, all loaded before the first store
+        int rmv[TM][16];
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                rmv[a][r] = epi.rowmap[min(m, M - 1)];
+            }
 #pragma unroll
         for (int b = 0; b < TN; ++b) {
             const int n = n0 + wcol0 + b * 32;
             if (n >= N) continue;
-            const float bias = epi.bias[n];
             const int part = n / H, hd = n - part * H;
             const int h = hd / epi.d_head, d = hd - h * epi.d_head;
             _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
@@ -490,39 +521,52 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     if (m >= M) continue;
-                    const int rm = epi.rowmap[m];
+                    const int rm = rmv[a][r];
                     const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                     const int pos = rm & 0xffff;
                     const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
                                                  : (sh * epi.dv_pad + d) * epi.len_pad + pos;
-                    dst[off] = f32_to_f16(acc[a][b][r] + bias);
+                    dst[off] = f32_to_f16(acc[a][b][r] + bias_v[b]);
                 }
         }
         return;
     }
 
+    // (mm + bias) [GELU | + residual] in acc, every residual load issued
+    // before the first store (y may be the residual itself: each element is
+    // read before it is written, and by the lane that writes it)
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int n = n0 + wcol0 + b * 32;
+            const int nc = min(n, N - 1);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = acc[a][b][r];
+                if (EPI == EPI_BIAS) {
+                    v = v + bias_v[b];
+                } else if (EPI == EPI_BIAS_GELU) {
+                    v = gelu_tanh(v + bias_v[b]);
+                } else if (EPI == EPI_BIAS_RESID) {
+                    const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int mc = min(m, M - 1);
+                    const int rm = epi.resid_rows > 0 && epi.resid_rows < M ? mc % (int)epi.resid_rows : mc;
+                    v = (v + bias_v[b]) + epi.resid[(int64_t)rm * epi.ld_resid + nc];
+                }
+                acc[a][b][r] = v;
+            }
+        }
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b) {
             const int n = n0 + wcol0 + b * 32;
             if (n >= N) continue;
-            float bias = 0.0f;
-            if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID) bias = epi.bias[n];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m >= M) continue;
-                float v = acc[a][b][r];
-                if (EPI == EPI_BIAS) {
-                    v = v + bias;
-                } else if (EPI == EPI_BIAS_GELU) {
-                    v = gelu_tanh(v + bias);
-                } else if (EPI == EPI_BIAS_RESID) {
-                    const int64_t rm = epi.resid_rows > 0 ? (int64_t)m % epi.resid_rows : (int64_t)m;
-                    v = (v + bias) + epi.resid[rm * epi.ld_resid + n];
-                }
-                y[(int64_t)m * ldy + n] = v;
+                if (m < M) y[(int64_t)m * ldy + n] = acc[a][b][r];
             }
         }
 }
