@@ -51,9 +51,10 @@ constexpr int GM = 8;         // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
 template <int BM_, int NS_, bool PIPE_, int TM_ = 2, bool SKEW_ = true, bool I8_ = false,
-          int TN_ = 2>
+          int TN_ = 2, int KS_ = 1>
 struct Cfg {
     static constexpr int BM = BM_, NS = NS_, TM = TM_;  // TM: 32-row subtiles per wave
+    static constexpr int KS = KS_;  // K blocks per stage (one barrier per stage)
     static constexpr int TN = TN_;                      // TN: 32-column subtiles per wave
     static constexpr int BN = 2 * 32 * TN;              // two waves along N
     static constexpr bool I8 = I8_;      // int8 quants, v_mfma_i32_32x32x32_i8 block dots
@@ -73,12 +74,15 @@ struct Cfg {
     static constexpr int Z_OFF = DW_OFF + BN * 2;       // 16 zero bytes
     static constexpr int STAGE = Z_OFF + 16;
     // the stage ring, or the epilogues' 32 x 144-byte scratch rows per wave
-    static constexpr int LDS = NS * STAGE > NWAVE * 32 * 144 ? NS * STAGE : NWAVE * 32 * 144;
+    static constexpr int LDS =
+        NS * KS * STAGE > NWAVE * 32 * 144 ? NS * KS * STAGE : NWAVE * 32 * 144;
     static_assert(BM % (32 * TM) == 0 && (TM == 1 || TM == 2) && (TN == 1 || TN == 2) && QI >= 1 &&
                       (BM + BN) * CH == QI * NT && (BM * CH) % WAVE == 0 && BM / 8 <= WAVE &&
                       BN / 8 <= WAVE && (!I8 || TM == 1),
                   "config");
-    static_assert(NS >= 2 && NS <= (PIPE ? 4 : 8), "wait table / unroll");
+    static_assert(NS >= 2 && NS <= (PIPE ? 4 : 8) && KS >= 1 && (KS == 1 || !PIPE) &&
+                      (NS - 2) * KS <= 6,
+                  "wait table / unroll");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
     };
 
     // the zero words read by lanes 32..63 for the scale operands
-    if (tid < NS) *reinterpret_cast<v4i *>(lds + tid * C::STAGE + C::Z_OFF) = v4i{0, 0, 0, 0};
+    if (tid < NS * C::KS) *reinterpret_cast<v4i *>(lds + tid * C::STAGE + C::Z_OFF) = v4i{0, 0, 0, 0};
 
     float acc[TM][TN][16];
 #pragma unroll
@@ -329,7 +333,46 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
         pending = true;
     };
 
-    if constexpr (!C::PIPE) {
+    if constexpr (C::KS > 1) {
+        // Stages of KS blocks (KS sub-buffers each), NS-1 stages in flight,
+        // one wait + barrier per stage; the blocks of a stage are separated
+        // by scheduling barriers so that only one block's fragments are live.
+        constexpr int KS = C::KS;
+        const int n_stages = (KB + KS - 1) / KS;
+        auto issue_stage = [&](int st, int sbuf) {
+#pragma unroll
+            for (int j = 0; j < KS; ++j)
+                if (st * KS + j < KB) issue(st * KS + j, sbuf * KS + j);
+        };
+        const int npro = min(NS - 1, n_stages);
+        for (int st = 0; st < npro; ++st) issue_stage(st, st);
+        Frag F;
+        F.zero_scales();
+        auto stage = [&](int st, auto bufc) {
+            constexpr int sbuf = decltype(bufc)::value;
+            // blocks issued after this stage's: those of the next
+            // min(NS - 2, n_stages - 1 - st) stages (the last one may be short)
+            const int later = min(st + NS - 1, n_stages) - (st + 1);
+            const int later_blocks = later <= 0 ? 0 : min(later * KS, KB - (st + 1) * KS);
+            wait_stage<C>(scale_wave, later_blocks);
+            block_sync_lds();
+            if (st + NS - 1 < n_stages) issue_stage(st + NS - 1, (sbuf + NS - 1) % NS);
+            unroll_const<0, KS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (st * KS + j < KB) {
+                    load_frag(lds + (sbuf * KS + j) * C::STAGE, F);
+                    mma(F);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        for (int st = 0; st < n_stages; st += NS) {
+            unroll_const<0, NS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (st + j < n_stages) stage(st + j, jc);
+            });
+        }
+    } else if constexpr (!C::PIPE) {
         // NS-1 blocks in flight; stage s+NS-1 refills the buffer of stage
         // s-1.  The stage loop is unrolled NS times so each LDS read's stage
         // offset is an instruction immediate.
@@ -712,7 +755,7 @@ hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *
                          hipStream_t stream) {
     if (M == 0 || w.N == 0) return hipSuccess;
     if (!w.qs || !mmq_args_ok(w, xq, xdT, ld_dx, M)) return hipErrorInvalidValue;
-    using Big = mmq16::Cfg<128, 3, false, 1, true, true, 2>;
+    using Big = mmq16::Cfg<128, 2, false, 1, true, true, 2, 3>;
     using Small = mmq16::Cfg<64, 3, false, 1, true, true, 1>;
     return mmq16::launch_tail_split<Big, Small>(w, reinterpret_cast<const uint8_t *>(xq), w.K_pad,
                                                 xdT, ld_dx, M, y, ldy, epi, stream);
