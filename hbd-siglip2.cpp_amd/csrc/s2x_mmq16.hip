@@ -60,6 +60,13 @@ struct Cfg {
     static constexpr bool I8 = I8_;      // int8 quants, v_mfma_i32_32x32x32_i8 block dots
     static constexpr int ROWB = QK * (I8 ? 1 : 2);  // bytes of one block of one row
     static constexpr int CH = ROWB / 16;            // 16-byte chunks per row and block
+    // Chunk permutation of tile row r (only r's low 5 bits matter).  A
+    // fragment read has each lane take one 16-byte chunk of its own row;
+    // the permutation spreads the chunks of rows r, r + 4, r + 8, r + 12
+    // over distinct LDS banks.
+    static __device__ __forceinline__ int swz(int r) {
+        return CH == 2 ? ((r >> 2) ^ (r >> 3)) & 1 : (r >> 2) & (CH - 1);
+    }
     static constexpr bool PIPE = PIPE_;  // next block's fragments read during this block's MFMAs
     static constexpr bool SKEW = SKEW_;  // a subtile's fmas issued after the next one's MFMAs
     static constexpr int WGM = BM / (32 * TM);          // waves along M (2 along N)
@@ -177,7 +184,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
 
     // Buffers over this tile's rows: rows past M / N read as zeros (their
     // outputs are never stored).  Position p (16-byte unit) of a stage's X
-    // (then W) rows holds chunk (p % CH) ^ ((row >> 2) & (CH - 1)) of row
+    // (then W) rows holds chunk (p % CH) ^ C::swz(row) of row
     // p / CH.
     const auto clip = [](int64_t bytes) { return (int)min(bytes, (int64_t)0x7fffffff); };
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -189,7 +196,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
     for (int i = 0; i < C::QI; ++i) {
         const int p = i * NT + tid;
         const int pr = p < BM * CH ? p : p - BM * CH;  // position within X or W
-        const int row = pr / CH, chunk = (pr % CH) ^ ((row >> 2) & (CH - 1));
+        const int row = pr / CH, chunk = (pr % CH) ^ C::swz(row);
         qv[i] = (uint32_t)(row * row_bytes) + (uint32_t)chunk * 16;
     }
     // wave 0: X scales (BM/8 lanes x 8), wave 1: W scales (BN/8 lanes x 8)
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
         const int n = n0 + wcol0 + b * 32;
         bias_v[b] = EPI != EPI_NONE && EPI != EPI_DUMP_I && n < N ? epi.bias[n] : 0.0f;
     }
-    const int sw = (lr >> 2) & (CH - 1);  // chunk permutation of the rows this lane reads
+    const int sw = C::swz(lr);  // chunk permutation of the rows this lane reads
     // k slots 8 lh .. 8 lh + 7 (f16: of each 16-value half) / 16 lh .. +15 (int8)
     const int c0 = (lh ^ sw) * 16, c1 = ((2 + lh) ^ sw) * 16;
     const int xo = xrow0 * ROWB, wo = C::X_BYTES + wcol0 * ROWB;
