@@ -174,10 +174,13 @@ __global__ __launch_bounds__(256) void k_attn(
     const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
     const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
     const int32_t *__restrict__ seg_len, const uint8_t *__restrict__ key_valid,
-    int n_head, int d_head, int len_pad, float scale_log2, float *__restrict__ out,
+    int n_head, int d_head, int len_pad, int n_qt, float scale_log2, float *__restrict__ out,
     int64_t ld_out) {
     __shared__ __align__(16) _Float16 lds[2 * FA_STAGE];
-    const int qt = blockIdx.x, h = blockIdx.y, sg = blockIdx.z;
+    // (query tile, head, segment), query tile fastest, in XCD-contiguous
+    // order: the query tiles of one head share their XCD's L2 for K and V^T
+    const int wg = xcd_linear(blockIdx.x, gridDim.x);
+    const int qt = wg % n_qt, h = (wg / n_qt) % n_head, sg = wg / (n_qt * n_head);
     const int len = seg_len[sg];
     if (qt * 128 >= len) return;  // whole workgroup past the segment
     const int64_t row0 = seg_start[sg];
@@ -414,13 +417,15 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     if (L.d_pad != FA_DP || L.dv_pad != FA_DV || (L.d_head % 4) != 0) return hipErrorInvalidValue;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
     const float log2e = 1.4426950408889634f;
-    const dim3 grid((unsigned)((L.max_len + 127) / 128), (unsigned)L.n_head, (unsigned)L.n_seg);
+    const int64_t n_qt = (L.max_len + 127) / 128;
+    const int64_t n_wg = n_qt * L.n_head * L.n_seg;
+    if (n_wg > 0x7fffffff) return hipErrorInvalidValue;
     auto kern = L.p_split ? k_attn<true> : k_attn<false>;
-    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream,
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(256), 0, stream,
                        reinterpret_cast<const _Float16 *>(base + L.q_off),
                        reinterpret_cast<const _Float16 *>(base + L.k_off),
                        reinterpret_cast<const _Float16 *>(base + L.vt_off), seg_start, seg_len,
-                       key_valid, (int)L.n_head, (int)L.d_head, (int)L.len_pad,
+                       key_valid, (int)L.n_head, (int)L.d_head, (int)L.len_pad, (int)n_qt,
                        scale * log2e, out, ld_out);
     return hipGetLastError();
 }

@@ -193,6 +193,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return x / (1.0f + exp_cw(t));
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
+// XCD b % 8), each with its own L2.  xcd_linear(b, G) renumbers the G
+// workgroups of a launch so that each XCD takes one contiguous range of the
+// new order: workgroups adjacent in it share their XCD's L2 (a bijection on
+// 0 .. G-1; XCDs below G % 8 take one index more).
+__device__ __forceinline__ int xcd_linear(int bid, int G) {
+    constexpr int NX = 8;
+    if (G < NX) return bid;
+    const int xcd = bid % NX, local = bid / NX;
+    const int per = G / NX, rem = G % NX;
+    return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
 // Output tile order: XCD-aware (gfx950 dispatches workgroup i to XCD i % 8,
 // so consecutive tile ids are given to the same XCD) and grouped (GM rows of
 // tiles walk N together) so an XCD's concurrent workgroups share X and W
@@ -200,14 +213,7 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 template <int GM>
 __device__ __forceinline__ void tile_coords(int bid, int G, int m_tiles, int n_tiles,
                                             int &tm, int &tn) {
-    constexpr int NX = 8;
-    int t = bid;
-    if (G >= NX) {
-        const int xcd = bid % NX, local = bid / NX;
-        const int per = G / NX, rem = G % NX;
-        // xcd < rem own per+1 tiles, the rest per
-        t = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    }
+    const int t = xcd_linear(bid, G);
     const int group_size = GM * n_tiles;
     const int group = t / group_size;
     const int first_m = group * GM;
