@@ -157,8 +157,11 @@ hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_b
 }
 
 // ---------------------------------------------------------------------------
-// flash attention: one workgroup = 4 waves x 32 queries of one (segment,
-// head); 64-key tiles of K and V^T staged through LDS (double buffered).
+// flash attention: one workgroup = FA_WAVES waves x 32 queries of one
+// (segment, head); 64-key tiles of K and V^T staged through LDS (double
+// buffered).  12 waves: each thread stages one K and one V^T chunk per
+// tile, which keeps the kernel at 151 VGPRs, i.e. 3 waves per SIMD -- one
+// workgroup per CU, and 1,024 workgroups (4 full rounds) at 32 x 729.
 // Specialised for d_pad = 80 (5 k-steps) and dv_pad = 96 (3 row tiles).
 // ---------------------------------------------------------------------------
 constexpr int FA_DP = 80;              // Q/K row length (halves)
@@ -168,9 +171,10 @@ constexpr int FA_KP = FA_DP + 8;       // K tile pitch (halves): conflict-free 1
 constexpr int FA_VP = FA_KT + 8;       // V^T tile pitch (halves): 16-byte rows, conflict-free reads
 constexpr int FA_ONES = 88;            // V^T padding row held at 1.0: O^T row 88 = sum of P
 constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
+constexpr int FA_WAVES = 12;  // waves (32 queries each) per workgroup
 
-template <bool P_SPLIT>
-__global__ __launch_bounds__(256) void k_attn(
+template <bool P_SPLIT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn(
     const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
     const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
     const int32_t *__restrict__ seg_len, const uint8_t *__restrict__ key_valid,
@@ -182,7 +186,8 @@ __global__ __launch_bounds__(256) void k_attn(
     const int wg = xcd_linear(blockIdx.x, gridDim.x);
     const int qt = wg % n_qt, h = (wg / n_qt) % n_head, sg = wg / (n_qt * n_head);
     const int len = seg_len[sg];
-    if (qt * 128 >= len) return;  // whole workgroup past the segment
+    constexpr int NT = 64 * NW, QT = 32 * NW;  // threads, queries per workgroup
+    if (qt * QT >= len) return;  // whole workgroup past the segment
     const int64_t row0 = seg_start[sg];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, lh = lane >> 5;
@@ -192,12 +197,15 @@ __global__ __launch_bounds__(256) void k_attn(
     const _Float16 *Vh = Vt + head_vt;
 
     // Q^T fragments (B operand): lane holds query q, d = 16 t + 8 lh + s
-    const int q = qt * 128 + wave * 32 + lr;
-    const bool active = __builtin_amdgcn_readfirstlane(qt * 128 + wave * 32) < len;
+    const int q = qt * QT + wave * 32 + lr;
+    const bool active = __builtin_amdgcn_readfirstlane(qt * QT + wave * 32) < len;
+    // (a workgroup's last queries may lie past len_pad, a multiple of 128:
+    // they read row len_pad - 1 and are never stored)
+    const int qrow = min(q, len_pad - 1);
     v8h qf[5];
 #pragma unroll
     for (int t = 0; t < 5; ++t)
-        qf[t] = *reinterpret_cast<const v8h *>(Q + head_qk + (int64_t)q * FA_DP + 16 * t + 8 * lh);
+        qf[t] = *reinterpret_cast<const v8h *>(Q + head_qk + (int64_t)qrow * FA_DP + 16 * t + 8 * lh);
 
     v16f o[3];
 #pragma unroll
@@ -208,17 +216,21 @@ __global__ __launch_bounds__(256) void k_attn(
 
     const int n_tiles = (len + FA_KT - 1) / FA_KT;
 
-    // global -> registers for one key tile: K 64x80 halves (10240 B contiguous),
-    // V^T 96 rows x 64 halves (128 B each)
+    // global -> registers for one key tile: K 64x80 halves (10240 B contiguous,
+    // 640 chunks of 16 B), V^T 96 rows x 64 halves (128 B each, 768 chunks)
+    constexpr int K_CH = FA_KT * FA_DP / 8, V_CH = FA_DV * FA_KT / 8;
+    constexpr int KC = (K_CH + NT - 1) / NT, VC = (V_CH + NT - 1) / NT;
     struct Tile {
-        uint4 k0, k1, k2, v0, v1, v2;
+        uint4 k[KC], v[VC];
     };
-    // 640 K chunks of 16 B; threads past the end re-load the last chunk
-    // (always in bounds) and later rewrite it with the value it already has
-    const int kc0 = tid, kc1 = tid + 256, kc2 = min(tid + 512, FA_KT * FA_DP / 8 - 1);
+    // threads past the last K chunk re-load it (always in bounds) and later
+    // rewrite it with the value it already has
+    int kc[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i) kc[i] = min(tid + i * NT, K_CH - 1);
     auto vload = [&](int k0, int i, auto edgec) {
         constexpr bool edge = decltype(edgec)::value;
-        const int c = tid + i * 256;  // 768 chunks: row c/8, col (c%8)*8 halves
+        const int c = tid + i * NT;  // V chunk c: row c/8, col (c%8)*8 halves
         const int r = c >> 3, cc = (c & 7) * 8;
         uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
         // keys past the segment hold zeros or stale finite data; zero them so
@@ -238,12 +250,11 @@ __global__ __launch_bounds__(256) void k_attn(
         const int k0 = t * FA_KT;
         const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
         Tile g;
-        g.k0 = ks[kc0];
-        g.k1 = ks[kc1];
-        g.k2 = ks[kc2];
-        g.v0 = vload(k0, 0, edgec);
-        g.v1 = vload(k0, 1, edgec);
-        g.v2 = vload(k0, 2, edgec);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) g.k[i] = ks[kc[i]];
+#pragma unroll
+        for (int i = 0; i < VC; ++i)
+            if (V_CH % NT == 0 || tid + i * NT < V_CH) g.v[i] = vload(k0, i, edgec);
         return g;
     };
     auto sstore = [&](int buf, const Tile &g) {
@@ -252,23 +263,22 @@ __global__ __launch_bounds__(256) void k_attn(
         const auto kput = [&](int c, uint4 v) {
             *reinterpret_cast<uint4 *>(kl + (c / 10) * FA_KP + (c % 10) * 8) = v;
         };
-        kput(kc0, g.k0);
-        kput(kc1, g.k1);
-        kput(kc2, g.k2);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) kput(kc[i], g.k[i]);
         // V^T rows keep each 16-key group in the order [0-3, 8-11, 4-7,
         // 12-15]: the 8 keys a lane feeds to one PV MFMA (4 lh + 0..3 and
         // 8 + 4 lh + 0..3, the S^T result layout) are then one 16-byte read
         const auto vput = [&](int i, uint4 v) {
-            const int c = tid + i * 256;
+            const int c = tid + i * NT;
             const int row = c >> 3, ch = c & 7;
             if (row == FA_ONES) v = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
             _Float16 *base = vl + row * FA_VP + (ch >> 1) * 16 + (ch & 1) * 4;
             *reinterpret_cast<uint2 *>(base) = make_uint2(v.x, v.y);
             *reinterpret_cast<uint2 *>(base + 8) = make_uint2(v.z, v.w);
         };
-        vput(0, g.v0);
-        vput(1, g.v1);
-        vput(2, g.v2);
+#pragma unroll
+        for (int i = 0; i < VC; ++i)
+            if (V_CH % NT == 0 || tid + i * NT < V_CH) vput(i, g.v[i]);
     };
 
     const int n_plain = key_valid ? 0 : len / FA_KT;  // whole tiles without a key mask
@@ -417,11 +427,12 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     if (L.d_pad != FA_DP || L.dv_pad != FA_DV || (L.d_head % 4) != 0) return hipErrorInvalidValue;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
     const float log2e = 1.4426950408889634f;
-    const int64_t n_qt = (L.max_len + 127) / 128;
+    constexpr int NW = FA_WAVES;
+    const int64_t n_qt = (L.max_len + 32 * NW - 1) / (32 * NW);
     const int64_t n_wg = n_qt * L.n_head * L.n_seg;
     if (n_wg > 0x7fffffff) return hipErrorInvalidValue;
-    auto kern = L.p_split ? k_attn<true> : k_attn<false>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(256), 0, stream,
+    auto kern = L.p_split ? k_attn<true, NW> : k_attn<false, NW>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(64 * NW), 0, stream,
                        reinterpret_cast<const _Float16 *>(base + L.q_off),
                        reinterpret_cast<const _Float16 *>(base + L.k_off),
                        reinterpret_cast<const _Float16 *>(base + L.vt_off), seg_start, seg_len,
