@@ -8,6 +8,7 @@ Importing this module loads the in-tree libs2x.so and fails loudly if it is
 missing: there is no CPU fallback.
 """
 import ctypes
+import importlib.util
 import os
 
 __all__ = [
@@ -26,6 +27,27 @@ if not os.path.exists(LIB_PATH):
         f"libs2x.so not found at {LIB_PATH}; build it with "
         "`python hbd-siglip2.cpp_amd/build.py` (no CPU fallback exists)")
 
+
+
+def _share_torch_hip_runtime():
+    """Load PyTorch's bundled HIP runtime first, when PyTorch is installed.
+
+    libs2x.so and PyTorch's ROCm build each bring a libamdhip64.so.7 (this
+    image: /opt/rocm's and torch/lib's).  The soname is the same, so the
+    process keeps whichever loads first for both; PyTorch fails to see any
+    GPU on the /opt/rocm copy ("No HIP GPUs are available"), while libs2x.so
+    runs on either.  Loading torch's copy (with RTLD_GLOBAL, without
+    importing torch) before libs2x.so makes the import order irrelevant.
+    """
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.origin:
+        return
+    hip = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
+    if os.path.exists(hip):
+        ctypes.CDLL(hip, mode=ctypes.RTLD_GLOBAL)
+
+
+_share_torch_hip_runtime()
 lib = ctypes.CDLL(LIB_PATH)
 
 
