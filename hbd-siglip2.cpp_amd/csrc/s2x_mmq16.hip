@@ -548,6 +548,64 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             }
             return;
         }
+        if (n0 >= 2 * H && H % BN == 0) {
+            // a V tile: V^T rows are positions, so the wave's 32 x 64 tile
+            // goes through LDS transposed (column-major, rows shifted by the
+            // first position's offset within its 8-position chunk) and each
+            // lane writes one column -- one d of one head: up to 32
+            // consecutive positions -- as 16-byte stores where the
+            // destination is 16-byte aligned, 2-byte stores at the ends
+            constexpr int PT = 48;  // halves per scratch column: shift <= 7 + 32 rows
+            static_assert(C::NWAVE * 64 * PT * 2 <= C::LDS, "epilogue scratch fits the stages");
+            const int mw = m0 + wm * 32;
+            const int rows = min(32, M - mw);  // wave-uniform, may be <= 0
+            int rm_first = 0, rm_last = 0;
+            if (rows > 0) {
+                rm_first = epi.rowmap[mw];
+                rm_last = epi.rowmap[mw + rows - 1];
+            }
+            // one segment, consecutive positions: the common case
+            const bool run = rows > 0 && (rm_last >> 16) == (rm_first >> 16) &&
+                             (rm_last & 0xffff) - (rm_first & 0xffff) == rows - 1;
+            const int shift = run ? (rm_first & 0xffff) & 7 : 0;
+            __syncthreads();
+            _Float16 *scr = reinterpret_cast<_Float16 *>(lds) + wave * 64 * PT;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        scr[(b * 32 + lr) * PT + shift + 8 * q + 4 * lh + j] =
+                            f32_to_f16(acc[0][b][4 * q + j] + bias_v[b]);
+            __syncthreads();
+            const int n = n0 + wn * 64 + lane;
+            if (rows <= 0 || n >= N) return;
+            const int hd = n - 2 * H, h = hd / epi.d_head, d = hd - h * epi.d_head;
+            const _Float16 *col = scr + lane * PT;
+            if (run) {
+                const int64_t sh = (int64_t)(rm_first >> 16) * epi.n_head + h;
+                _Float16 *dst = epi.vt + (sh * epi.dv_pad + d) * epi.len_pad + (rm_first & 0xffff) - shift;
+                // positions [shift, shift + rows) of the 8-aligned window dst[0 ..)
+                const int lo = shift, hi = shift + rows;
+                const int a0 = (lo + 7) & ~7, a1 = hi & ~7;
+                if (a0 <= a1) {
+                    for (int i = lo; i < a0; ++i) dst[i] = col[i];
+                    for (int i = a0; i < a1; i += 8)
+                        *reinterpret_cast<v8h *>(dst + i) = *reinterpret_cast<const v8h *>(col + i);
+                    for (int i = a1; i < hi; ++i) dst[i] = col[i];
+                } else {
+                    for (int i = lo; i < hi; ++i) dst[i] = col[i];
+                }
+            } else {
+                for (int i = 0; i < rows; ++i) {
+                    const int rm = epi.rowmap[mw + i];
+                    const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                    epi.vt[(sh * epi.dv_pad + d) * epi.len_pad + (rm & 0xffff)] = col[i];
+                }
+            }
+            return;
+        }
         }
         // the row map of this lane's rows, all loaded before the first store
         int rmv[TM][16];
