@@ -228,36 +228,26 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
     int kc[KC];
 #pragma unroll
     for (int i = 0; i < KC; ++i) kc[i] = min(tid + i * NT, K_CH - 1);
-    auto vload = [&](int k0, int i, auto edgec) {
-        constexpr bool edge = decltype(edgec)::value;
-        const int c = tid + i * NT;  // V chunk c: row c/8, col (c%8)*8 halves
-        const int r = c >> 3, cc = (c & 7) * 8;
-        uint4 v = *reinterpret_cast<const uint4 *>(Vh + (int64_t)r * len_pad + k0 + cc);
-        // keys past the segment hold zeros or stale finite data; zero them so
-        // a stale NaN/Inf can never meet a zero probability (only the tile
-        // holding the segment end has such keys)
-        const int valid = len - (k0 + cc);
-        if (edge && valid < 8) {
-            const auto keep = [valid](int j) {
-                return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
-            };
-            v = make_uint4(v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3));
-        }
-        return v;
-    };
-    auto gload = [&](int t, auto edgec) {
-        constexpr bool edge = decltype(edgec)::value;
+    // One code path for every tile (the edge masking happens at the LDS
+    // store): the next tile's loads stay in flight through the current
+    // tile's MFMAs, with no merge of differently loaded registers that would
+    // make the compiler wait for them right after issue.
+    auto gload = [&](int t) {
         const int k0 = t * FA_KT;
         const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
         Tile g;
 #pragma unroll
         for (int i = 0; i < KC; ++i) g.k[i] = ks[kc[i]];
 #pragma unroll
-        for (int i = 0; i < VC; ++i)
-            if (V_CH % NT == 0 || tid + i * NT < V_CH) g.v[i] = vload(k0, i, edgec);
+        for (int i = 0; i < VC; ++i) {
+            const int c = tid + i * NT;  // V chunk c: row c/8, col (c%8)*8 halves
+            if (V_CH % NT == 0 || c < V_CH)
+                g.v[i] = *reinterpret_cast<const uint4 *>(Vh + (int64_t)(c >> 3) * len_pad + k0 +
+                                                          (c & 7) * 8);
+        }
         return g;
     };
-    auto sstore = [&](int buf, const Tile &g) {
+    auto sstore = [&](int buf, int t, const Tile &g) {
         _Float16 *kl = lds + buf * FA_STAGE;
         _Float16 *vl = kl + FA_KT * FA_KP;
         const auto kput = [&](int c, uint4 v) {
@@ -271,6 +261,16 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
         const auto vput = [&](int i, uint4 v) {
             const int c = tid + i * NT;
             const int row = c >> 3, ch = c & 7;
+            // keys past the segment hold zeros or stale finite data; zero
+            // them so a stale NaN/Inf can never meet a zero probability
+            // (only the tile holding the segment end has such keys)
+            const int valid = len - (t * FA_KT + ch * 8);
+            if (valid < 8) {
+                const auto keep = [valid](int j) {
+                    return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
+                };
+                v = make_uint4(v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3));
+            }
             if (row == FA_ONES) v = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
             _Float16 *base = vl + row * FA_VP + (ch >> 1) * 16 + (ch & 1) * 4;
             *reinterpret_cast<uint2 *>(base) = make_uint2(v.x, v.y);
@@ -282,21 +282,15 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
     };
 
     const int n_plain = key_valid ? 0 : len / FA_KT;  // whole tiles without a key mask
-    if (n_plain == 0)
-        sstore(0, gload(0, std::true_type{}));
-    else
-        sstore(0, gload(0, std::false_type{}));
+    sstore(0, 0, gload(0));
     __syncthreads();
 
     // one 64-key tile; MASK: the tile holding the segment end, or a key mask
     auto tile = [&](int t, auto maskc) {
         constexpr bool MASK = decltype(maskc)::value;
         const int buf = t & 1;
-        Tile nxt{};
-        if (t + 1 < n_plain)
-            nxt = gload(t + 1, std::false_type{});
-        else if (t + 1 < n_tiles)
-            nxt = gload(t + 1, std::true_type{});
+        // (past the last tile: the last tile again, never stored)
+        const Tile nxt = gload(min(t + 1, n_tiles - 1));
         const _Float16 *kl = lds + buf * FA_STAGE;
         const _Float16 *vl = kl + FA_KT * FA_KP;
         // a wave whose 32 queries all lie past the segment end only stages
@@ -393,7 +387,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
             }
         }
         }
-        if (t + 1 < n_tiles) sstore(buf ^ 1, nxt);
+        if (t + 1 < n_tiles) sstore(buf ^ 1, t + 1, nxt);
         __syncthreads();
     };
     // whole tiles without a key mask take the unmasked instance
