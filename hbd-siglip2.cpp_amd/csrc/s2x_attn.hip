@@ -548,6 +548,7 @@ hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bi
 // f16 as the reference's FA inputs are.  One workgroup per (head, segment).
 // ---------------------------------------------------------------------------
 constexpr int A1_MAXLEN = (int)MAX_SEG_LEN;
+constexpr int A1_GROUPS = 16;  // key groups of the PV pass
 
 __global__ __launch_bounds__(256) void k_attn_1q(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -555,7 +556,7 @@ __global__ __launch_bounds__(256) void k_attn_1q(
     int n_head, int d_head, float scale, float *__restrict__ out) {
     __shared__ float p[A1_MAXLEN];
     __shared__ float red[256];
-    __shared__ float part[4][128];
+    __shared__ float part[A1_GROUPS][128];
     const int h = blockIdx.x, sg = blockIdx.y;
     const int len = seg_len[sg];
     const int64_t row0 = seg_start[sg];
@@ -608,20 +609,42 @@ __global__ __launch_bounds__(256) void k_attn_1q(
         __syncthreads();
     }
     const float den = red[0];
-    // out[d] = sum_j p_j v[j][d] / den: 4 key groups x up to 128 dims
-    const int grp = threadIdx.x >> 6, dl = threadIdx.x & 63;
-    for (int d0 = 0; d0 < d_head; d0 += 64) {
-        const int d = d0 + dl;
-        float acc = 0.0f;
-        if (d < d_head)
-            for (int j = grp; j < len; j += 4)
-                acc = fmaf(p[j], (float)(_Float16)v[(row0 + j) * ld + h * d_head + d], acc);
-        part[grp][dl] = acc;
-        __syncthreads();
-        if (grp == 0 && d < d_head)
-            out[(int64_t)sg * H + h * d_head + d] =
-                ((part[0][dl] + part[1][dl]) + (part[2][dl] + part[3][dl])) / den;
-        __syncthreads();
+    // out[d] = sum_j p_j v[j][d] / den: threads = key groups x 4-column
+    // chunks of the head (d_head 72: 14 groups x 18 chunks), each group's
+    // partial sums then added in group order
+    const int nch = (d_head + 3) / 4;
+    const int ng = min(256 / nch, A1_GROUPS);
+    const int grp = threadIdx.x / nch, ch = threadIdx.x - grp * nch;
+    if (grp < ng) {
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float *vh = v + h * d_head + 4 * ch;
+        if (v4 && (reinterpret_cast<uintptr_t>(v) & 15) == 0) {
+            for (int j = grp; j < len; j += ng) {
+                const float4 t = *reinterpret_cast<const float4 *>(vh + (row0 + j) * ld);
+                const float pj = p[j];
+                a[0] = fmaf(pj, (float)(_Float16)t.x, a[0]);
+                a[1] = fmaf(pj, (float)(_Float16)t.y, a[1]);
+                a[2] = fmaf(pj, (float)(_Float16)t.z, a[2]);
+                a[3] = fmaf(pj, (float)(_Float16)t.w, a[3]);
+            }
+        } else {
+            for (int j = grp; j < len; j += ng) {
+                const float *vr = vh + (row0 + j) * ld;
+                const float pj = p[j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (4 * ch + i < d_head) a[i] = fmaf(pj, (float)(_Float16)vr[i], a[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * ch + i < d_head) part[grp][4 * ch + i] = a[i];
+    }
+    __syncthreads();
+    if (threadIdx.x < d_head) {
+        float acc = part[0][threadIdx.x];
+        for (int g = 1; g < ng; ++g) acc = acc + part[g][threadIdx.x];
+        out[(int64_t)sg * H + h * d_head + threadIdx.x] = acc / den;
     }
 }
 
@@ -630,7 +653,7 @@ hipError_t launch_attn_1q(const float *q, const float *k, const float *v, int64_
                           int64_t n_head, int64_t d_head, float scale, float *out,
                           hipStream_t stream) {
     if (n_seg == 0) return hipSuccess;
-    if (d_head > 128) return hipErrorInvalidValue;  // the PV pass covers 2 x 64 dims
+    if (d_head > 128) return hipErrorInvalidValue;  // the PV partial sums hold 128 dims
     hipLaunchKernelGGL(k_attn_1q, dim3((unsigned)n_head, (unsigned)n_seg), dim3(256), 0, stream,
                        q, k, v, ld, seg_start, seg_len, (int)n_head, (int)d_head, scale, out);
     return hipGetLastError();
