@@ -555,7 +555,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             // lane writes one column -- one d of one head: up to 32
             // consecutive positions -- as 16-byte stores where the
             // destination is 16-byte aligned, 2-byte stores at the ends
-            constexpr int PT = 48;  // halves per scratch column: shift <= 7 + 32 rows
+            // halves per scratch column: shift <= 7 + 32 rows; 80-byte columns
+            // keep 16-byte alignment and put lanes 0..31 on 16 bank groups
+            constexpr int PT = 40;
             static_assert(C::NWAVE * 64 * PT * 2 <= C::LDS, "epilogue scratch fits the stages");
             const int mw = m0 + wm * 32;
             const int rows = min(32, M - mw);  // wave-uniform, may be <= 0
