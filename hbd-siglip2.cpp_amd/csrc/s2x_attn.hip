@@ -297,17 +297,20 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
         // tiles for the others
         if (active) {
         // S^T for the tile's two 32-key halves (raw q.k, unscaled)
-        v16f sc[2];
+        // (both halves' K fragments read up front, then the two
+        // independent MFMA chains interleaved)
+        v16f sc[2] = {};
+        v8h kf[2][5];
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            v16f acc = {};
+        for (int st = 0; st < 5; ++st)
 #pragma unroll
-            for (int st = 0; st < 5; ++st) {
-                const v8h kf = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], acc, 0, 0, 0);
-            }
-            sc[sub] = acc;
-        }
+            for (int sub = 0; sub < 2; ++sub)
+                kf[sub][st] = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
+#pragma unroll
+        for (int st = 0; st < 5; ++st)
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+                sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sub][st], qf[st], sc[sub], 0, 0, 0);
         // mask (only the tile holding the segment end, or a key mask), then
         // the tile max; one softmax rescale per 64 keys
         const int kbase = t * FA_KT;
