@@ -377,15 +377,24 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
                 pl0 = __builtin_bit_cast(v8h, v4u{lw[0], lw[1], lw[2], lw[3]});
                 pl1 = __builtin_bit_cast(v8h, v4u{lw[4], lw[5], lw[6], lw[7]});
             }
-            // O^T += V^T P^T (row FA_ONES of V^T is 1: O^T row FA_ONES sums P)
+            // O^T += V^T P^T (row FA_ONES of V^T is 1: O^T row FA_ONES sums P).
+            // Each o[j] takes its products in the order hh 0 (hi, lo), hh 1
+            // (hi, lo); consecutive MFMAs go to different j (independent).
+            v8h vf[3][2];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
+            for (int j = 0; j < 3; ++j)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const v8h vf = *reinterpret_cast<const v8h *>(vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 8 * lh);
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? ph1 : ph0, o[j], 0, 0, 0);
-                    if (P_SPLIT)
-                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, hh ? pl1 : pl0, o[j], 0, 0, 0);
+                for (int hh = 0; hh < 2; ++hh)
+                    vf[j][hh] = *reinterpret_cast<const v8h *>(vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 8 * lh);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? ph1 : ph0, o[j], 0, 0, 0);
+                if (P_SPLIT) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? pl1 : pl0, o[j], 0, 0, 0);
                 }
             }
         }
