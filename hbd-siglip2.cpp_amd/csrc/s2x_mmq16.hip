@@ -548,7 +548,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             }
             return;
         }
-        if (n0 >= 2 * H && H % BN == 0) {
+        constexpr int VT_PT = 40;  // halves per V^T scratch column (below)
+        constexpr bool VT_FITS = C::NWAVE * 64 * VT_PT * 2 <= C::LDS;
+        if (VT_FITS && n0 >= 2 * H && H % BN == 0) {
             // a V tile: V^T rows are positions, so the wave's 32 x 64 tile
             // goes through LDS transposed (column-major, rows shifted by the
             // first position's offset within its 8-position chunk) and each
@@ -557,8 +559,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             // destination is 16-byte aligned, 2-byte stores at the ends
             // halves per scratch column: shift <= 7 + 32 rows; 80-byte columns
             // keep 16-byte alignment and put lanes 0..31 on 16 bank groups
-            constexpr int PT = 40;
-            static_assert(C::NWAVE * 64 * PT * 2 <= C::LDS, "epilogue scratch fits the stages");
+            // (configurations whose LDS is smaller take the generic path)
+            constexpr int PT = VT_PT;
             const int mw = m0 + wm * 32;
             const int rows = min(32, M - mw);  // wave-uniform, may be <= 0
             int rm_first = 0, rm_last = 0;
