@@ -152,6 +152,15 @@ __device__ __forceinline__ void unroll_const(F &&f) {
     }
 }
 
+// a / b for 0 <= a < 2^20 and b >= 1, exact: the float estimate a * (1/b)
+// is within a/b * 2^-23 <= 1/8 of a/b, so one correction either way suffices
+__device__ __forceinline__ int small_div(int a, int b, float inv_b) {
+    int q = (int)((float)a * inv_b);
+    const int r = a - q * b;
+    q += (r >= b) - (r < 0);
+    return q;
+}
+
 // Waves 0 and 1 also fetch the X and the W scales.
 template <class C>
 __device__ __forceinline__ void wait_stage(bool scale_wave, int after) {
@@ -513,6 +522,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
         // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad] or
         // V^T [seg][head][dv_pad][pos]; padding slots are not written
         const int H = epi.n_head * epi.d_head;
+        const float inv_dh = 1.0f / (float)epi.d_head;
         if constexpr (TM == 1 && TN == 2) {
         if (n0 + BN <= 2 * H && H % BN == 0 && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
             // a Q or K tile (the q|k|v boundaries fall on tile edges): the
@@ -540,7 +550,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
                 const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
                 const int m = m0 + wm * 32 + row, n = n0 + wn * 64 + c;
                 if (m >= M || n >= N) continue;
-                const int hd = n % H, h = hd / epi.d_head, d = hd - h * epi.d_head;
+                const int hd = n0 < H ? n : n - H;  // the tile is all Q or all K
+                const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
                 const int rm = rmv[i];
                 const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                 const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
@@ -585,7 +596,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
             __syncthreads();
             const int n = n0 + wn * 64 + lane;
             if (rows <= 0 || n >= N) return;
-            const int hd = n - 2 * H, h = hd / epi.d_head, d = hd - h * epi.d_head;
+            const int hd = n - 2 * H, h = small_div(hd, epi.d_head, inv_dh);
+            const int d = hd - h * epi.d_head;
             const _Float16 *col = scr + lane * PT;
             if (run) {
                 const int64_t sh = (int64_t)(rm_first >> 16) * epi.n_head + h;
@@ -624,8 +636,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::TM == 
         for (int b = 0; b < TN; ++b) {
             const int n = n0 + wcol0 + b * 32;
             if (n >= N) continue;
-            const int part = n / H, hd = n - part * H;
-            const int h = hd / epi.d_head, d = hd - h * epi.d_head;
+            const int part = small_div(n, H, 1.0f / (float)H), hd = n - part * H;
+            const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
             _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
 #pragma unroll
             for (int a = 0; a < TM; ++a)
@@ -720,7 +732,7 @@ hipError_t dispatch(const WeightView &w, const void *xh, const uint16_t *xdT, in
         return run<C, EPI_GELU_Q81>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     case EPI_QKV:
         if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
-            epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head)
+            epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head || w.N >= (1 << 20))
             return hipErrorInvalidValue;
         return run<C, EPI_QKV>(w, xh, xdT, ld_dx, M, y, ldy, epi, stream);
     default: return hipErrorInvalidValue;
