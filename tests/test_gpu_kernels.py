@@ -219,9 +219,8 @@ def test_gemm_large_m_batch_invariant(orc, gemm_data):
 def test_drop_in_large_m(orc, gemm_data, label):
     # batch-32 row count through the drop-in (int8) GEMM: partial last row
     # tile (23328 = 182 * 128 + 32), partial column tile for fc1 (4304 =
-    # 33 * 128 + 80); for fc1 the rows past the last full round of 128 x 128
-    # tiles (the last 288) come from the second, 64 x 64-tile launch.  The
-    # checked rows include the last 40
+    # 33 * 128 + 80), a partly filled last round of tiles.  The checked rows
+    # include the last 40
     raw, N, K, K_pad = gemm_data[label]
     M = 23328
     say(f"drop-in {label} M=23328")
