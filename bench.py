@@ -76,7 +76,7 @@ def main():
                          "(1..4; default: the library's)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py runs on one GPU: this build has no multi-GPU path (the tower "
+        print("bench.py runs on one GPU: the library has no multi-GPU path (the tower "
               "shards as independent data-parallel replicas; see the design notes)",
               file=sys.stderr)
         sys.exit(2)

@@ -27,7 +27,7 @@ extern "C" {
 typedef enum {
     S2X_OK = 0,
     S2X_ERR_INVALID_ARG = 1,   /* bad shape / null pointer / misalignment */
-    S2X_ERR_UNSUPPORTED = 2,   /* shape or feature this build does not handle */
+    S2X_ERR_UNSUPPORTED = 2,   /* shape or feature the library does not handle */
     S2X_ERR_HIP = 3,           /* a HIP runtime call failed */
     S2X_ERR_WORKSPACE = 4,     /* caller workspace too small */
     S2X_ERR_OOM = 5,           /* device allocation failed */

@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of the SigLIP2 Q8_0 matmul hot path.
  *
- * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker and the timed CPU
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the tests' parity reference and the timed CPU
  * baseline, never part of the product.  Built with -ffp-contract=off so every
  * float operation rounds where the restated code rounds; fused multiply-adds
  * appear only as explicit fmaf() calls.

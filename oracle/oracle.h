@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
  * C++ encoders, the Python bindings) may include, link or call this code.
  * Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it,
- * and only as the checker / the timed CPU baseline.
+ * and only as the parity reference / the timed CPU baseline.
  *
  * The reference runs this path through ggml (dbrain/ggml fork, a git
  * submodule that is empty in the reference tree, commit unrecorded).  ggml's
