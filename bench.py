@@ -204,19 +204,18 @@ def main():
 
 def bench_preproc(args, np, torch, s2x):
     """The NaFlex front end on its own: B RGB images of 640 x 480 resized to
-    at most 729 patches of 16 x 16 and patchified (s2x_nf_preprocess_rgb_dev
-    per image, images already in HBM).  Roofline: HBM, algorithmic bytes =
-    the u8 image read + the f32 patch rows written."""
+    at most 729 patches of 16 x 16 and patchified (s2x_nf_preprocess_rgb_batch_dev:
+    one launch per pass for the batch, images already in HBM).  Roofline:
+    HBM, algorithmic bytes = the u8 images read + the f32 patch rows written."""
     B, H, W, MP, P = args.batch, 480, 640, 729, 16
     rng = np.random.default_rng(7)
-    imgs = [torch.from_numpy(rng.integers(0, 256, (H, W, 3), dtype=np.uint8)).to("cuda:0")
-            for _ in range(B)]
+    imgs = torch.from_numpy(rng.integers(0, 256, (B, H, W, 3), dtype=np.uint8)).to("cuda:0")
     th, tw = ctypes.c_int32(), ctypes.c_int32()
     s2x.call("s2x_nf_target_size", H, W, P, MP, ctypes.byref(th), ctypes.byref(tw))
     n_rows = (th.value // P) * (tw.value // P)
     feat = 3 * P * P
     out = torch.empty((B, n_rows * feat), dtype=torch.float32, device="cuda:0")
-    wsb = s2x.lib.s2x_nf_workspace_size(H, W, P, MP)
+    wsb = B * s2x.lib.s2x_nf_workspace_size(H, W, P, MP)
     ws = torch.empty((wsb,), dtype=torch.uint8, device="cuda:0")
     mean = np.array([0.5, 0.5, 0.5], np.float32)
     std = np.array([0.5, 0.5, 0.5], np.float32)
@@ -224,12 +223,11 @@ def bench_preproc(args, np, torch, s2x):
     nh, nw = ctypes.c_int32(), ctypes.c_int32()
 
     def step():
-        for i in range(B):
-            s2x.call("s2x_nf_preprocess_rgb_dev", ctypes.c_void_p(imgs[i].data_ptr()), H, W, MP, P,
-                     ctypes.c_float(1.0 / 255.0), mean.ctypes.data, std.ctypes.data,
-                     ctypes.c_void_p(out[i].data_ptr()), n_rows * feat, ctypes.byref(nh),
-                     ctypes.byref(nw), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(wsb),
-                     ctypes.c_void_p(stream))
+        s2x.call("s2x_nf_preprocess_rgb_batch_dev", ctypes.c_void_p(imgs.data_ptr()), B, H, W, MP,
+                 P, ctypes.c_float(1.0 / 255.0), mean.ctypes.data, std.ctypes.data,
+                 ctypes.c_void_p(out.data_ptr()), n_rows * feat, ctypes.byref(nh),
+                 ctypes.byref(nw), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(wsb),
+                 ctypes.c_void_p(stream))
 
     for _ in range(args.warmup):
         step()
@@ -254,13 +252,15 @@ def bench_preproc(args, np, torch, s2x):
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import pyoracle
         host_imgs = [im.cpu().numpy() for im in imgs[:8]]
+        done = 0
         c0 = time.perf_counter()
-        for im in host_imgs:
-            pyoracle.nf_preprocess_rgb(im, MP, p=P, fused=1)
+        while time.perf_counter() - c0 < 10.0:  # a bounded ~10 s sample
+            pyoracle.nf_preprocess_rgb(host_imgs[done % len(host_imgs)], MP, p=P, fused=1)
+            done += 1
         c1 = time.perf_counter()
-        cpu = {"value": round(len(host_imgs) / (c1 - c0), 2), "unit": "images/s", "cores": 1,
-               "kind": "port", "sample": f"{len(host_imgs)} images of the same 640x480 -> "
-                                         f"{n_rows}-patch workload, {c1 - c0:.2f} s"}
+        cpu = {"value": round(done / (c1 - c0), 2), "unit": "images/s", "cores": 1,
+               "kind": "port", "sample": f"{done} images (8 distinct) of the same 640x480 -> "
+                                         f"{n_rows}-patch workload, {c1 - c0:.1f} s"}
     rec = {
         "metric": f"images/sec NaFlex preprocessing 640x480 RGB -> {n_rows} patches of 16x16",
         "value": round(ips, 1), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
@@ -271,8 +271,8 @@ def bench_preproc(args, np, torch, s2x):
                    "global_batch": B, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(gbs / 8000.0, 4), "traffic": None,
-                     "kernel": "k_nf_vpass + k_nf_hpass (per image)",
-                     "avg_launch_ms": round(gpu_ms / B, 4), "launches": 2 * B * args.steps},
+                     "kernel": "k_nf_vpass + k_nf_hpass (one launch each per batch)",
+                     "avg_launch_ms": round(gpu_ms / 2, 4), "launches": 2 * args.steps},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -425,6 +425,38 @@ int s2x_nf_preprocess_rgb_dev(const uint8_t *rgb, int32_t h, int32_t w, int32_t 
     return S2X_OK;
 }
 
+int s2x_nf_preprocess_rgb_batch_dev(const uint8_t *rgb, int32_t n_img, int32_t h, int32_t w,
+                                    int32_t max_num_patches, int32_t patch, float rescale,
+                                    const float *mean, const float *std_, float *out,
+                                    int64_t out_cap, int32_t *n_h, int32_t *n_w, void *workspace,
+                                    size_t ws_bytes, void *stream) {
+    if (int st = check_nf(h, w, patch, max_num_patches, "nf_preprocess_rgb_batch_dev")) return st;
+    if (n_img <= 0 || n_img > 65535)
+        return fail(S2X_ERR_INVALID_ARG, "nf_preprocess_rgb_batch_dev: n_img %d not in 1..65535",
+                    n_img);
+    if (!rgb || !mean || !std_ || !out || !n_h || !n_w || !workspace)
+        return fail(S2X_ERR_INVALID_ARG, "nf_preprocess_rgb_batch_dev: null pointer");
+    const size_t need = (size_t)n_img * nf_workspace_bytes(h, w, patch, max_num_patches);
+    if (ws_bytes < need)
+        return fail(S2X_ERR_WORKSPACE, "nf_preprocess_rgb_batch_dev: workspace %zu < %zu bytes",
+                    ws_bytes, need);
+    int32_t th = 0, tw = 0;
+    nf_target_size(h, w, patch, max_num_patches, &th, &tw);
+    const int64_t need_out = (int64_t)(th / patch) * (tw / patch) * 3 * patch * patch;
+    if (out_cap < need_out)
+        return fail(S2X_ERR_INVALID_ARG,
+                    "nf_preprocess_rgb_batch_dev: out_cap %lld < %lld floats per image",
+                    (long long)out_cap, (long long)need_out);
+    int nh = 0, nw = 0;
+    hipError_t e = launch_nf_preprocess_batch(rgb, n_img, h, w, max_num_patches, patch, rescale,
+                                              mean, std_, out, out_cap, &nh, &nw, workspace,
+                                              ws_bytes, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "nf_preprocess_batch launch");
+    *n_h = nh;
+    *n_w = nw;
+    return S2X_OK;
+}
+
 int s2x_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows_table, const int32_t *ids,
                       int64_t n_ids, const float *add, int64_t add_rows, float *out,
                       void *stream) {

@@ -179,5 +179,12 @@ hipError_t launch_nf_preprocess(const uint8_t *rgb, int h, int w, int max_patche
                                 float rescale, const float mean[3], const float stdv[3],
                                 float *out, int64_t out_cap, int *n_h, int *n_w, void *ws,
                                 size_t ws_bytes, hipStream_t stream);
+// n_img same-size images, rgb contiguous (h*w*3 bytes each), out contiguous
+// (n_h*n_w*3*p*p floats each, out_cap >= that), ws >= n_img x
+// nf_workspace_bytes(): one launch per pass for the whole batch
+hipError_t launch_nf_preprocess_batch(const uint8_t *rgb, int n_img, int h, int w,
+                                      int max_patches, int p, float rescale, const float mean[3],
+                                      const float stdv[3], float *out, int64_t out_cap, int *n_h,
+                                      int *n_w, void *ws, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace s2x

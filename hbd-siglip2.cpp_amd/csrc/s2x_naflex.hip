@@ -78,11 +78,15 @@ __device__ inline float nf_weight(const NfAxis &a, const NfTaps &f, int t) {
     return (float)(w > 0.0 ? w : 0.0) * f.inv;
 }
 
-// pass 1: tmp[y][x][c], one thread per (y, x)
+// pass 1: tmp[y][x][c], one thread per (y, x); blockIdx.y = image of a
+// batch of same-size images (rgb_stride bytes / tmp_stride floats apart)
 __global__ __launch_bounds__(256) void k_nf_vpass(const uint8_t *__restrict__ rgb, int h, int w,
-                                                  int th, NfAxis ay, float *__restrict__ tmp) {
+                                                  int th, NfAxis ay, float *__restrict__ tmp,
+                                                  int64_t rgb_stride, int64_t tmp_stride) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)th * w) return;
+    rgb += blockIdx.y * rgb_stride;
+    tmp += blockIdx.y * tmp_stride;
     const int y = (int)(i / w), x = (int)(i - (int64_t)y * w);
     const NfTaps f = nf_taps(ay, y);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
@@ -101,13 +105,17 @@ __global__ __launch_bounds__(256) void k_nf_vpass(const uint8_t *__restrict__ rg
     out[2] = a2;
 }
 
-// pass 2 + rescale, normalise, patchify: one thread per (y, x)
+// pass 2 + rescale, normalise, patchify: one thread per (y, x); blockIdx.y
+// as in pass 1 (out_stride floats between images)
 __global__ __launch_bounds__(256) void k_nf_hpass(const float *__restrict__ tmp, int w, int th,
                                                   int tw, NfAxis ax, int p, float rescale,
                                                   float m0, float m1, float m2, float s0,
-                                                  float s1, float s2, float *__restrict__ out) {
+                                                  float s1, float s2, float *__restrict__ out,
+                                                  int64_t tmp_stride, int64_t out_stride) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)th * tw) return;
+    tmp += blockIdx.y * tmp_stride;
+    out += blockIdx.y * out_stride;
     const int y = (int)(i / tw), x = (int)(i - (int64_t)y * tw);
     const NfTaps f = nf_taps(ax, x);
     float a[3] = {0.0f, 0.0f, 0.0f};
@@ -155,27 +163,39 @@ size_t nf_workspace_bytes(int h, int w, int p, int max_patches) {
     return (size_t)th * (size_t)w * 3 * sizeof(float);
 }
 
-hipError_t launch_nf_preprocess(const uint8_t *rgb, int h, int w, int max_patches, int p,
-                                float rescale, const float mean[3], const float stdv[3],
-                                float *out, int64_t out_cap, int *n_h, int *n_w, void *ws,
-                                size_t ws_bytes, hipStream_t stream) {
-    if (!rgb || !out || !ws || h <= 0 || w <= 0 || p <= 0 || max_patches <= 0)
+hipError_t launch_nf_preprocess_batch(const uint8_t *rgb, int n_img, int h, int w,
+                                      int max_patches, int p, float rescale, const float mean[3],
+                                      const float stdv[3], float *out, int64_t out_cap, int *n_h,
+                                      int *n_w, void *ws, size_t ws_bytes, hipStream_t stream) {
+    if (!rgb || !out || !ws || n_img <= 0 || n_img > 65535 || h <= 0 || w <= 0 || p <= 0 ||
+        max_patches <= 0)
         return hipErrorInvalidValue;
     int th = 0, tw = 0;
     nf_target_size(h, w, p, max_patches, &th, &tw);
     const int nh = th / p, nw = tw / p;
-    if ((int64_t)nh * nw * 3 * p * p > out_cap || ws_bytes < (size_t)th * w * 3 * sizeof(float))
+    const int64_t out_stride = (int64_t)nh * nw * 3 * p * p;
+    const int64_t tmp_stride = (int64_t)th * w * 3;
+    if (out_stride > out_cap || ws_bytes < (size_t)n_img * (size_t)tmp_stride * sizeof(float))
         return hipErrorInvalidValue;
     float *tmp = reinterpret_cast<float *>(ws);
     const int64_t n1 = (int64_t)th * w, n2 = (int64_t)th * tw;
-    hipLaunchKernelGGL(k_nf_vpass, dim3((unsigned)((n1 + 255) / 256)), dim3(256), 0, stream, rgb,
-                       h, w, th, nf_axis(h, th), tmp);
-    hipLaunchKernelGGL(k_nf_hpass, dim3((unsigned)((n2 + 255) / 256)), dim3(256), 0, stream, tmp,
-                       w, th, tw, nf_axis(w, tw), p, rescale, mean[0], mean[1], mean[2], stdv[0],
-                       stdv[1], stdv[2], out);
+    hipLaunchKernelGGL(k_nf_vpass, dim3((unsigned)((n1 + 255) / 256), (unsigned)n_img), dim3(256),
+                       0, stream, rgb, h, w, th, nf_axis(h, th), tmp, (int64_t)h * w * 3,
+                       tmp_stride);
+    hipLaunchKernelGGL(k_nf_hpass, dim3((unsigned)((n2 + 255) / 256), (unsigned)n_img), dim3(256),
+                       0, stream, tmp, w, th, tw, nf_axis(w, tw), p, rescale, mean[0], mean[1],
+                       mean[2], stdv[0], stdv[1], stdv[2], out, tmp_stride, out_stride);
     *n_h = nh;
     *n_w = nw;
     return hipGetLastError();
+}
+
+hipError_t launch_nf_preprocess(const uint8_t *rgb, int h, int w, int max_patches, int p,
+                                float rescale, const float mean[3], const float stdv[3],
+                                float *out, int64_t out_cap, int *n_h, int *n_w, void *ws,
+                                size_t ws_bytes, hipStream_t stream) {
+    return launch_nf_preprocess_batch(rgb, 1, h, w, max_patches, p, rescale, mean, stdv, out,
+                                      out_cap, n_h, n_w, ws, ws_bytes, stream);
 }
 
 }  // namespace s2x

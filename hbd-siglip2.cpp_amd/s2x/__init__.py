@@ -127,6 +127,8 @@ _sig("s2x_nf_target_size", [_i32, _i32, _i32, _i32, _p, _p])
 _sig("s2x_nf_workspace_size", [_i32, _i32, _i32, _i32], _sz)
 _sig("s2x_nf_preprocess_rgb_dev", [_p, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _i64, _p, _p, _p,
                                    _sz, _p])
+_sig("s2x_nf_preprocess_rgb_batch_dev", [_p, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _i64,
+                                         _p, _p, _p, _sz, _p])
 _sig("s2x_attn_workspace_size", [_i64, _i64, _i64, _i64], _sz)
 _sig("s2x_attn_prep", [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p])
 _sig("s2x_attn_run", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])

@@ -216,6 +216,18 @@ int s2x_nf_preprocess_rgb_dev(const uint8_t *rgb, int32_t h, int32_t w,
                               const float *mean, const float *std_, float *out,
                               int64_t out_cap, int32_t *n_h, int32_t *n_w,
                               void *workspace, size_t ws_bytes, void *stream);
+/* s2x_nf_preprocess_rgb_batch_dev: n_img same-size images in one call (one  */
+/* launch per pass): rgb = n_img contiguous h*w*3 u8 images, out = n_img     */
+/* contiguous blocks of n_h*n_w*3*patch*patch floats (out_cap: floats per    */
+/* image available, >= one block), workspace >= n_img *                     */
+/* s2x_nf_workspace_size() bytes; each image's output equals                 */
+/* s2x_nf_preprocess_rgb_dev's.  No counterpart in the reference, which      */
+/* preprocesses one image per call (src/siglip2_preproc.cpp:217-251).        */
+int s2x_nf_preprocess_rgb_batch_dev(const uint8_t *rgb, int32_t n_img, int32_t h, int32_t w,
+                                    int32_t max_num_patches, int32_t patch, float rescale,
+                                    const float *mean, const float *std_, float *out,
+                                    int64_t out_cap, int32_t *n_h, int32_t *n_w,
+                                    void *workspace, size_t ws_bytes, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* a11  Q8_0 get_rows (replaces ggml_get_rows on the Q8_0 token table,        */

@@ -70,3 +70,35 @@ def test_preprocess_workspace_and_capacity_errors():
     assert s2x.lib.s2x_nf_preprocess_rgb_dev(*args(16 * 768, need)) == 0
     torch.cuda.synchronize()
     assert (nh.value, nw.value) == (4, 4)
+
+
+@pytest.mark.parametrize("h,w,mp,n_img", [(480, 640, 729, 5), (17, 23, 256, 3), (1000, 300, 729, 1)])
+def test_preprocess_batch_matches_per_image(h, w, mp, n_img):
+    # one call for n_img same-size images: each image's patches equal the
+    # single-image entry point's (and so the oracle's)
+    say(f"naflex batch {n_img} x {h}x{w} max_patches={mp}")
+    p = 16
+    rng = np.random.default_rng(20 + n_img)
+    imgs = rng.integers(0, 256, (n_img, h, w, 3), dtype=np.uint8)
+    d = dev(imgs)
+    th, tw = ctypes.c_int32(), ctypes.c_int32()
+    s2x.call("s2x_nf_target_size", h, w, p, mp, ctypes.byref(th), ctypes.byref(tw))
+    per = (th.value // p) * (tw.value // p) * 3 * p * p
+    out = empty((n_img * per,), torch.float32)
+    wsb = n_img * s2x.lib.s2x_nf_workspace_size(h, w, p, mp)
+    ws = empty((wsb,), torch.uint8)
+    nh, nw = ctypes.c_int32(), ctypes.c_int32()
+    s2x.call("s2x_nf_preprocess_rgb_batch_dev", ptr(d), n_img, h, w, mp, p,
+             ctypes.c_float(1.0 / 255.0), MEAN.ctypes.data, STD.ctypes.data, ptr(out), per,
+             ctypes.byref(nh), ctypes.byref(nw), ptr(ws), ctypes.c_size_t(wsb), stream())
+    got = host(out).reshape(n_img, per)
+    for i in range(n_img):
+        one, oh, ow = _gpu_preprocess(imgs[i], mp, p)
+        assert (nh.value, nw.value) == (oh, ow)
+        assert np.array_equal(got[i], one.reshape(-1)), f"image {i}"
+    # a workspace one byte short of n_img images is rejected before any launch
+    st = s2x.lib.s2x_nf_preprocess_rgb_batch_dev(
+        ptr(d), n_img, h, w, mp, p, ctypes.c_float(1.0 / 255.0), MEAN.ctypes.data,
+        STD.ctypes.data, ptr(out), per, ctypes.byref(nh), ctypes.byref(nw), ptr(ws),
+        ctypes.c_size_t(wsb - 1), stream())
+    assert st != 0
