@@ -20,9 +20,10 @@
 //   patchify      v = fma(u8, rescale, -mean) / std at row (y/p)*n_w + x/p,
 //                 column ((y%p)*p + x%p)*3 + c (:176-207)
 //
-// Each thread computes the filter of its own output row / column on the fly
-// (two passes over its taps: the double sum, then the normalised weights),
-// so no tables are built or uploaded.
+// The filters are set up on the GPU, once per output row in pass 1 (per
+// block) and once per output column and 16 rows in pass 2 (per thread): two
+// passes over the taps, the double sum, then the normalised weights, kept
+// in LDS; no tables are built on the host or uploaded.
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
@@ -78,64 +79,87 @@ __device__ inline float nf_weight(const NfAxis &a, const NfTaps &f, int t) {
     return (float)(w > 0.0 ? w : 0.0) * f.inv;
 }
 
-// pass 1: tmp[y][x][c], one thread per (y, x); blockIdx.y = image of a
-// batch of same-size images (rgb_stride bytes / tmp_stride floats apart)
+// pass 1: tmp[y][x][c]; a block is 256 columns of one output row y
+// (blockIdx.x = y, blockIdx.y = column chunk, blockIdx.z = image of a batch
+// of same-size images, rgb_stride bytes / tmp_stride floats apart).  The
+// row's filter is set up once per block: its tap weights in LDS when there
+// are at most NF_MAXT taps, else each thread evaluates them.
+constexpr int NF_MAXT = 64;
+
 __global__ __launch_bounds__(256) void k_nf_vpass(const uint8_t *__restrict__ rgb, int h, int w,
                                                   int th, NfAxis ay, float *__restrict__ tmp,
                                                   int64_t rgb_stride, int64_t tmp_stride) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)th * w) return;
-    rgb += blockIdx.y * rgb_stride;
-    tmp += blockIdx.y * tmp_stride;
-    const int y = (int)(i / w), x = (int)(i - (int64_t)y * w);
-    const NfTaps f = nf_taps(ay, y);
+    __shared__ float wts[NF_MAXT];
+    const int y = blockIdx.x, x = blockIdx.y * 256 + threadIdx.x;
+    rgb += blockIdx.z * rgb_stride;
+    tmp += blockIdx.z * tmp_stride;
+    const NfTaps f = nf_taps(ay, y);  // block-uniform
+    const bool cached = f.n <= NF_MAXT;
+    if (cached) {
+        if ((int)threadIdx.x < f.n) wts[threadIdx.x] = nf_weight(ay, f, threadIdx.x);
+        __syncthreads();
+    }
+    if (x >= w) return;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
     for (int t = 0; t < f.n; ++t) {
         int sy = f.k0 + t;
         sy = sy < 0 ? 0 : sy >= h ? h - 1 : sy;
-        const float wt = nf_weight(ay, f, t);
+        const float wt = cached ? wts[t] : nf_weight(ay, f, t);
         const uint8_t *sp = rgb + ((int64_t)sy * w + x) * 3;
         a0 = fmaf(wt, (float)sp[0], a0);
         a1 = fmaf(wt, (float)sp[1], a1);
         a2 = fmaf(wt, (float)sp[2], a2);
     }
-    float *out = tmp + i * 3;
+    float *out = tmp + ((int64_t)y * w + x) * 3;
     out[0] = a0;
     out[1] = a1;
     out[2] = a2;
 }
 
-// pass 2 + rescale, normalise, patchify: one thread per (y, x); blockIdx.y
-// as in pass 1 (out_stride floats between images)
+// pass 2 + rescale, normalise, patchify: a block is 256 output columns x
+// NF_RY output rows of one image (blockIdx.z as in pass 1, out_stride floats
+// between images).  Each thread sets up its column's filter once and keeps
+// the tap weights in LDS when there are at most NF_MAXT_H, then walks the
+// rows.
+constexpr int NF_RY = 16;
+constexpr int NF_MAXT_H = 16;
+
 __global__ __launch_bounds__(256) void k_nf_hpass(const float *__restrict__ tmp, int w, int th,
                                                   int tw, NfAxis ax, int p, float rescale,
                                                   float m0, float m1, float m2, float s0,
                                                   float s1, float s2, float *__restrict__ out,
                                                   int64_t tmp_stride, int64_t out_stride) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)th * tw) return;
-    tmp += blockIdx.y * tmp_stride;
-    out += blockIdx.y * out_stride;
-    const int y = (int)(i / tw), x = (int)(i - (int64_t)y * tw);
+    __shared__ float wts[NF_MAXT_H][256];
+    const int x = blockIdx.x * 256 + threadIdx.x, y0 = blockIdx.y * NF_RY;
+    if (x >= tw) return;  // no block-wide barrier below
+    tmp += blockIdx.z * tmp_stride;
+    out += blockIdx.z * out_stride;
     const NfTaps f = nf_taps(ax, x);
-    float a[3] = {0.0f, 0.0f, 0.0f};
-    for (int t = 0; t < f.n; ++t) {
-        int sx = f.k0 + t;
-        sx = sx < 0 ? 0 : sx >= w ? w - 1 : sx;
-        const float wt = nf_weight(ax, f, t);
-        const float *sp = tmp + ((int64_t)y * w + sx) * 3;
-        a[0] = fmaf(wt, sp[0], a[0]);
-        a[1] = fmaf(wt, sp[1], a[1]);
-        a[2] = fmaf(wt, sp[2], a[2]);
-    }
+    const bool cached = f.n <= NF_MAXT_H;
+    if (cached)
+        for (int t = 0; t < f.n; ++t) wts[t][threadIdx.x] = nf_weight(ax, f, t);
     const float mean[3] = {m0, m1, m2}, stdv[3] = {s0, s1, s2};
-    const int nw = tw / p, ph = y / p, py = y - ph * p, pw = x / p, px = x - pw * p;
-    float *dst = out + ((int64_t)ph * nw + pw) * (3 * p * p) + ((int64_t)py * p + px) * 3;
+    const int nw = tw / p, pw = x / p, px = x - pw * p;
+    const int y1 = min(y0 + NF_RY, th);
+    for (int y = y0; y < y1; ++y) {
+        float a[3] = {0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < f.n; ++t) {
+            int sx = f.k0 + t;
+            sx = sx < 0 ? 0 : sx >= w ? w - 1 : sx;
+            const float wt = cached ? wts[t][threadIdx.x] : nf_weight(ax, f, t);
+            const float *sp = tmp + ((int64_t)y * w + sx) * 3;
+            a[0] = fmaf(wt, sp[0], a[0]);
+            a[1] = fmaf(wt, sp[1], a[1]);
+            a[2] = fmaf(wt, sp[2], a[2]);
+        }
+        const int ph = y / p, py = y - ph * p;
+        float *dst = out + ((int64_t)ph * nw + pw) * (3 * p * p) + ((int64_t)py * p + px) * 3;
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        float r = __builtin_rintf(a[c]);  // lrintf: nearest, ties to even
-        r = r < 0.0f ? 0.0f : r > 255.0f ? 255.0f : r;
-        dst[c] = fmaf(r, rescale, -mean[c]) / stdv[c];
+        for (int c = 0; c < 3; ++c) {
+            float r = __builtin_rintf(a[c]);  // lrintf: nearest, ties to even
+            r = r < 0.0f ? 0.0f : r > 255.0f ? 255.0f : r;
+            dst[c] = fmaf(r, rescale, -mean[c]) / stdv[c];
+        }
     }
 }
 
@@ -178,11 +202,13 @@ hipError_t launch_nf_preprocess_batch(const uint8_t *rgb, int n_img, int h, int 
     if (out_stride > out_cap || ws_bytes < (size_t)n_img * (size_t)tmp_stride * sizeof(float))
         return hipErrorInvalidValue;
     float *tmp = reinterpret_cast<float *>(ws);
-    const int64_t n1 = (int64_t)th * w, n2 = (int64_t)th * tw;
-    hipLaunchKernelGGL(k_nf_vpass, dim3((unsigned)((n1 + 255) / 256), (unsigned)n_img), dim3(256),
-                       0, stream, rgb, h, w, th, nf_axis(h, th), tmp, (int64_t)h * w * 3,
-                       tmp_stride);
-    hipLaunchKernelGGL(k_nf_hpass, dim3((unsigned)((n2 + 255) / 256), (unsigned)n_img), dim3(256),
+    hipLaunchKernelGGL(k_nf_vpass, dim3((unsigned)th, (unsigned)((w + 255) / 256), (unsigned)n_img),
+                       dim3(256), 0, stream, rgb, h, w, th, nf_axis(h, th), tmp,
+                       (int64_t)h * w * 3, tmp_stride);
+    hipLaunchKernelGGL(k_nf_hpass,
+                       dim3((unsigned)((tw + 255) / 256), (unsigned)((th + NF_RY - 1) / NF_RY),
+                            (unsigned)n_img),
+                       dim3(256),
                        0, stream, tmp, w, th, tw, nf_axis(w, tw), p, rescale, mean[0], mean[1],
                        mean[2], stdv[0], stdv[1], stdv[2], out, tmp_stride, out_stride);
     *n_h = nh;
