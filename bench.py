@@ -2,7 +2,7 @@
 patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
-                    [--cpu-images 3] [--no-cpu] [--gemm i8|f16] [--lanes N]
+                    [--cpu-images 3] [--no-cpu]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
@@ -24,29 +24,19 @@ sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
-KERNELS = {
-    "i8": "k_mmq16<int8> (Q8_0 x Q8_1 GEMM: int8 quants by LDS DMA, v_mfma_i32_32x32x32_i8 "
-          "block dots, dx*dw scale tile on v_mfma_f32_32x32x8_f16, one convert + fma per "
-          "element and block; priced against the int8 peak)",
-    "f16": "k_mmq16<f16> (Q8_0 x Q8_1 GEMM: f16-coded quants, block dots on two "
-           "v_mfma_f32_32x32x16_f16, scale tile on v_mfma_f32_32x32x8_f16; priced against "
-           "the int8 peak)",
-}
-
-TRAFFIC_FILES = {
-    "i8": os.path.join(ROOT, "profiles", "mmq_i8_vision_b32_traffic.json"),
-    "f16": os.path.join(ROOT, "profiles", "mmq16_vision_b32_traffic.json"),
-}
+KERNEL = ("k_gemm (Q8_0 x Q8_1 GEMM, persistent 256x128 tiles: int8 quants and scales by LDS DMA, "
+          "v_mfma_i32_32x32x32_i8 block dots, dx*dw scale tile on v_mfma_f32_32x32x8_f16, one "
+          "convert + fma per element and block; priced against the int8 peak)")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_vision_b32_traffic.json")
 
 
-def traffic_per_launch(gemm):
+def traffic_per_launch():
     """HBM bytes per GEMM launch of this workload, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated on a copy kernel);
     None when not measured for this kernel."""
-    path = TRAFFIC_FILES.get(gemm)
-    if not path or not os.path.exists(path):
+    if not os.path.exists(TRAFFIC_FILE):
         return None
-    with open(path) as f:
+    with open(TRAFFIC_FILE) as f:
         return int(json.load(f)["bytes_per_launch"])
 
 
@@ -65,15 +55,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (a plain copy kernel "
                          "for calibrating HBM byte counters) and exit")
-    ap.add_argument("--gemm", choices=["i8", "f16"], default="i8",
-                    help="GEMM quant format: int8 quants on the int8 MFMA (default) or "
-                         "f16-coded quants on the f16 MFMA; same bits")
     ap.add_argument("--preproc", action="store_true",
                     help="instead of the tower: time the NaFlex front end (GPU resize + "
                          "patchify of a batch of RGB images) and print its own JSON line")
-    ap.add_argument("--lanes", type=int, default=0,
-                    help="row ranges (whole images) run concurrently on their own streams "
-                         "(1..4; default: the library's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: the library has no multi-GPU path (the tower "
@@ -108,10 +92,6 @@ def main():
     hm = synth.vision_model(cfg, seed=0)
     v = ctypes.c_void_p()
     s2x.call("s2x_vision_create", ctypes.byref(hm.struct), ctypes.byref(v))
-    s2x.call("s2x_vision_set_gemm_variant", v,
-             s2x.GEMM_F16_MFMA if args.gemm == "f16" else s2x.GEMM_I8_MFMA)
-    if args.lanes:
-        s2x.call("s2x_vision_set_lanes", v, args.lanes)
     stream = torch.cuda.ExternalStream  # noqa: F841 (the encoder owns its stream)
     px = synth.pixels(B, n_pos, seed=1234)
     pd = torch.from_numpy(px).to("cuda:0")
@@ -193,8 +173,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
-                     "traffic": traffic_per_launch(args.gemm),
-                     "kernel": KERNELS[args.gemm],
+                     "traffic": traffic_per_launch(),
+                     "kernel": KERNEL,
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "launches": int(launches.value)},
         "cpu_baseline": cpu,

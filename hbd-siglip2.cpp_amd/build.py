@@ -21,8 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     "s2x_quant.hip",
-    "s2x_mmq.hip",
-    "s2x_mmq16.hip",
+    "s2x_gemm.hip",
     "s2x_attn.hip",
     "s2x_misc.hip",
     "s2x_naflex.hip",

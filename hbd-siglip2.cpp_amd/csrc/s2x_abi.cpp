@@ -136,7 +136,7 @@ int64_t s2x_weight_n(const s2x_weight *w) { return w ? w->view.N : 0; }
 // ---------------------------------------------------------------------------
 // a3
 // ---------------------------------------------------------------------------
-static int check_epi(const s2x_epilogue *epi, EpiParams &p) {
+static int check_epi(const s2x_epilogue *epi, int64_t N, EpiParams &p) {
     p = EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0};
     if (!epi) return S2X_OK;
     p.kind = epi->kind;
@@ -151,30 +151,50 @@ static int check_epi(const s2x_epilogue *epi, EpiParams &p) {
         if (!epi->bias) return fail(S2X_ERR_INVALID_ARG, "epilogue: bias is null");
         return S2X_OK;
     case S2X_EPI_BIAS_RESID:
-        if (!epi->bias || !epi->resid || epi->ld_resid <= 0 || epi->resid_rows < 0)
+        if (!epi->bias || !epi->resid || epi->ld_resid < N || epi->resid_rows < 0)
             return fail(S2X_ERR_INVALID_ARG, "epilogue: bias/resid/ld_resid invalid");
+        return S2X_OK;
+    case S2X_EPI_GELU_Q81:
+        if (!epi->bias || !epi->q_out || !epi->q_ds || epi->q_kpad % QK_ || epi->q_kpad < N ||
+            epi->q_kpad - N >= QK_)
+            return fail(S2X_ERR_INVALID_ARG, "epilogue GELU_Q81: bias/q_out/q_ds/q_kpad invalid");
+        if (!aligned(epi->q_out, 16) || !aligned(epi->q_ds, 4))
+            return fail(S2X_ERR_INVALID_ARG, "epilogue GELU_Q81: q_out must be 16-byte aligned");
+        p.kind = EPI_GELU_Q81;
+        p.q_out8 = (int8_t *)epi->q_out;
+        p.q_ds = (uint32_t *)epi->q_ds;
+        p.q_kpad = epi->q_kpad;
+        p.q_ldds = epi->q_kpad / QK_;
         return S2X_OK;
     default: return fail(S2X_ERR_INVALID_ARG, "epilogue: unknown kind %d", epi->kind);
     }
 }
 
+static int check_q81_input(const s2x_weight *w, const void *qs, const void *ds, int64_t M,
+                           const char *who) {
+    if (!w) return fail(S2X_ERR_INVALID_ARG, "%s: weight is null", who);
+    if (M < 0) return fail(S2X_ERR_INVALID_ARG, "%s: M < 0", who);
+    if (M > (1 << 30)) return fail(S2X_ERR_UNSUPPORTED, "%s: M too large", who);
+    if (M > 0 && (!qs || !ds)) return fail(S2X_ERR_INVALID_ARG, "%s: null qs/ds", who);
+    if (!aligned(qs, 16) || !aligned(ds, 4))
+        return fail(S2X_ERR_INVALID_ARG, "%s: qs must be 16-byte and ds 4-byte aligned", who);
+    return S2X_OK;
+}
+
 int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds, int64_t M,
                           float *y, int64_t ldy, const s2x_epilogue *epi, void *stream) {
-    if (!w) return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: weight is null");
-    if (M < 0 || ldy < w->view.N)
-        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: bad M=%lld or ldy=%lld < N=%lld",
-                    (long long)M, (long long)ldy, (long long)w->view.N);
-    if (M == 0) return S2X_OK;
-    if (M > INT32_MAX / 2) return fail(S2X_ERR_UNSUPPORTED, "mul_mat: M too large");
-    if (!qs || !ds || !y) return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: null pointer");
-    if (!aligned(qs, 16) || !aligned(ds, 4) || !aligned(y, 4))
-        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: qs must be 16-byte aligned");
-    EpiParams p;
-    int st = check_epi(epi, p);
+    int st = check_q81_input(w, qs, ds, M, "mul_mat_q8_0_q8_1");
     if (st != S2X_OK) return st;
-    hipError_t e = launch_mmq(w->view, (const int8_t *)qs, (const uint32_t *)ds, M, y, ldy, p,
-                              (hipStream_t)stream);
-    return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
+    EpiParams p;
+    st = check_epi(epi, w->view.N, p);
+    if (st != S2X_OK) return st;
+    if (p.kind != EPI_GELU_Q81 && (!y || ldy < w->view.N || !aligned(y, 4)))
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: y null/misaligned or ldy=%lld < N=%lld",
+                    (long long)ldy, (long long)w->view.N);
+    if (M == 0) return S2X_OK;
+    hipError_t e = launch_gemm(w->view, (const int8_t *)qs, (const uint32_t *)ds,
+                               w->view.K_pad / QK_, M, y, ldy, p, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
 }
 
 size_t s2x_mul_mat_workspace_size(int64_t K_pad, int64_t N, int64_t M) {
@@ -190,6 +210,7 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
                     "mul_mat_q8_0_f32: bad shape K=%lld K_pad=%lld N=%lld M=%lld ldx=%lld",
                     (long long)K, (long long)K_pad, (long long)N, (long long)M, (long long)ldx);
     if (M == 0) return S2X_OK;
+    if (M > (1 << 30)) return fail(S2X_ERR_UNSUPPORTED, "mul_mat_q8_0_f32: M too large");
     if (!w_raw || !x || !y || !workspace)
         return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_f32: null pointer");
     const MulMatWs L = mul_mat_ws_layout(K_pad, N, M);
@@ -205,26 +226,27 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
     if (e != hipSuccess) return hip_fail(e, "repack launch");
     Q81Out o;
     o.qs = (int8_t *)(ws + L.xq_off);
-    o.dT = (uint16_t *)(ws + L.dT_off);
-    o.ldT = mmq16_ld_dx(M);
+    o.ds = (uint32_t *)(ws + L.ds_off);
+    o.ld_ds = K_pad / QK_;
     e = launch_quantize_q8_1(x, K, M, ldx, K_pad, o, s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
-    e = launch_mmq_i8(wv, o.qs, o.dT, o.ldT, M, y, N, p, s);
-    return e == hipSuccess ? S2X_OK : hip_fail(e, "mmq launch");
+    e = launch_gemm(wv, o.qs, o.ds, o.ld_ds, M, y, N, p, s);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
 }
 
 int s2x_block_dots(const s2x_weight *w, const void *qs, int64_t M, int64_t kb, int32_t *out,
                    void *stream) {
     if (!w || !qs || !out) return fail(S2X_ERR_INVALID_ARG, "block_dots: null pointer");
-    if (M <= 0 || kb < 0 || kb >= w->view.K_pad / QK_)
+    if (M <= 0 || M > (1 << 30) || kb < 0 || kb >= w->view.K_pad / QK_)
         return fail(S2X_ERR_INVALID_ARG, "block_dots: bad M=%lld or kb=%lld", (long long)M,
                     (long long)kb);
     if (!aligned(qs, 16)) return fail(S2X_ERR_INVALID_ARG, "block_dots: qs must be 16-byte aligned");
-    // the integer stage reads no scales (the EPI_DUMP_I kernel skips them)
+    // the integer stage reads no activation scales (the DMA of a null plane
+    // returns zeros)
     EpiParams p{EPI_DUMP_I, nullptr, nullptr, 0, 0, kb};
-    hipError_t e = launch_mmq(w->view, (const int8_t *)qs, nullptr, M, reinterpret_cast<float *>(out),
-                              w->view.N, p, (hipStream_t)stream);
+    hipError_t e = launch_gemm(w->view, (const int8_t *)qs, nullptr, 0, M,
+                               reinterpret_cast<float *>(out), w->view.N, p, (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "block dots launch");
 }
 
@@ -318,6 +340,43 @@ int s2x_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
     hipError_t e = launch_attn_prep(qkv, ld_qkv, qkv_bias, seg_start_dev, seg_len_dev, L, ws,
                                     (hipStream_t)stream);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "attn_prep launch");
+}
+
+int s2x_mul_mat_qkv_attn_prep(const s2x_weight *w, const void *qs, const void *ds, int64_t M,
+                              const float *qkv_bias, const int32_t *seg_start_dev,
+                              const int32_t *seg_len_dev, int64_t n_seg, int64_t max_len,
+                              int64_t n_head, int64_t d_head, void *ws, size_t ws_bytes,
+                              void *stream) {
+    int st = check_attn_shape(n_seg, max_len, n_head, d_head, "mul_mat_qkv_attn_prep");
+    if (st != S2X_OK) return st;
+    st = check_q81_input(w, qs, ds, M, "mul_mat_qkv_attn_prep");
+    if (st != S2X_OK) return st;
+    if (w->view.N != 3 * n_head * d_head)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_qkv_attn_prep: W has N=%lld, not 3*%lld*%lld",
+                    (long long)w->view.N, (long long)n_head, (long long)d_head);
+    if (n_seg > 32767 || max_len > 65535 || max_len > MAX_SEG_LEN)
+        return fail(S2X_ERR_UNSUPPORTED, "mul_mat_qkv_attn_prep: n_seg or max_len too large");
+    if (M > n_seg * max_len)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_qkv_attn_prep: M > n_seg * max_len");
+    if (n_seg == 0 || M == 0) return S2X_OK;
+    if (!qkv_bias || !seg_start_dev || !seg_len_dev || !ws)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_qkv_attn_prep: null pointer");
+    const AttnLayout L = attn_layout(n_seg, max_len, n_head, d_head);
+    if (ws_bytes < L.bytes)
+        return fail(S2X_ERR_WORKSPACE, "mul_mat_qkv_attn_prep: workspace %zu < %zu bytes", ws_bytes,
+                    L.bytes);
+    if (!aligned(ws, 256)) return fail(S2X_ERR_INVALID_ARG, "mul_mat_qkv_attn_prep: ws misaligned");
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *base = (uint8_t *)ws;
+    // padding slots zero, and rows no segment covers map to (0, 0)
+    hipError_t e = launch_fill_zero(ws, L.bytes, s);
+    if (e != hipSuccess) return hip_fail(e, "fill launch");
+    int32_t *rowmap = reinterpret_cast<int32_t *>(base + L.rowmap_off);
+    e = launch_rowmap(seg_start_dev, seg_len_dev, n_seg, max_len, rowmap, M, s);
+    if (e != hipSuccess) return hip_fail(e, "rowmap launch");
+    e = launch_gemm(w->view, (const int8_t *)qs, (const uint32_t *)ds, w->view.K_pad / QK_, M,
+                    nullptr, 0, epi_qkv(L, ws, qkv_bias, rowmap), s);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
 }
 
 int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,

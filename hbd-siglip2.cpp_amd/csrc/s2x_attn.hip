@@ -44,22 +44,13 @@ AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d
     L.q_off = 0;
     L.k_off = round_up((int64_t)qk, 256);
     L.vt_off = L.k_off + round_up((int64_t)qk, 256);
-    L.bytes = L.vt_off + round_up((int64_t)vt, 256);
+    L.planes_bytes = L.vt_off + round_up((int64_t)vt, 256);
+    // packed row -> (segment, position) table of the fused QKV entry point
+    L.rowmap_off = L.planes_bytes;
+    L.bytes = L.rowmap_off + round_up(n_seg * max_len * 4, 256);
     return L;
 }
 
-// Segments [s0, s1) of layout L as a layout of their own: the same plane
-// geometry with the Q / K / V^T bases moved to segment s0.
-AttnLayout attn_sublayout(const AttnLayout &L, int64_t s0, int64_t s1) {
-    AttnLayout S = L;
-    const size_t qk_seg = (size_t)(L.n_head * L.len_pad * L.d_pad) * 2;
-    const size_t vt_seg = (size_t)(L.n_head * L.dv_pad * L.len_pad) * 2;
-    S.n_seg = s1 - s0;
-    S.q_off = L.q_off + (size_t)s0 * qk_seg;
-    S.k_off = L.k_off + (size_t)s0 * qk_seg;
-    S.vt_off = L.vt_off + (size_t)s0 * vt_seg;
-    return S;
-}
 
 // ---------------------------------------------------------------------------
 // staging: one workgroup per (64-position tile, head, segment)
@@ -109,20 +100,23 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     }
 }
 
+// rowmap[seg_start[s] + pos] = s << 16 | pos for pos < min(seg_len[s],
+// max_len); entries outside [0, n_rows) are skipped
 __global__ __launch_bounds__(256) void k_rowmap(const int32_t *__restrict__ seg_start,
                                                 const int32_t *__restrict__ seg_len,
-                                                int32_t *__restrict__ rowmap) {
+                                                int32_t *__restrict__ rowmap, int64_t n_rows) {
     const int sg = blockIdx.y;
     const int pos = blockIdx.x * 256 + threadIdx.x;
-    if (pos < seg_len[sg]) rowmap[seg_start[sg] + pos] = (sg << 16) | pos;
+    const int64_t r = (int64_t)seg_start[sg] + pos;
+    if (pos < seg_len[sg] && r >= 0 && r < n_rows) rowmap[r] = (sg << 16) | pos;
 }
 
 hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
-                         int64_t max_len, int32_t *rowmap, hipStream_t stream) {
+                         int64_t max_len, int32_t *rowmap, int64_t n_rows, hipStream_t stream) {
     if (n_seg == 0 || max_len == 0) return hipSuccess;
     if (n_seg > 32767 || max_len > 65535) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_rowmap, dim3((unsigned)((max_len + 255) / 256), (unsigned)n_seg),
-                       dim3(256), 0, stream, seg_start, seg_len, rowmap);
+                       dim3(256), 0, stream, seg_start, seg_len, rowmap, n_rows);
     return hipGetLastError();
 }
 

@@ -193,6 +193,15 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return x / (1.0f + exp_cw(t));
 }
 
+// a / b for 0 <= a < 2^20 and b >= 1, exact: the float estimate a * (1/b)
+// is within a/b * 2^-23 <= 1/8 of a/b, so one correction either way suffices
+__device__ __forceinline__ int small_div(int a, int b, float inv_b) {
+    int q = (int)((float)a * inv_b);
+    const int r = a - q * b;
+    q += (r >= b) - (r < 0);
+    return q;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
 // XCD b % 8), each with its own L2.  xcd_linear(b, G) renumbers the G
 // workgroups of a launch so that each XCD takes one contiguous range of the

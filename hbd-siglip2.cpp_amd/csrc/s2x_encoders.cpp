@@ -183,47 +183,23 @@ struct Tower {
     float eps = 1e-6f;
     std::vector<DevLayer> layers;
     hipStream_t own = nullptr, stream = nullptr;
-    DevBuf x, qs, ds, qkv, att, u, attn_ws, seg, kvalid, rowmap;
-    DevBuf qs2, ds2;  // the fc1 epilogue's Q8_1 output (fc2 input)
+    // x: residual stream f32 [M][H]; qs / ds: Q8_1 of the current GEMM input
+    // ([M][kmax] int8, [M][kmax/32] ds words); qs2 / ds2: the fc1 epilogue's
+    // Q8_1 output (fc2 input, K = F_pad)
+    DevBuf x, qs, ds, qs2, ds2, qkv, att, attn_ws, seg, rowmap;
     GemmTiming timing;
-    // attention in fp64 (k_attn_f64) instead of the f16-MFMA flash kernel
+    // attention in fp64 (k_attn_f64, from an f32 QKV GEMM output) instead of
+    // the f16-MFMA flash kernel fed by the QKV GEMM's attention-layout epilogue
     bool attn_f64 = false;
-    // GEMM variant: int8 quants on v_mfma_i32_32x32x32_i8 (true, default) or
-    // f16-coded quants on v_mfma_f32_32x32x16_f16; same bits.  The quantized
-    // activations in `qs` / `qs2` are int8 or f16 accordingly; `ds` / `ds2`
-    // hold the transposed fp16 scales [KB][mmq16_ld_dx(M)].
-    bool gemm_i8 = true;
-    int64_t qbytes() const { return gemm_i8 ? 1 : 2; }
-    // The encoder blocks of a batch run as up to MAX_LANES independent row
-    // ranges (whole segments), each on a stream of its own: while one
-    // lane's GEMM drains its last, partly filled round of tiles, the other
-    // lanes' kernels occupy the idle CUs.  Lanes fork from `stream` and
-    // join back into it, so callers see one ordered stream.
-    static constexpr int MAX_LANES = 4;
-    int n_lanes = 1;
-    hipStream_t lane_s[MAX_LANES] = {};
-    hipEvent_t ev_fork = nullptr, ev_join[MAX_LANES] = {}, ev_phase[MAX_LANES] = {};
 
     ~Tower() {
         for (auto &L : layers) L.release();
-        for (int i = 0; i < MAX_LANES; ++i) {
-            if (lane_s[i]) (void)hipStreamDestroy(lane_s[i]);
-            if (ev_join[i]) (void)hipEventDestroy(ev_join[i]);
-            if (ev_phase[i]) (void)hipEventDestroy(ev_phase[i]);
-        }
-        if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (own) (void)hipStreamDestroy(own);
     }
 
     int init_stream() {
         S2X_HIP_TRY(hipStreamCreateWithFlags(&own, hipStreamNonBlocking));
         stream = own;
-        S2X_HIP_TRY(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
-        for (int i = 0; i < MAX_LANES; ++i) {
-            S2X_HIP_TRY(hipStreamCreateWithFlags(&lane_s[i], hipStreamNonBlocking));
-            S2X_HIP_TRY(hipEventCreateWithFlags(&ev_join[i], hipEventDisableTiming));
-            S2X_HIP_TRY(hipEventCreateWithFlags(&ev_phase[i], hipEventDisableTiming));
-        }
         return S2X_OK;
     }
 
@@ -249,228 +225,133 @@ struct Tower {
         return S2X_OK;
     }
 
-    // GEMM with optional event timing; k_logical excludes the K padding.
+    // GEMM over the Q8_1 rows in qs / ds (or qs2 / ds2), with optional event
+    // timing; k_logical excludes the K padding.
     int gemm(const s2x_weight *w, int64_t M, float *y, int64_t ldy, const EpiParams &e,
              int64_t k_logical, bool from_qs2 = false) {
         const DevBuf &xq = from_qs2 ? qs2 : qs, &xd = from_qs2 ? ds2 : ds;
-        return gemm_rows(w, xq.as<uint8_t>(), xd.as<uint16_t>(), mmq16_ld_dx(M), M, y, ldy, e,
-                         k_logical, stream);
-    }
-    // GEMM over rows whose quants start at xq and transposed scales at xdT
-    // (row stride ld_dx of the whole batch), on stream st.
-    int gemm_rows(const s2x_weight *w, const uint8_t *xq, const uint16_t *xdT, int64_t ld_dx,
-                  int64_t M, float *y, int64_t ldy, const EpiParams &e, int64_t k_logical,
-                  hipStream_t st) {
-        return timed(w, M, k_logical, st, [&] {
-            return gemm_i8 ? launch_mmq_i8(w->view, reinterpret_cast<const int8_t *>(xq), xdT,
-                                           ld_dx, M, y, ldy, e, st)
-                           : launch_mmq_f16(w->view, reinterpret_cast<const _Float16 *>(xq), xdT,
-                                            ld_dx, M, y, ldy, e, st);
-        });
-    }
-    // Q8_1 planes of rows starting at quant bytes q and scale column d.
-    Q81Out qplanes(uint8_t *q, uint16_t *d, int64_t ld) const {
-        Q81Out o;
-        if (gemm_i8)
-            o.qs = reinterpret_cast<int8_t *>(q);
-        else
-            o.qh = reinterpret_cast<_Float16 *>(q);
-        o.dT = d;
-        o.ldT = ld;
-        return o;
-    }
-    template <class Launch>
-    int timed(const s2x_weight *w, int64_t M, int64_t k_logical, hipStream_t st, Launch &&launch) {
         hipEvent_t a = nullptr, b = nullptr;
         if (timing.on) {
             a = timing.get();
             b = timing.get();
-            S2X_HIP_TRY(hipEventRecord(a, st));
+            S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        const hipError_t err = launch();
-        if (err != hipSuccess) return hip_fail(err, "mmq launch");
+        const hipError_t err = launch_gemm(w->view, xq.as<int8_t>(), xd.as<uint32_t>(),
+                                           w->view.K_pad / QK_, M, y, ldy, e, stream);
+        if (err != hipSuccess) return hip_fail(err, "gemm launch");
         if (timing.on) {
-            S2X_HIP_TRY(hipEventRecord(b, st));
+            S2X_HIP_TRY(hipEventRecord(b, stream));
             timing.pending.push_back({a, b, 2.0 * (double)M * (double)w->view.N * (double)k_logical});
         }
         return S2X_OK;
     }
 
-    // Quantized-activation planes for a GEMM over M rows.
-    Q81Out qout(int64_t M) { return qplanes(qs.as<uint8_t>(), ds.as<uint16_t>(), mmq16_ld_dx(M)); }
-    static size_t ds_bytes(int64_t M, int64_t kmax) {
-        return sizeof(uint16_t) * (size_t)(mmq16_ld_dx(M) * (kmax / QK_));
+    // Q8_1 planes of the GEMM input buffers for rows of K_pad values
+    Q81Out qout(int64_t K_pad) {
+        Q81Out o;
+        o.qs = qs.as<int8_t>();
+        o.ds = ds.as<uint32_t>();
+        o.ld_ds = K_pad / QK_;
+        return o;
     }
 
     int quantize(const float *src, int64_t K, int64_t M, int64_t ldx, int64_t K_pad) {
-        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, qout(M), stream);
+        hipError_t e = launch_quantize_q8_1(src, K, M, ldx, K_pad, qout(K_pad), stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "quantize launch");
     }
 
     int layernorm_q(const float *src, int64_t M, const float *w, const float *b, float *y) {
-        const Q81Out o = qout(M);
+        const Q81Out o = qout(H);
         hipError_t e = launch_layernorm(src, H, M, H, w, b, eps, &o, y, H, stream);
         return e == hipSuccess ? S2X_OK : hip_fail(e, "layernorm launch");
     }
 
-    int reserve(int64_t M, int64_t n_seg, int64_t max_len) {
-        const int64_t kmax = F_pad > H ? F_pad : H;
+    // Buffers for M packed rows; kmax: the widest GEMM input (patch_dim for
+    // the vision patch embedding).
+    int reserve(int64_t M, int64_t n_seg, int64_t max_len, int64_t kmax_in = 0) {
+        const int64_t kmax = std::max<int64_t>(H, kmax_in);
         S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
-        S2X_TRY(ensure(qs, 2 * (size_t)(M * kmax), stream));  // int8 or f16 quants
-        S2X_TRY(ensure(ds, ds_bytes(M, kmax), stream));
-        S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
+        S2X_TRY(ensure(qs, (size_t)(M * kmax), stream));
+        S2X_TRY(ensure(ds, sizeof(uint32_t) * (size_t)(M * (kmax / QK_)), stream));
+        S2X_TRY(ensure(qs2, (size_t)(M * F_pad), stream));
+        S2X_TRY(ensure(ds2, sizeof(uint32_t) * (size_t)(M * (F_pad / QK_)), stream));
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
-        if (!attn_f64) {
-            S2X_TRY(ensure(qs2, 2 * (size_t)(M * F_pad), stream));
-            S2X_TRY(ensure(ds2, ds_bytes(M, F_pad), stream));
-        } else {
-            S2X_TRY(ensure(u, sizeof(float) * (size_t)(M * F), stream));
-        }
-        S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
+        if (attn_f64)
+            S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
+        else
+            S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
         S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
         S2X_TRY(ensure(rowmap, sizeof(int32_t) * (size_t)M, stream));
         return S2X_OK;
     }
 
-    // The attention workspace's padding slots (d_head..d_pad of Q / K rows)
-    // must hold zeros; the QKV GEMM epilogue writes real slots only, so the
-    // workspace is cleared whenever its layout or address changes.
+    // The attention workspace's padding slots (d_head..d_pad of Q / K rows,
+    // positions past a segment's length) must hold zeros; the QKV GEMM
+    // epilogue writes real slots only, so the workspace is cleared whenever
+    // its layout or address changes.
     void *attn_zeroed_at = nullptr;
     int64_t attn_zeroed_key[3] = {-1, -1, -1};
     int attn_ws_ready(const AttnLayout &AL) {
         const int64_t key[3] = {AL.n_seg, AL.len_pad, AL.n_head};
         if (attn_zeroed_at == attn_ws.p && std::equal(key, key + 3, attn_zeroed_key)) return S2X_OK;
-        S2X_HIP_TRY(hipMemsetAsync(attn_ws.p, 0, AL.bytes, stream));
+        hipError_t e = launch_fill_zero(attn_ws.p, AL.planes_bytes, stream);
+        if (e != hipSuccess) return hip_fail(e, "fill launch");
         attn_zeroed_at = attn_ws.p;
         std::copy(key, key + 3, attn_zeroed_key);
         return S2X_OK;
     }
 
-    // Upload the segment table (starts then lengths) to `seg`; skipped when
-    // it equals the table already there (steady-state batches stay async).
+    // Upload the segment table (starts then lengths) to `seg` and build the
+    // row map; skipped when the table is the one already there (steady-state
+    // batches stay asynchronous).
     std::vector<int32_t> seg_host;
-    void *seg_dev_at = nullptr;
-    int set_segments(const std::vector<int32_t> &start, const std::vector<int32_t> &len) {
+    void *seg_dev_at = nullptr, *rowmap_at = nullptr;
+    int64_t rowmap_rows = -1;
+    int set_segments(const std::vector<int32_t> &start, const std::vector<int32_t> &len, int64_t M) {
         const size_t n = start.size();
         std::vector<int32_t> tab(2 * n);
         std::memcpy(tab.data(), start.data(), n * 4);
         std::memcpy(tab.data() + n, len.data(), n * 4);
-        if (tab == seg_host && seg_dev_at == seg.p && rowmap_at == rowmap.p) return S2X_OK;
+        if (tab == seg_host && seg_dev_at == seg.p && rowmap_at == rowmap.p && rowmap_rows == M)
+            return S2X_OK;
         S2X_HIP_TRY(hipMemcpyAsync(seg.p, tab.data(), 8 * n, hipMemcpyHostToDevice, stream));
         S2X_HIP_TRY(hipStreamSynchronize(stream));  // `tab` is pageable host memory
         const int64_t max_len = n ? *std::max_element(len.begin(), len.end()) : 0;
         hipError_t e = launch_rowmap(seg_start(), seg_len((int64_t)n), (int64_t)n, max_len,
-                                     rowmap.as<int32_t>(), stream);
+                                     rowmap.as<int32_t>(), M, stream);
         if (e != hipSuccess) return hip_fail(e, "rowmap launch");
         seg_host = std::move(tab);
         seg_dev_at = seg.p;
         rowmap_at = rowmap.p;
+        rowmap_rows = M;
         return S2X_OK;
     }
-    void *rowmap_at = nullptr;
     const int32_t *seg_start() const { return seg.as<int32_t>(); }
     const int32_t *seg_len(int64_t n_seg) const { return seg.as<int32_t>() + n_seg; }
 
-    // Lane boundaries: segment indices b[0] = 0 < b[1] < ... < b[n] = n_seg
-    // splitting the rows as evenly as whole segments allow.  A lane's first
-    // row must be a multiple of 8 (16-byte aligned transposed scales).
-    std::vector<int64_t> lane_bounds(int64_t M, int64_t n_seg) const {
-        std::vector<int64_t> b{0};
-        const int64_t n = std::min<int64_t>(n_lanes, MAX_LANES);
-        const int32_t *start = seg_host.data();
-        for (int64_t i = 1; i < n && (int64_t)seg_host.size() == 2 * n_seg; ++i) {
-            const int64_t target = M * i / n;
-            int64_t best = -1;
-            for (int64_t s = b.back() + 1; s < n_seg; ++s)
-                if (start[s] % 8 == 0 &&
-                    (best < 0 || std::llabs(start[s] - target) < std::llabs(start[best] - target)))
-                    best = s;
-            if (best > 0) b.push_back(best);
-        }
-        b.push_back(n_seg);
-        return b;
-    }
-
-    // Encoder blocks, f16 GEMM + flash attention path, for rows [r0, r1)
-    // = segments [s0, s1) of an M-row batch, on stream st.  The QKV GEMM
-    // writes the attention operands itself (EPI_QKV); every buffer is
-    // addressed by absolute row / segment, so lanes touch disjoint parts.
-    int run_rows(hipStream_t st, int64_t r0, int64_t r1, int64_t s0, int64_t s1, int64_t M,
-                 const AttnLayout &AL, float kq_scale, const uint8_t *key_valid,
-                 hipEvent_t phase = nullptr) {
-        const int64_t Mp = r1 - r0, ld = mmq16_ld_dx(M);
-        if (Mp == 0) return S2X_OK;
-        float *xp = x.as<float>() + r0 * H;
-        uint8_t *q1 = qs.as<uint8_t>() + r0 * H * qbytes(), *q2 = qs2.as<uint8_t>() + r0 * F_pad * qbytes();
-        uint16_t *d1 = ds.as<uint16_t>() + r0, *d2 = ds2.as<uint16_t>() + r0;
-        const Q81Out qa = qplanes(q1, d1, ld);
-        const AttnLayout ALs = attn_sublayout(AL, s0, s1);
-        const int32_t *rm = rowmap.as<int32_t>() + r0;
-        hipError_t e;
-        for (auto &L : layers) {
-            e = launch_layernorm(xp, H, Mp, H, L.ln1_w, L.ln1_b, eps, &qa, nullptr, H, st);
-            if (e != hipSuccess) return hip_fail(e, "layernorm launch");
-            S2X_TRY(gemm_rows(L.qkv, q1, d1, ld, Mp, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rm), H, st));
-            e = launch_attn(attn_ws.p, seg_start() + s0, seg.as<int32_t>() + AL.n_seg + s0,
-                            key_valid, ALs, kq_scale, att.as<float>(), H, st);
-            if (e != hipSuccess) return hip_fail(e, "attn launch");
-            if (phase && &L == &layers[0]) S2X_HIP_TRY(hipEventRecord(phase, st));
-            e = launch_quantize_q8_1(att.as<float>() + r0 * H, H, Mp, H, H, qa, st);
-            if (e != hipSuccess) return hip_fail(e, "quantize launch");
-            S2X_TRY(gemm_rows(L.o, q1, d1, ld, Mp, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H, st));
-            e = launch_layernorm(xp, H, Mp, H, L.ln2_w, L.ln2_b, eps, &qa, nullptr, H, st);
-            if (e != hipSuccess) return hip_fail(e, "layernorm launch");
-            EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
-            if (gemm_i8)
-                up.q_out8 = reinterpret_cast<int8_t *>(q2);
-            else
-                up.q_out = reinterpret_cast<_Float16 *>(q2);
-            up.q_dT = d2;
-            up.q_kpad = F_pad;
-            up.q_ld = ld;
-            S2X_TRY(gemm_rows(L.up, q1, d1, ld, Mp, nullptr, 0, up, H, st));
-            S2X_TRY(gemm_rows(L.down, q2, d2, ld, Mp, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F, st));
-        }
-        return S2X_OK;
-    }
-
-    // The 27 encoder blocks in place on x (M packed rows).
+    // The encoder blocks in place on x (M packed rows, n_seg segments):
+    //   LN1+Q8_1 -> QKV GEMM -> attention -> Q8_1 -> O GEMM (+bias +residual,
+    //   in place) -> LN2+Q8_1 -> FC1 GEMM (+bias, GELU, Q8_1 of the result
+    //   with K padded to F_pad) -> FC2 GEMM (+bias +residual, in place)
+    // The QKV GEMM writes the flash kernel's operands itself (EPI_QKV); with
+    // fp64 attention it writes f32 rows for k_attn_f64 instead.
     int run_layers(int64_t M, int64_t n_seg, int64_t max_len, const uint8_t *key_valid) {
         const AttnLayout AL = attn_layout(n_seg, max_len, n_head, d_head);
         const float kq_scale = 1.0f / std::sqrt((float)d_head);
         float *xp = x.as<float>();
-        if (!attn_f64) {
-            S2X_TRY(attn_ws_ready(AL));
-            const std::vector<int64_t> b = lane_bounds(M, n_seg);
-            const int nl = (int)b.size() - 1;
-            if (nl == 1) return run_rows(stream, 0, M, 0, n_seg, M, AL, kq_scale, key_valid);
-            const int32_t *start = seg_host.data();
-            S2X_HIP_TRY(hipEventRecord(ev_fork, stream));
-            for (int i = 0; i < nl; ++i) {
-                const int64_t r0 = start[b[i]], r1 = b[i + 1] < n_seg ? start[b[i + 1]] : M;
-                // each lane starts when the previous one has reached its first
-                // attention, so the lanes' GEMM tails fall at different times
-                S2X_HIP_TRY(hipStreamWaitEvent(lane_s[i], i ? ev_phase[i - 1] : ev_fork, 0));
-                S2X_TRY(run_rows(lane_s[i], r0, r1, b[i], b[i + 1], M, AL, kq_scale, key_valid,
-                                 i + 1 < nl ? ev_phase[i] : nullptr));
-                S2X_HIP_TRY(hipEventRecord(ev_join[i], lane_s[i]));
-            }
-            for (int i = 0; i < nl; ++i) S2X_HIP_TRY(hipStreamWaitEvent(stream, ev_join[i], 0));
-            return S2X_OK;
-        }
+        if (!attn_f64) S2X_TRY(attn_ws_ready(AL));
+        hipError_t e;
         for (auto &L : layers) {
             S2X_TRY(layernorm_q(xp, M, L.ln1_w, L.ln1_b, nullptr));
-            hipError_t e;
-            S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H, EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
             if (attn_f64) {
+                S2X_TRY(gemm(L.qkv, M, qkv.as<float>(), 3 * H,
+                             EpiParams{EPI_NONE, nullptr, nullptr, 0, 0, 0}, H));
                 e = launch_attn_f64(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
                                     key_valid, n_seg, max_len, n_head, d_head, kq_scale,
                                     att.as<float>(), H, stream);
                 if (e != hipSuccess) return hip_fail(e, "attn_f64 launch");
             } else {
-                e = launch_attn_prep(qkv.as<float>(), 3 * H, L.qkv_b, seg_start(), seg_len(n_seg),
-                                     AL, attn_ws.p, stream);
-                if (e != hipSuccess) return hip_fail(e, "attn_prep launch");
+                S2X_TRY(gemm(L.qkv, M, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rowmap.as<int32_t>()), H));
                 e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
                                 att.as<float>(), H, stream);
                 if (e != hipSuccess) return hip_fail(e, "attn launch");
@@ -478,9 +359,13 @@ struct Tower {
             S2X_TRY(quantize(att.as<float>(), H, M, H, H));
             S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
             S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
-            S2X_TRY(gemm(L.up, M, u.as<float>(), F, EpiParams{EPI_BIAS_GELU, L.up_b, nullptr, 0, 0, 0}, H));
-            S2X_TRY(quantize(u.as<float>(), F, M, F, F_pad));
-            S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F));
+            EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
+            up.q_out8 = qs2.as<int8_t>();
+            up.q_ds = ds2.as<uint32_t>();
+            up.q_kpad = F_pad;
+            up.q_ldds = F_pad / QK_;
+            S2X_TRY(gemm(L.up, M, nullptr, 0, up, H));
+            S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F, true));
         }
         return S2X_OK;
     }
@@ -515,7 +400,7 @@ struct s2x_vision {
     float *probe_q = nullptr, *hkv_b = nullptr, *ho_b = nullptr, *hln_w = nullptr,
           *hln_b = nullptr, *hup_b = nullptr, *hdown_b = nullptr;
     std::vector<std::pair<std::pair<int, int>, float *>> pos_cache;  // LRU of resized grids
-    DevBuf pix, pos_packed, kv, hq, ha, hu, hout, hid, nf_ws;
+    DevBuf pix, pos_packed, kv, hq, ha, hout, hid, nf_ws;
 
     ~s2x_vision() {
         for (s2x_weight *w : {patch, hkv, ho, hup, hdown}) s2x_weight_destroy(w);
@@ -576,7 +461,6 @@ struct s2x_vision {
         S2X_TRY(ensure(kv, sizeof(float) * (size_t)(M * 2 * H), t.stream));
         S2X_TRY(ensure(hq, sizeof(float) * (size_t)(n_img * H), t.stream));
         S2X_TRY(ensure(ha, sizeof(float) * (size_t)(n_img * H), t.stream));
-        S2X_TRY(ensure(hu, sizeof(float) * (size_t)(n_img * t.F), t.stream));
         S2X_TRY(t.gemm(hkv, M, kv.as<float>(), 2 * H, EpiParams{EPI_BIAS, hkv_b, nullptr, 0, 0, 0}, H));
         hipError_t e = launch_attn_1q(probe_q, kv.as<float>(), kv.as<float>() + H, 2 * H,
                                       t.seg_start(), t.seg_len(n_img), n_img, t.n_head, t.d_head,
@@ -585,9 +469,13 @@ struct s2x_vision {
         S2X_TRY(t.quantize(hq.as<float>(), H, n_img, H, H));
         S2X_TRY(t.gemm(ho, n_img, ha.as<float>(), H, EpiParams{EPI_BIAS, ho_b, nullptr, 0, 0, 0}, H));
         S2X_TRY(t.layernorm_q(ha.as<float>(), n_img, hln_w, hln_b, nullptr));
-        S2X_TRY(t.gemm(hup, n_img, hu.as<float>(), t.F, EpiParams{EPI_BIAS_GELU, hup_b, nullptr, 0, 0, 0}, H));
-        S2X_TRY(t.quantize(hu.as<float>(), t.F, n_img, t.F, t.F_pad));
-        S2X_TRY(t.gemm(hdown, n_img, out_dev, H, EpiParams{EPI_BIAS_RESID, hdown_b, ha.as<float>(), H, 0, 0}, t.F));
+        EpiParams up{EPI_GELU_Q81, hup_b, nullptr, 0, 0, 0};
+        up.q_out8 = t.qs2.as<int8_t>();
+        up.q_ds = t.ds2.as<uint32_t>();
+        up.q_kpad = t.F_pad;
+        up.q_ldds = t.F_pad / QK_;
+        S2X_TRY(t.gemm(hup, n_img, nullptr, 0, up, H));
+        S2X_TRY(t.gemm(hdown, n_img, out_dev, H, EpiParams{EPI_BIAS_RESID, hdown_b, ha.as<float>(), H, 0, 0}, t.F, true));
         return S2X_OK;
     }
 };
@@ -665,8 +553,8 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
         }
         if (hipMalloc(reinterpret_cast<void **>(&v->probe_q), sizeof(float) * (size_t)H) != hipSuccess)
             st = fail(S2X_ERR_OOM, "probe_q alloc");
-        if (!st) st = ensure(t.qs, 2 * (size_t)H, s);
-        if (!st) st = ensure(t.ds, Tower::ds_bytes(1, H), s);
+        if (!st) st = ensure(t.qs, (size_t)H, s);
+        if (!st) st = ensure(t.ds, sizeof(uint32_t) * (size_t)(H / QK_), s);
         if (!st) st = t.quantize(probe, H, 1, H, H);
         if (!st) st = t.gemm(hq, 1, v->probe_q, H, EpiParams{EPI_BIAS, hq_b, nullptr, 0, 0, 0}, H);
         if (!st && hipStreamSynchronize(s) != hipSuccess) st = fail(S2X_ERR_HIP, "probe sync");
@@ -698,23 +586,6 @@ int s2x_vision_set_attention_fp64(s2x_vision *v, int enable) {
     return S2X_OK;
 }
 
-int s2x_vision_set_gemm_variant(s2x_vision *v, int variant) {
-    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
-    if (variant != S2X_GEMM_F16_MFMA && variant != S2X_GEMM_I8_MFMA)
-        return fail(S2X_ERR_INVALID_ARG, "gemm variant %d unknown", variant);
-    S2X_HIP_TRY(hipStreamSynchronize(v->t.stream));  // the activation buffer changes format
-    v->t.gemm_i8 = variant == S2X_GEMM_I8_MFMA;
-    return S2X_OK;
-}
-
-int s2x_vision_set_lanes(s2x_vision *v, int n) {
-    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
-    if (n < 1 || n > Tower::MAX_LANES)
-        return fail(S2X_ERR_INVALID_ARG, "lanes %d outside 1..%d", n, Tower::MAX_LANES);
-    v->t.n_lanes = n;
-    return S2X_OK;
-}
-
 int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t n_img, int32_t n_h,
                                 int32_t n_w, int32_t pooling, float *out_dev) {
     if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
@@ -725,10 +596,10 @@ int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t 
     if (n_pos > MAX_SEG_LEN) return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
     Tower &t = v->t;
     const int64_t M = n_pos * n_img;
-    S2X_TRY(t.reserve(M, n_img, n_pos));
+    S2X_TRY(t.reserve(M, n_img, n_pos, v->patch_dim));
     std::vector<int32_t> st((size_t)n_img), ln((size_t)n_img, (int32_t)n_pos);
     for (int i = 0; i < n_img; ++i) st[(size_t)i] = (int32_t)(i * n_pos);
-    S2X_TRY(t.set_segments(st, ln));
+    S2X_TRY(t.set_segments(st, ln, M));
     const float *pos = nullptr;
     S2X_TRY(v->pos_for(n_h, n_w, &pos));
     S2X_TRY(t.quantize(pixels_dev, v->patch_dim, M, v->patch_dim, v->patch_dim));
@@ -774,8 +645,8 @@ int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
         M += (int64_t)h * w;
         if (h * w > max_len) max_len = h * w;
     }
-    S2X_TRY(t.reserve(M, n_img, max_len));
-    S2X_TRY(t.set_segments(st, ln));
+    S2X_TRY(t.reserve(M, n_img, max_len, v->patch_dim));
+    S2X_TRY(t.set_segments(st, ln, M));
     S2X_TRY(ensure(v->pix, sizeof(float) * (size_t)(M * v->patch_dim), t.stream));
     S2X_TRY(ensure(v->pos_packed, sizeof(float) * (size_t)(M * t.H), t.stream));
     hipError_t e = launch_pack_rows(pixels_dev, v->patch_dim, max_patches, t.seg_start(),
@@ -829,8 +700,8 @@ int s2x_vision_encode_rgb_batch_dev(s2x_vision *v, const uint8_t *const *rgb_dev
         ws_bytes = std::max(ws_bytes, nf_workspace_bytes(h, w, p, max_num_patches));
     }
     if (max_len > MAX_SEG_LEN) return fail(S2X_ERR_UNSUPPORTED, "vision: more than 4096 patches");
-    S2X_TRY(t.reserve(M, n_img, max_len));
-    S2X_TRY(t.set_segments(st, ln));
+    S2X_TRY(t.reserve(M, n_img, max_len, v->patch_dim));
+    S2X_TRY(t.set_segments(st, ln, M));
     S2X_TRY(ensure(v->pix, sizeof(float) * (size_t)(M * v->patch_dim), t.stream));
     S2X_TRY(ensure(v->pos_packed, sizeof(float) * (size_t)(M * t.H), t.stream));
     S2X_TRY(ensure(v->nf_ws, ws_bytes, t.stream));
@@ -902,7 +773,7 @@ struct s2x_text {
             st[(size_t)b] = b * n_tok;
             last[(size_t)b] = b * n_tok + n_tok - 1;
         }
-        S2X_TRY(t.set_segments(st, ln));
+        S2X_TRY(t.set_segments(st, ln, M));
         hipError_t e = launch_get_rows_q8_0(tok, H, vocab, ids.as<int32_t>(), M, pos_embd, n_tok,
                                             t.x.as<float>(), t.stream);
         if (e != hipSuccess) return hip_fail(e, "get_rows launch");

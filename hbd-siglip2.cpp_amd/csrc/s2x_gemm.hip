@@ -1,0 +1,725 @@
+// s2x_gemm.hip -- Q8_0 (weights) x Q8_1 (activations) GEMM on gfx950 int8
+// MFMA, with the fused epilogues of the SigLIP2 encoder block.
+//
+//   Y[m, n] = epilogue( sum over K blocks kb, in block order:
+//                         acc = fmaf((float)I_kb[m,n], dw[n,kb] * dx[m,kb], acc) )
+//
+// I_kb is the exact int32 dot of the 32 quants of block kb; dw and dx are the
+// fp16 block scales (src/cuda/siglip2_custom_mmq.cu:259-267 is the same
+// per-block rescale).  Per 32 x 32 output subtile and K block:
+//   * I   = one v_mfma_i32_32x32x32_i8 (exact);
+//   * s   = dx[i] * dw[j] as one v_mfma_f32_32x32x8_f16 whose A holds dx in
+//           k-slot 0 and B holds dw in k-slot 0, every other slot zero: each
+//           output is one exact f16 x f16 product in f32;
+//   * acc = fmaf((float)I, s, acc) on the VALU (convert + fma).
+// The VALU part (32 instructions per subtile and block, 128 SIMD cycles) is
+// the arithmetic bound of this formulation: a quarter of the int8 MFMA peak.
+//
+// Work decomposition.  128 x 128 output tiles, one per workgroup of 8 / TM
+// waves (each 32 TM x 64: TM x 2 subtiles), two workgroups per CU so that
+// one's epilogue and pipeline fill overlap the other's K loop.  The K loop
+// runs over stages of KS = 4 blocks (each row's 128 contiguous bytes) whose
+// operands (X and W quants and scales) arrive by LDS DMA
+// (buffer_load ... lds) into a ring of 2 stage buffers, one stage ahead;
+// one workgroup barrier per stage.  With TM = 2 the fragments of the next K
+// block are read from LDS while the current block is in the MFMAs.
+//
+// Scale layouts: X scales are the Q8_1 ds words of the activation
+// (ds[m * ld_ds + kb] = fp16 d | fp16 s << 16, the block_q8_1 scale pair);
+// W scales are fp16 bits transposed, dT[kb * ldT + n].
+//
+// LDS layout of one stage (bytes):
+//   XQ  [KS][128 rows][32]  X quants, the two 16-byte chunks of row r at
+//                            chunk position c ^ swz(r)
+//   WQ  [KS][128 rows][32]  W quants, same swizzle
+//   XS  [KS][128] u32        X ds words
+//   WS  [KS][128 + 40] u16   W scales, each block's followed by zeros
+// A fragment read (lane l: row l & 31, chunk l >> 5, 16 bytes) then touches
+// 16 distinct 16-byte bank groups per 16 lanes: no bank conflicts.
+#include "s2x_device.h"
+#include "s2x_kernels.h"
+
+namespace s2x {
+namespace gemm {
+
+constexpr int BN = 128;  // output tile columns
+constexpr int KS = 4;    // K blocks per stage
+constexpr int GM = 8;    // tile-row group of the tile order
+constexpr int WSB = BN * 2 + 80;  // W scales of a block: BN fp16 values, then 80 zero bytes
+constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
+
+// 128 x 128 output tiles; 8 / TM waves of 32 TM x 64 outputs; PF: the next
+// block's fragments are read during the current block (register budget:
+// TM = 2 waves run 2 per SIMD, TM = 1 waves 4 per SIMD).
+template <int TM_>
+struct Cfg {
+    static constexpr int TM = TM_, BM = 128, NS = 2;
+    static constexpr int NWAVE = 8 / TM, NT = NWAVE * WAVE;
+    static constexpr bool PF = TM == 2;
+    static constexpr int XQ = 0;                  // [KS][BM][32] X quants
+    static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
+    static constexpr int XS = WQ + KS * BN * 32;  // [KS][BM] u32 X ds words
+    static constexpr int WS = XS + KS * BM * 4;   // [KS] x (BN fp16 + zeros) W scales
+    static constexpr int STAGE = WS + KS * WSB;
+    static constexpr int LDS_BYTES = NS * STAGE;
+    // DMA instructions per stage and wave: QPW X-quant and QPW W-quant (each
+    // 32 rows of one block), SPW X-scale (64 rows of one block) and 1 W-scale
+    // (with 8 waves, waves w and w + 4 both fetch the W scales of block
+    // w & 3 -- the same bytes to the same place -- so that every wave issues
+    // the same count)
+    static constexpr int QPW = 16 / NWAVE, SPW = 8 / NWAVE;
+    static constexpr int DMA_N = 2 * QPW + SPW + 1;
+    static_assert(TM == 1 || TM == 2, "wave tile");
+    static_assert(2 * LDS_BYTES <= 163840, "two workgroups per CU");
+    static_assert(NWAVE * 32 * 36 * 4 <= LDS_BYTES && NWAVE * 64 * 40 * 2 <= LDS_BYTES,
+                  "epilogue scratch");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// chunk permutation of the two 16-byte chunks of a 32-byte row
+__device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                      uint8_t *lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                     uint8_t *lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 4, voff, soff, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ int clip32(int64_t bytes) {
+    return (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
+}
+
+// Output tile of logical index T: groups of GM row tiles walk N together.
+__device__ __forceinline__ void tile_of(int T, int m_tiles, int n_tiles, int &tm, int &tn) {
+    const int group_size = GM * n_tiles;
+    const int group = T / group_size;
+    const int first_m = group * GM;
+    const int gm = min(GM, m_tiles - first_m);
+    const int in_group = T - group * group_size;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
+// One K block's MFMA operands for a wave's TM x 2 subtiles.  The scale
+// operands are the 4-half (two-dword) f16 vectors of a 32x32x8 MFMA: dword 0
+// holds the scale in its low half (k slot 0 on lanes 0..31, slot 4 on lanes
+// 32..63), dword 1 is always zero.  Lanes 32..63 load the row scale too but
+// a zero column scale, so slot 4 adds nothing.
+template <int TM>
+struct Frag {
+    v4i a[TM], b[2];
+    v2i sx[TM], sw[2];
+};
+
+template <class C, int EPI>
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm(
+    const uint8_t *__restrict__ xq, const uint32_t *__restrict__ xds, int64_t ld_ds,
+    const uint8_t *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ldT, int M, int N,
+    int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
+    constexpr int BM = C::BM, NS = C::NS, STAGE = C::STAGE, TM = C::TM;
+    constexpr int XQ = C::XQ, WQ = C::WQ, XS = C::XS, WS = C::WS;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(xcd_linear(blockIdx.x, gridDim.x), m_tiles, n_tiles, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int n_st = (KB + KS - 1) / KS;
+    const int64_t row_bytes = (int64_t)KB * QK;
+
+    // Per-lane DMA source offsets (relative to the tile's first row / column;
+    // the K position goes into the scalar offset).
+    //   X and W quants, instructions t < QPW: i = QPW wave + t, block i & 3,
+    //             rows 32 (i >> 2) .. + 31
+    //   X scales, instructions t < SPW: i = SPW wave + t, block i >> 1,
+    //             rows 64 (i & 1) .. + 63 (one ds word per lane)
+    //   W scales: block wave & 3, columns 2 lane, 2 lane + 1
+    uint32_t vq, vxs[C::SPW];
+    {
+        const int r = 32 * ((C::QPW * wave) >> 2) + (lane >> 1);
+        vq = (uint32_t)(r * row_bytes) + (uint32_t)(((lane & 1) ^ swz(r)) * 16);
+#pragma unroll
+        for (int t = 0; t < C::SPW; ++t) {
+            const int i = C::SPW * wave + t;
+            vxs[t] = (uint32_t)(((i & 1) * 64 + lane) * ld_ds * 4);
+        }
+    }
+    const __amdgpu_buffer_rsrc_t xr_live = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(xq + (int64_t)m0 * row_bytes), (short)0, clip32((int64_t)(M - m0) * row_bytes), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t wr_live = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(wq + (int64_t)n0 * row_bytes), (short)0, clip32((int64_t)(N - n0) * row_bytes), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t xsr_live = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(xds + (int64_t)m0 * ld_ds), (short)0, clip32((int64_t)(M - m0) * ld_ds * 4), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t wsr_live = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(wdT + n0), (short)0, clip32(((int64_t)KB * ldT - n0) * 2), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, 0, BUF_DW3);
+
+    // Issue the DMA of stage g into buffer g % NS.  Reads past M, N or the
+    // planes return zeros; blocks past KB in the last stage are fetched and
+    // never used.  The stage after the last is issued too, through
+    // zero-size buffers (no memory is read), so that no branch splits the K
+    // loop.
+    auto issue = [&](int g) {
+        const bool live = g < n_st;
+        const __amdgpu_buffer_rsrc_t xr = live ? xr_live : none, wr = live ? wr_live : none;
+        const __amdgpu_buffer_rsrc_t xsr = live ? xsr_live : none, wsr = live ? wsr_live : none;
+        uint8_t *sb = lds + (g & 1) * STAGE;
+        const uint32_t k0 = (uint32_t)(g * KS);
+#pragma unroll
+        for (int t = 0; t < C::QPW; ++t) {
+            const int i = C::QPW * wave + t, j = i & 3;
+            dma16(xr, vq, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i >> 2) * 1024);
+        }
+#pragma unroll
+        for (int t = 0; t < C::QPW; ++t) {
+            const int i = C::QPW * wave + t, j = i & 3;
+            dma16(wr, vq, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i >> 2) * 1024);
+        }
+#pragma unroll
+        for (int t = 0; t < C::SPW; ++t) {
+            const int i = C::SPW * wave + t, j = i >> 1;
+            dma4(xsr, vxs[t], (k0 + j) * 4, sb + XS + j * BM * 4 + (i & 1) * 256);
+        }
+        dma4(wsr, (uint32_t)lane * 4, (uint32_t)((k0 + (wave & 3)) * ldT * 2),
+             sb + WS + (wave & 3) * WSB);
+    };
+
+    // Stage g visible to every wave: this wave's DMA of it has landed, then
+    // the barrier.  After the barrier no wave reads the buffer of stage
+    // g - 1 any more (its last fragments were read before this point), so
+    // stage g + 1 refills it.
+    auto arrive = [&](int g) {
+        wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(g + 1);
+    };
+
+    // fragment addresses (bytes within a stage buffer) of this lane
+    const int xrow = wm * 32 * TM + lr, wcol = wn * 64 + lr;
+    const int a_off = XQ + xrow * 32 + ((lh ^ swz(lr)) * 16);
+    const int b_off = WQ + wcol * 32 + ((lh ^ swz(lr)) * 16);
+    const int sx_off = XS + xrow * 4;
+    const int sw_off = lh ? WS + BN * 2 : WS + wcol * 2;  // lanes 32..63: the zero pad
+    auto load_frag = [&](const uint8_t *sb, auto jc, Frag<TM> &f) {
+        constexpr int j = decltype(jc)::value;
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+            f.a[a] = *reinterpret_cast<const v4i *>(sb + a_off + j * BM * 32 + a * 32 * 32);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            f.b[b] = *reinterpret_cast<const v4i *>(sb + b_off + j * BN * 32 + b * 32 * 32);
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+            f.sx[a][0] = *reinterpret_cast<const uint16_t *>(sb + sx_off + j * BM * 4 + a * 32 * 4);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            f.sw[b][0] = *reinterpret_cast<const uint16_t *>(sb + sw_off + j * WSB + b * 32 * 2);
+    };
+
+    float acc[TM][2][16];
+    Frag<TM> F[C::PF ? 2 : 1];
+#pragma unroll
+    for (int i = 0; i < (C::PF ? 2 : 1); ++i) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a) F[i].sx[a] = v2i{0, 0};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) F[i].sw[b] = v2i{0, 0};
+    }
+
+    // One K block, subtile k = 2a + b.  Step k issues subtile k's two MFMAs
+    // into result slot k & 1, each followed by half of the rescale of the
+    // previous subtile (k - 1, or the last subtile of the previous block for
+    // k = 0), so every MFMA result is read two MFMAs after its issue and the
+    // matrix pipe and the VALU overlap within the wave.  The last subtile's
+    // rescale stays pending into the next block (flush() after the last
+    // block).  The pending slot starts as I = 0, s = 0: fmaf(0, 0, +0) = +0.
+    // Each acc element still receives its fmas in block order.
+    constexpr int NSUB = 2 * TM;
+    v16i I[2];
+    v16f S[2];
+    auto rescale = [&](int slot, int pa, int pb) {
+        float c[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) c[r] = (float)I[slot][r];
+        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf(c[r], S[slot][r], acc[pa][pb][r]);
+        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+    };
+    auto compute = [&](const Frag<TM> &f, int kb) {
+        const v16f zf = {};
+        const v16i zi = {};
+        if constexpr (EPI == EPI_DUMP_I) {
+#pragma unroll
+            for (int k = 0; k < NSUB; ++k) {
+                const int a = k >> 1, b = k & 1;
+                const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], zi, 0, 0, 0);
+                if (kb == (int)epi.dump_kb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        // through a scalar: bit_cast of a vector element
+                        // operand compiles to element 0 here
+                        const int t = D[r];
+                        acc[a][b][r] = __builtin_bit_cast(float, t);
+                    }
+                }
+            }
+        } else {
+            // the next block's fragment reads (issued just before) go first
+            if constexpr (C::PF) __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * TM, 0);
+#pragma unroll
+            for (int k = 0; k < NSUB; ++k) {
+                const int a = k >> 1, b = k & 1;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                I[k & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], zi, 0, 0, 0);
+                const int p = (k + NSUB - 1) % NSUB;  // previous subtile, in the other slot
+                S[k & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.sx[a]),
+                                                                __builtin_bit_cast(v4h, f.sw[b]), zf, 0, 0, 0);
+                rescale((k + 1) & 1, p >> 1, p & 1);
+            }
+        }
+        // one scheduling region per block: nothing moves across blocks
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto flush = [&] {
+        if constexpr (EPI != EPI_DUMP_I) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acc[TM - 1][1][r] = fmaf((float)I[1][r], S[1][r], acc[TM - 1][1][r]);
+        }
+    };
+
+    // the zero pads after each block's W scales (never written by the DMA)
+    if (tid < NS * KS * 5) {
+        const int i = tid / 5, c = tid % 5;
+        *reinterpret_cast<v4i *>(lds + (i / KS) * STAGE + WS + (i % KS) * WSB + BN * 2 + c * 16) =
+            v4i{0, 0, 0, 0};
+    }
+    float bias_v[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int n = n0 + wcol + b * 32;
+        bias_v[b] = EPI != EPI_NONE && EPI != EPI_DUMP_I && n < N ? epi.bias[n] : 0.0f;
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        I[1][r] = 0;
+        S[1][r] = 0.0f;
+    }
+
+    issue(0);
+    arrive(0);
+    using J0 = std::integral_constant<int, 0>;
+    using J1 = std::integral_constant<int, 1>;
+    using J2 = std::integral_constant<int, 2>;
+    using J3 = std::integral_constant<int, 3>;
+    if constexpr (C::PF) {
+        // block j uses fragment set j & 1 and reads block j + 1's fragments
+        // into the other set (at j = 3: the next stage's block 0, after the
+        // barrier that makes that stage visible)
+        load_frag(lds, J0{}, F[0]);
+        for (int g = 0; g < n_st - 1; ++g) {
+            const uint8_t *sb = lds + (g & 1) * STAGE;
+            const int kb0 = g * KS;
+            load_frag(sb, J1{}, F[1]);
+            compute(F[0], kb0);
+            load_frag(sb, J2{}, F[0]);
+            compute(F[1], kb0 + 1);
+            load_frag(sb, J3{}, F[1]);
+            compute(F[0], kb0 + 2);
+            arrive(g + 1);
+            load_frag(lds + ((g + 1) & 1) * STAGE, J0{}, F[0]);
+            compute(F[1], kb0 + 3);
+        }
+        // the last stage: nb = 1..4 blocks
+        const uint8_t *sb = lds + ((n_st - 1) & 1) * STAGE;
+        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
+        if (nb > 1) load_frag(sb, J1{}, F[1]);
+        compute(F[0], kb0);
+        if (nb > 1) {
+            if (nb > 2) load_frag(sb, J2{}, F[0]);
+            compute(F[1], kb0 + 1);
+            if (nb > 2) {
+                if (nb > 3) load_frag(sb, J3{}, F[1]);
+                compute(F[0], kb0 + 2);
+                if (nb > 3) compute(F[1], kb0 + 3);
+            }
+        }
+    } else {
+        // each block's fragments read right before its MFMAs (the other
+        // waves of the SIMD cover the LDS latency)
+        for (int g = 0; g < n_st - 1; ++g) {
+            const uint8_t *sb = lds + (g & 1) * STAGE;
+            const int kb0 = g * KS;
+            load_frag(sb, J0{}, F[0]);
+            compute(F[0], kb0);
+            load_frag(sb, J1{}, F[0]);
+            compute(F[0], kb0 + 1);
+            load_frag(sb, J2{}, F[0]);
+            compute(F[0], kb0 + 2);
+            load_frag(sb, J3{}, F[0]);
+            compute(F[0], kb0 + 3);
+            arrive(g + 1);
+        }
+        const uint8_t *sb = lds + ((n_st - 1) & 1) * STAGE;
+        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
+        load_frag(sb, J0{}, F[0]);
+        compute(F[0], kb0);
+        if (nb > 1) {
+            load_frag(sb, J1{}, F[0]);
+            compute(F[0], kb0 + 1);
+            if (nb > 2) {
+                load_frag(sb, J2{}, F[0]);
+                compute(F[0], kb0 + 2);
+                if (nb > 3) {
+                    load_frag(sb, J3{}, F[0]);
+                    compute(F[0], kb0 + 3);
+                }
+            }
+        }
+    }
+    flush();
+
+    {
+        // ------------------------------------------------------------------
+        // Epilogue.  The LDS is free scratch once the last (empty) stage's
+        // DMA has landed and every wave has read its last fragments.
+        // ------------------------------------------------------------------
+        uint8_t *scratch = lds;
+        const int mw = m0 + wm * 32 * TM;  // first row of this wave
+        const int nw = n0 + wn * 64;       // first column of this wave
+
+        if constexpr (EPI == EPI_GELU_Q81) {
+            // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over
+            // rows of q_kpad values (columns >= N are zeros): each 32 x 32
+            // subtile is one quant block per row; it goes through LDS so that
+            // lane pairs own a row (16 values each)
+            constexpr int P = 36;  // floats per scratch row
+            wait_vm<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            float *scr = reinterpret_cast<float *>(scratch) + wave * 32 * P;
+            const int row = lane >> 1, half = lane & 1;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int nb0 = nw + b * 32;  // first column of this quant block
+                    if (nb0 >= epi.q_kpad) continue;  // wave-uniform
+                    const int n = nb0 + lr;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
+                            n < N ? gelu_tanh(acc[a][b][r] + bias_v[b]) : 0.0f;
+                    float v[16];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4f t = *reinterpret_cast<const v4f *>(scr + row * P + half * 16 + 4 * j);
+                        v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
+                    }
+                    float am = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
+                    am = fmaxf(am, dpp_f<0xb1>(am));  // partner lane (xor 1)
+                    const float d = am / 127.0f;
+                    const float inv = am != 0.0f ? 127.0f / am : 0.0f;
+                    int qi[16], qs = 0;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        qi[j] = q8_round(v[j], inv);
+                        qs += qi[j];
+                    }
+                    qs += dpp_i<0xb1>(qs);
+                    const int m = mw + a * 32 + row;
+                    if (m < M) {
+                        const int64_t off = (int64_t)m * epi.q_kpad + nb0 + half * 16;
+                        *reinterpret_cast<uint4 *>(epi.q_out8 + off) =
+                            make_uint4(pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7]),
+                                       pack4_i8(qi[8], qi[9], qi[10], qi[11]),
+                                       pack4_i8(qi[12], qi[13], qi[14], qi[15]));
+                        if (half == 0)
+                            epi.q_ds[(int64_t)m * epi.q_ldds + nb0 / QK] =
+                                (uint32_t)f32_to_f16_bits(d) |
+                                ((uint32_t)f32_to_f16_bits((float)qs * d) << 16);
+                    }
+                }
+        } else if constexpr (EPI == EPI_QKV) {
+            // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad]
+            // or V^T [seg][head][dv_pad][pos]; padding slots are not written
+            const int H = epi.n_head * epi.d_head;
+            const float inv_dh = 1.0f / (float)epi.d_head;
+            wait_vm<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (H % BN == 0 && n0 < 2 * H && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
+                // a Q or K tile: each 32-row half of the wave's 32 x 64 block
+                // goes through LDS so that each 8-column chunk of a row (8
+                // consecutive d of one head) leaves as one 16-byte store
+                constexpr int P = 72;  // halves per scratch row
+                _Float16 *scr = reinterpret_cast<_Float16 *>(scratch) + wave * 32 * P;
+                _Float16 *dst0 = n0 < H ? epi.q : epi.k;
+                const int hd0 = n0 < H ? 0 : H;
+#pragma unroll
+                for (int a = 0; a < TM; ++a) {
+                    int rmv[4];  // row map entries, loaded before the stores
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        rmv[i] = epi.rowmap[min(mw + a * 32 + ((lane + 64 * i) >> 3), M - 1)];
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] =
+                                f32_to_f16(acc[a][b][r] + bias_v[b]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
+                        const int m = mw + a * 32 + row, n = nw + c;
+                        if (m >= M || n >= N) continue;
+                        const int hd = n - hd0;
+                        const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
+                        const int rm = rmv[i];
+                        const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                        const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
+                        *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
+                    }
+                }
+            } else if (H % BN == 0 && n0 >= 2 * H) {
+                // a V tile: V^T rows are positions, so each 32-row half goes
+                // through LDS transposed (column-major, rows shifted by the
+                // first position's offset within its 8-position chunk) and
+                // each lane writes one column -- one d of one head: up to 32
+                // consecutive positions -- as 16-byte stores where the
+                // destination is 16-byte aligned, 2-byte stores at the ends
+                constexpr int PT = 40;  // halves per scratch column (shift <= 7, 32 rows)
+                _Float16 *scr = reinterpret_cast<_Float16 *>(scratch) + wave * 64 * PT;
+                const int n = nw + lane;
+                const int hd = n - 2 * H, h = small_div(max(hd, 0), epi.d_head, inv_dh);
+                const int d = hd - h * epi.d_head;
+#pragma unroll
+                for (int a = 0; a < TM; ++a) {
+                    const int mr = mw + a * 32;
+                    const int rows = min(32, M - mr);  // wave-uniform, may be <= 0
+                    int rm_first = 0, rm_last = 0;
+                    if (rows > 0) {
+                        rm_first = epi.rowmap[mr];
+                        rm_last = epi.rowmap[mr + rows - 1];
+                    }
+                    // one segment, consecutive positions: the common case
+                    const bool run = rows > 0 && (rm_last >> 16) == (rm_first >> 16) &&
+                                     (rm_last & 0xffff) - (rm_first & 0xffff) == rows - 1;
+                    const int shift = run ? (rm_first & 0xffff) & 7 : 0;
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                scr[(b * 32 + lr) * PT + shift + 8 * q + 4 * lh + j] =
+                                    f32_to_f16(acc[a][b][4 * q + j] + bias_v[b]);
+                    if (rows > 0 && n < N) {
+                        const _Float16 *col = scr + lane * PT;
+                        if (run) {
+                            const int64_t sh = (int64_t)(rm_first >> 16) * epi.n_head + h;
+                            _Float16 *dst =
+                                epi.vt + (sh * epi.dv_pad + d) * epi.len_pad + (rm_first & 0xffff) - shift;
+                            // positions [shift, shift + rows) of the 8-aligned window dst[0 ..)
+                            const int lo = shift, hi = shift + rows;
+                            const int a0 = (lo + 7) & ~7, a1 = hi & ~7;
+                            if (a0 <= a1) {
+                                for (int i = lo; i < a0; ++i) dst[i] = col[i];
+                                for (int i = a0; i < a1; i += 8)
+                                    *reinterpret_cast<v8h *>(dst + i) = *reinterpret_cast<const v8h *>(col + i);
+                                for (int i = a1; i < hi; ++i) dst[i] = col[i];
+                            } else {
+                                for (int i = lo; i < hi; ++i) dst[i] = col[i];
+                            }
+                        } else {
+                            for (int i = 0; i < rows; ++i) {
+                                const int rm = epi.rowmap[mr + i];
+                                const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                                epi.vt[(sh * epi.dv_pad + d) * epi.len_pad + (rm & 0xffff)] = col[i];
+                            }
+                        }
+                    }
+                }
+            } else {
+                // any H: one 2-byte store per element
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int n = nw + b * 32 + lr;
+                    if (n >= N) continue;
+                    const int part = small_div(n, H, 1.0f / (float)H), hd = n - part * H;
+                    const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
+                    _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                            if (m >= M) continue;
+                            const int rm = epi.rowmap[m];
+                            const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                            const int pos = rm & 0xffff;
+                            const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
+                                                         : (sh * epi.dv_pad + d) * epi.len_pad + pos;
+                            dst[off] = f32_to_f16(acc[a][b][r] + bias_v[b]);
+                        }
+                }
+            }
+        } else {
+            // (mm + bias) [GELU | + residual], through buffer loads and stores
+            // whose bounds drop the rows past M (and the columns past N, sent
+            // out of range): no branch per element.  Each 32-row half's
+            // residual loads are all issued before its first store (y may be
+            // the residual itself: each element is read, then written, by
+            // one lane).
+            constexpr uint32_t OOB = 0x80000000u;
+            const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(y + (int64_t)m0 * ldy), (short)0, clip32((int64_t)(M - m0) * ldy * 4), BUF_DW3);
+            const bool rmod = epi.resid_rows > 0;
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(epi.resid + (rmod ? 0 : (int64_t)m0 * epi.ld_resid)), (short)0,
+                EPI == EPI_BIAS_RESID
+                    ? clip32((rmod ? epi.resid_rows : (int64_t)(M - m0)) * epi.ld_resid * 4)
+                    : 0,
+                BUF_DW3);
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                float res[2][16];
+                if constexpr (EPI == EPI_BIAS_RESID) {
+                    // residual row of this lane's first row in the half; the
+                    // others are at most 27 rows further (one wrap when
+                    // resid_rows >= 28)
+                    const int R = (int)epi.resid_rows;
+                    const int m_first = mw + a * 32 + 4 * lh;
+                    const int r_first = rmod ? m_first % R : m_first - m0;
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        const int n = nw + b * 32 + lr;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int dm = 8 * (r >> 2) + (r & 3);
+                            int rm = r_first + dm;
+                            if (rmod) rm = R >= 28 ? (rm >= R ? rm - R : rm) : rm % R;
+                            const uint32_t off =
+                                n < N ? (uint32_t)(rm * (int)epi.ld_resid + n) * 4u : OOB;
+                            const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0);
+                            res[b][r] = __builtin_bit_cast(float, bits);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int n = nw + b * 32 + lr;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float v = acc[a][b][r];
+                        if (EPI == EPI_BIAS) {
+                            v = v + bias_v[b];
+                        } else if (EPI == EPI_BIAS_GELU) {
+                            v = gelu_tanh(v + bias_v[b]);
+                        } else if (EPI == EPI_BIAS_RESID) {
+                            v = (v + bias_v[b]) + res[b][r];
+                        }
+                        const int mr = wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        const uint32_t off = n < N ? (uint32_t)(mr * (int)ldy + n) * 4u : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr,
+                                                              off, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // Every DMA this wave issued has landed before the workgroup ends.
+    wait_vm<0>();
+}
+
+template <class C, int EPI>
+hipError_t run(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+               int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    auto kern = k_gemm<C, EPI>;
+    static bool attr_set = false;  // idempotent; a racing second call repeats it harmlessly
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 C::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((w.N + BN - 1) / BN);
+    // without scales (the block-dot dump) the scale DMA reads a zero-size
+    // buffer at a valid address
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::NT), C::LDS_BYTES, stream,
+                       reinterpret_cast<const uint8_t *>(xq),
+                       xds ? xds : reinterpret_cast<const uint32_t *>(xq), xds ? ld_ds : 0,
+                       reinterpret_cast<const uint8_t *>(w.qs), w.dT, w.ldT, (int)M, (int)w.N,
+                       (int)(w.K_pad / QK), y, ldy, epi);
+    return hipGetLastError();
+}
+
+}  // namespace gemm
+
+#ifndef S2X_GEMM_TM
+#define S2X_GEMM_TM 1
+#endif
+using Default = gemm::Cfg<S2X_GEMM_TM>;
+
+hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                       int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                       hipStream_t stream) {
+    using C = Default;
+    if (M == 0 || w.N == 0) return hipSuccess;
+    const int64_t KB = w.K_pad / QK;
+    if (!w.qs || !w.dT || !xq || w.K_pad <= 0 || w.K_pad % QK || w.ldT < (w.N + 127) / 128 * 128 ||
+        M > (1 << 30) || w.N > (1 << 30) || ((uintptr_t)xq & 15) || ((uintptr_t)w.qs & 15) ||
+        ((uintptr_t)xds & 3) || (epi.kind != EPI_DUMP_I && (!xds || ld_ds < KB)) ||
+        (int64_t)C::BM * KB * QK > 0x7fffffff || w.ldT * KB * 2 > 0x7fffffff ||
+        C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff)
+        return hipErrorInvalidValue;
+    switch (epi.kind) {
+    case EPI_NONE: return gemm::run<C, EPI_NONE>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_BIAS: return gemm::run<C, EPI_BIAS>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_BIAS_GELU: return gemm::run<C, EPI_BIAS_GELU>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_BIAS_RESID:
+        if (!epi.resid || epi.ld_resid < w.N || epi.resid_rows < 0 ||
+            (epi.resid_rows > 0 ? epi.resid_rows : C::BM) * epi.ld_resid * 4 > 0x7fffffff)
+            return hipErrorInvalidValue;
+        return gemm::run<C, EPI_BIAS_RESID>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_DUMP_I:
+        if (epi.dump_kb < 0 || epi.dump_kb >= KB) return hipErrorInvalidValue;
+        return gemm::run<C, EPI_DUMP_I>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_GELU_Q81:
+        if (!epi.q_out8 || !epi.q_ds || !epi.bias || epi.q_kpad % QK || epi.q_kpad < w.N ||
+            epi.q_kpad - w.N >= QK || epi.q_ldds < epi.q_kpad / QK ||
+            ((uintptr_t)epi.q_out8 & 15) || ((uintptr_t)epi.q_ds & 3))
+            return hipErrorInvalidValue;
+        return gemm::run<C, EPI_GELU_Q81>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_QKV:
+        if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
+            epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head || w.N >= (1 << 20))
+            return hipErrorInvalidValue;
+        return gemm::run<C, EPI_QKV>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace s2x

@@ -15,34 +15,29 @@ constexpr int64_t MAX_SEG_LEN = 4096;
 
 // Device view of a repacked Q8_0 weight (K_pad, N).
 struct WeightView {
-    const int8_t *qs;     // N rows of K_pad int8
-    const float  *d;      // N rows of KB f32 (fp16 values widened)
-    const _Float16 *qh;   // N rows of K_pad f16 holding the same integers
+    const int8_t *qs;     // N rows of K_pad int8 (16-byte aligned)
     const uint16_t *dT;   // KB rows of ldT fp16 bits of d (transposed)
-    int64_t ldT;          // >= round_up(N, MMQ16_BN)
+    int64_t ldT;          // >= round_up(N, GEMM_BN)
     int64_t K_pad;        // multiple of 32
     int64_t N;
 };
 
-// Output tile of the f16-MFMA GEMM; transposed scale planes are padded to it.
-constexpr int64_t MMQ16_BM = 256;
-constexpr int64_t MMQ16_BN = 128;
-inline int64_t mmq16_ld_dx(int64_t M) { return (M + MMQ16_BM - 1) / MMQ16_BM * MMQ16_BM; }
-inline int64_t mmq16_ld_dw(int64_t N) { return (N + MMQ16_BN - 1) / MMQ16_BN * MMQ16_BN; }
+// Column tile of the GEMM; the transposed weight scales are padded to it.
+constexpr int64_t GEMM_BN = 128;
+inline int64_t gemm_ld_dw(int64_t N) { return (N + GEMM_BN - 1) / GEMM_BN * GEMM_BN; }
 
-// Destination planes of a Q8_1 quantization (any subset may be null).
+// Destination planes of a Q8_1 quantization: int8 quants [M][K_pad] and the
+// block_q8_1 scale words [M][ld_ds] (fp16 d | fp16 s << 16), ld_ds >= K_pad/32.
 struct Q81Out {
-    int8_t   *qs = nullptr;  // [M][K_pad] int8 quants
-    _Float16 *qh = nullptr;  // [M][K_pad] the same quants as f16 (exact)
-    uint32_t *ds = nullptr;  // [M][KB] fp16 d | fp16 s << 16 (block_q8_1 scales)
-    uint16_t *dT = nullptr;  // [KB][ldT] fp16 bits of d, transposed
-    int64_t   ldT = 0;
+    int8_t   *qs = nullptr;
+    uint32_t *ds = nullptr;
+    int64_t   ld_ds = 0;  // 0: K_pad / 32
 };
 
 enum EpiKind {
     EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4,
-    EPI_QKV = 5,       // f16 GEMM only: (mm + bias) -> f16 Q / K / V^T in the attention layout
-    EPI_GELU_Q81 = 6,  // f16 GEMM only: GELU(mm + bias) quantized to Q8_1 (f16 quants + d^T)
+    EPI_QKV = 5,       // (mm + bias) -> f16 Q / K / V^T in the attention layout
+    EPI_GELU_Q81 = 6,  // GELU(mm + bias) quantized to Q8_1 (int8 quants + ds words)
 };
 
 struct EpiParams {
@@ -57,13 +52,11 @@ struct EpiParams {
     _Float16      *q, *k, *vt;
     const int32_t *rowmap;
     int            n_head, d_head, d_pad, dv_pad, len_pad;
-    // EPI_GELU_Q81: quants [M][q_kpad] (columns N..q_kpad-1 quantize zeros),
-    // f16 (q_out, f16 GEMM) or int8 (q_out8, int8 GEMM), and transposed
-    // scales [q_kpad/32][q_ld]
-    _Float16 *q_out;
+    // EPI_GELU_Q81: quants [M][q_kpad] (columns N..q_kpad-1 quantize zeros)
+    // and ds words [M][q_ldds]
     int8_t   *q_out8;
-    uint16_t *q_dT;
-    int64_t   q_kpad, q_ld;
+    uint32_t *q_ds;
+    int64_t   q_kpad, q_ldds;
 };
 
 // a1: F32 -> Q8_1 into the planes of `out`.
@@ -71,29 +64,15 @@ hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ld
                                 int64_t K_pad, const Q81Out &out, hipStream_t stream);
 
 // a2: raw block_q8_0 (N rows of K_pad/32 34-byte blocks, device) -> WeightView
-// planes (qh / dT may be null)
+// planes
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
-                              float *d, _Float16 *qh, uint16_t *dT, int64_t ldT,
-                              hipStream_t stream);
+                              uint16_t *dT, int64_t ldT, hipStream_t stream);
 
-// a3: Y = W x X(Q8_1) with epilogue.
-// launch_mmq: int8 operands, v_mfma_i32_32x32x32_i8 block dots, VALU rescale.
-hipError_t launch_mmq(const WeightView &w, const int8_t *xq, const uint32_t *xds,
-                      int64_t M, float *y, int64_t ldy, const EpiParams &epi,
-                      hipStream_t stream);
-// launch_mmq_f16: f16-coded operands (w.qh / w.dT, xh [M][K_pad] and the
-// transposed X scales xdT [KB][ld_dx], ld_dx >= mmq16_ld_dx(M)), block dots
-// and the dx*dw scale tile on f16 MFMA, one VALU fma per element and block.
-// xh, xdT, w.qh and w.dT must be 16-byte aligned and ld_dx a multiple of 8.
-hipError_t launch_mmq_f16(const WeightView &w, const _Float16 *xh, const uint16_t *xdT,
-                          int64_t ld_dx, int64_t M, float *y, int64_t ldy,
-                          const EpiParams &epi, hipStream_t stream);
-// The same kernel over int8 quants (w.qs, xq [M][K_pad]): one
-// v_mfma_i32_32x32x32_i8 per block dot, then (float) I in the fma.  Same
-// bits as launch_mmq_f16 and launch_mmq.
-hipError_t launch_mmq_i8(const WeightView &w, const int8_t *xq, const uint16_t *xdT,
-                         int64_t ld_dx, int64_t M, float *y, int64_t ldy, const EpiParams &epi,
-                         hipStream_t stream);
+// a3: Y = W x X(Q8_1) with epilogue, on int8 MFMA (s2x_gemm.hip).  xq: int8
+// quants [M][K_pad] (16-byte aligned), xds: ds words [M][ld_ds].
+hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                       int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                       hipStream_t stream);
 
 // a4: LayerNorm (+ Q8_1).  q may be null (no quantized output), y may be
 // null (no f32 output); at least one is set.
@@ -113,19 +92,20 @@ struct AttnLayout {
     int64_t d_pad;     // d_head rounded up to 16 (Q/K row length)
     int64_t dv_pad;    // d_head rounded up to 32 (V^T rows)
     int64_t len_pad;   // max_len rounded up to 128 (query tile)
-    size_t q_off, k_off, vt_off, bytes;
+    size_t q_off, k_off, vt_off, planes_bytes;  // Q, K, V^T planes
+    size_t rowmap_off, bytes;  // + n_seg * max_len int32 (fused QKV entry point)
     // softmax probabilities enter the PV product as an exact f16 pair
     // (hi + lo, ~22 bits) instead of one f16 (11 bits)
     bool p_split = true;
 };
 AttnLayout attn_layout(int64_t n_seg, int64_t max_len, int64_t n_head, int64_t d_head);
-AttnLayout attn_sublayout(const AttnLayout &L, int64_t s0, int64_t s1);
 hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                             const int32_t *seg_start, const int32_t *seg_len,
                             const AttnLayout &L, void *ws, hipStream_t stream);
-// Row -> (segment << 16 | position) table of packed segments, for EPI_QKV.
+// Row -> (segment << 16 | position) table of packed segments, for EPI_QKV
+// (rows outside [0, n_rows) are not written).
 hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
-                         int64_t max_len, int32_t *rowmap, hipStream_t stream);
+                         int64_t max_len, int32_t *rowmap, int64_t n_rows, hipStream_t stream);
 // EPI_QKV destination planes of layout L in workspace ws.
 EpiParams epi_qkv(const AttnLayout &L, void *ws, const float *qkv_bias, const int32_t *rowmap);
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
@@ -167,6 +147,8 @@ hipError_t launch_gather_rows(const float *x, int64_t H, const int32_t *rows,
 hipError_t launch_pack_rows(const float *padded, int64_t row_len, int64_t max_rows,
                             const int32_t *seg_start, const int32_t *seg_len,
                             int64_t n_seg, float *packed, hipStream_t stream);
+// bytes of zeros (16-byte aligned p), a kernel (no memset node in captured graphs)
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t stream);
 // y[i] = a[i] + b[i]
 hipError_t launch_add(const float *a, const float *b, float *y, int64_t n,
                       hipStream_t stream);

@@ -1,5 +1,7 @@
 // s2x_misc.hip -- pointwise epilogues, position-embedding resize, Q8_0
 // get_rows, pooling and packing helpers for gfx950.  All HBM-bound.
+#include <algorithm>
+
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
@@ -44,6 +46,25 @@ hipError_t launch_bias_gelu(const float *mm, const float *bias, float *y, int64_
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(k_bias_gelu, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        stream, mm, bias, y, H, total);
+    return hipGetLastError();
+}
+
+// 16 bytes per thread (grid-stride), then the tail bytes
+__global__ __launch_bounds__(256) void k_fill_zero(uint8_t *__restrict__ p, int64_t n16, int64_t bytes) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        reinterpret_cast<uint4 *>(p)[i] = make_uint4(0, 0, 0, 0);
+    const int64_t t = n16 * 16 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < bytes) p[t] = 0;
+}
+
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return hipSuccess;
+    if (reinterpret_cast<uintptr_t>(p) & 15) return hipErrorInvalidValue;
+    const int64_t n16 = (int64_t)(bytes / 16);
+    const int64_t blocks = std::min<int64_t>((n16 + 255) / 256 + 1, 8192);
+    hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<uint8_t *>(p), n16, (int64_t)bytes);
     return hipGetLastError();
 }
 

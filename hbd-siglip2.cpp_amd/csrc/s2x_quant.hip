@@ -17,24 +17,11 @@ namespace s2x {
 // a1: quantizer.  Semantics: src/cuda/siglip2_custom_mmq.cu:63-76 (d, inv,
 // round-half-even, clamp) plus the Q8_1 sum s = fp16(sum(q) * d).
 // ---------------------------------------------------------------------------
-// Store the four quants of a lane: as int8 (4 bytes) and/or as f16 (8 bytes,
-// exact: |q| <= 128).
-__device__ __forceinline__ void store_q4(int8_t *qs, _Float16 *qh, int64_t off, int q0, int q1,
-                                         int q2, int q3) {
-    if (qs) *reinterpret_cast<uint32_t *>(qs + off) = pack4_i8(q0, q1, q2, q3);
-    if (qh) {
-        const v4h h = {(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};
-        *reinterpret_cast<v4h *>(qh + off) = h;
-    }
-}
-
-// The block's scale words: d | s << 16 in ds [row][KB] and d alone in the
-// transposed plane dT [kb][row].
-__device__ __forceinline__ void store_scales(const Q81Out &o, int64_t row, int64_t kb, int64_t KB,
+// The block's scale word d | s << 16 at ds [row][ld_ds].
+__device__ __forceinline__ void store_scales(const Q81Out &o, int64_t row, int64_t kb, int64_t ld_ds,
                                              float d, int s) {
-    const uint32_t dbits = f32_to_f16_bits(d);
-    if (o.ds) o.ds[row * KB + kb] = dbits | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
-    if (o.dT) o.dT[kb * o.ldT + row] = (uint16_t)dbits;
+    o.ds[row * ld_ds + kb] =
+        (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
 }
 
 __global__ __launch_bounds__(256) void k_quantize_q8_1(
@@ -64,70 +51,66 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;
     const int q0 = q8_round(v0, inv), q1 = q8_round(v1, inv);
     const int q2 = q8_round(v2, inv), q3 = q8_round(v3, inv);
-    store_q4(o.qs, o.qh, m * K_pad + c, q0, q1, q2, q3);
+    *reinterpret_cast<uint32_t *>(o.qs + m * K_pad + c) = pack4_i8(q0, q1, q2, q3);
     const int s = group8_isum(q0 + q1 + q2 + q3);
-    if (sub == 0) store_scales(o, m, kb, KB, d, s);
+    if (sub == 0) store_scales(o, m, kb, o.ld_ds, d, s);
 }
 
 hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
                                 int64_t K_pad, const Q81Out &o, hipStream_t stream) {
     const int64_t groups = M * (K_pad / QK);
     if (groups == 0) return hipSuccess;
+    if (!o.qs || !o.ds) return hipErrorInvalidValue;
     const int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     const int64_t threads = groups * 8;
     const unsigned grid = (unsigned)((threads + 255) / 256);
+    Q81Out oo = o;
+    if (oo.ld_ds == 0) oo.ld_ds = K_pad / QK;
     hipLaunchKernelGGL(k_quantize_q8_1, dim3(grid), dim3(256), 0, stream, x, K, M, ldx,
-                       K_pad, o, vec4);
+                       K_pad, oo, vec4);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // a2: weight repack.  One thread per 34-byte block: the int8 qs go to a
-// 16-byte aligned row-major plane, d widens (exactly) to f32; optionally the
-// same quants as f16 (exact) and d's fp16 bits transposed ([kb][n]) for the
-// f16-MFMA GEMM.
+// 16-byte aligned row-major plane, d's fp16 bits to the transposed plane
+// dT [kb][n] (the GEMM's weight-scale layout).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__ raw,
                                                      int64_t n_blocks, int64_t KB,
                                                      int8_t *__restrict__ qs,
-                                                     float *__restrict__ d,
-                                                     _Float16 *__restrict__ qh,
                                                      uint16_t *__restrict__ dT, int64_t ldT) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_blocks) return;
     const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + i * 34);  // 2-byte aligned
-    d[i] = f16_bits_to_f32(src[0]);
-    if (dT) {
-        const int64_t n = i / KB, kb = i - n * KB;
-        dT[kb * ldT + n] = src[0];
-    }
+    const int64_t n = i / KB, kb = i - n * KB;
+    dT[kb * ldT + n] = src[0];
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = (uint32_t)src[1 + 2 * j] | ((uint32_t)src[2 + 2 * j] << 16);
     uint4 *dst = reinterpret_cast<uint4 *>(qs + i * QK);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-    if (qh) {
-        v8h *hd = reinterpret_cast<v8h *>(qh + i * QK);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            v8h h;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                h[j] = (_Float16)(int8_t)((w[(c * 8 + j) >> 2] >> (8 * ((c * 8 + j) & 3))) & 0xff);
-            hd[c] = h;
-        }
-    }
+}
+
+// the padding columns N .. ldT-1 of every dT row
+__global__ __launch_bounds__(256) void k_zero_pad_cols(uint16_t *__restrict__ dT, int64_t KB,
+                                                        int64_t N, int64_t ldT) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t w = ldT - N;
+    if (i >= KB * w) return;
+    dT[(i / w) * ldT + N + i % w] = 0;
 }
 
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,
-                              float *d, _Float16 *qh, uint16_t *dT, int64_t ldT,
-                              hipStream_t stream) {
-    const int64_t nb = N * (K_pad / QK);
+                              uint16_t *dT, int64_t ldT, hipStream_t stream) {
+    const int64_t KB = K_pad / QK, nb = N * KB;
     if (nb == 0) return hipSuccess;
     hipLaunchKernelGGL(k_repack_q8_0, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
-                       stream, reinterpret_cast<const uint8_t *>(raw), nb, K_pad / QK, qs, d,
-                       qh, dT, ldT);
+                       stream, reinterpret_cast<const uint8_t *>(raw), nb, KB, qs, dT, ldT);
+    if (ldT > N)
+        hipLaunchKernelGGL(k_zero_pad_cols, dim3((unsigned)((KB * (ldT - N) + 255) / 256)),
+                           dim3(256), 0, stream, dT, KB, N, ldT);
     return hipGetLastError();
 }
 
@@ -243,9 +226,9 @@ __global__ __launch_bounds__(256) void k_layernorm(
                 const float inv = a != 0.0f ? 127.0f / a : 0.0f;
                 const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
                 const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
-                store_q4(q.qs, q.qh, row * H + c, q0, q1, q2, q3);
+                *reinterpret_cast<uint32_t *>(q.qs + row * H + c) = pack4_i8(q0, q1, q2, q3);
                 const int sq = group8_isum(q0 + q1 + q2 + q3);
-                if ((lane & 7) == 0) store_scales(q, row, c / QK, H / QK, d, sq);
+                if ((lane & 7) == 0) store_scales(q, row, c / QK, q.ld_ds, d, sq);
             }
         }
 #pragma unroll
@@ -279,7 +262,9 @@ hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
     if (H <= 0 || H % QK != 0 || H > LN_MAXIT * 256 || (!q && !y)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)std::min<int64_t>((M + 3) / 4, LN_MAX_BLOCKS));
     const bool quant = q != nullptr;
-    const Q81Out qo = q ? *q : Q81Out{};
+    Q81Out qo = q ? *q : Q81Out{};
+    if (quant && (!qo.qs || !qo.ds)) return hipErrorInvalidValue;
+    if (quant && qo.ld_ds == 0) qo.ld_ds = H / QK;
     switch ((H + 255) / 256) {
     case 1: launch_ln_nit<1>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;
     case 2: launch_ln_nit<2>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream); break;

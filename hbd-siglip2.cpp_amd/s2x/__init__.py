@@ -13,13 +13,14 @@ import os
 
 __all__ = [
     "S2XError", "lib", "Epilogue", "LayerWeights", "VisionWeights", "TextWeights",
-    "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_BIAS_RESID", "POOL_MEAN", "POOL_PROBE",
+    "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU", "EPI_BIAS_RESID", "EPI_GELU_Q81", "POOL_MEAN",
+    "POOL_PROBE",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "libs2x.so")
 
-EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID = 0, 1, 2, 3
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_GELU_Q81 = 0, 1, 2, 3, 4
 POOL_MEAN, POOL_PROBE = 0, 1
 
 if not os.path.exists(LIB_PATH):
@@ -67,7 +68,7 @@ _fp = ctypes.POINTER(ctypes.c_float)
 
 class Epilogue(ctypes.Structure):
     _fields_ = [("kind", _i32), ("bias", _p), ("resid", _p), ("ld_resid", _i64),
-                ("resid_rows", _i64)]
+                ("resid_rows", _i64), ("q_out", _p), ("q_ds", _p), ("q_kpad", _i64)]
 
 
 class LayerWeights(ctypes.Structure):
@@ -119,6 +120,8 @@ _sig("s2x_mul_mat_q8_0_q8_1", [_p, _p, _p, _i64, _p, _i64, ctypes.POINTER(Epilog
 _sig("s2x_mul_mat_workspace_size", [_i64, _i64, _i64], _sz)
 _sig("s2x_mul_mat_q8_0_f32", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _sz, _p])
 _sig("s2x_block_dots", [_p, _p, _i64, _i64, _p, _p])
+_sig("s2x_mul_mat_qkv_attn_prep", [_p, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz,
+                                   _p])
 _sig("s2x_layernorm", [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p])
 _sig("s2x_layernorm_quantize_q8_1", [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _p, _p, _i64, _p])
 _sig("s2x_bias_residual", [_p, _p, _p, _p, _i64, _i64, _p])
@@ -139,10 +142,7 @@ _sig("s2x_vision_create", [ctypes.POINTER(VisionWeights), ctypes.POINTER(_p)])
 _sig("s2x_vision_destroy", [_p], None)
 _sig("s2x_vision_set_stream", [_p, _p])
 _sig("s2x_vision_set_attention_fp64", [_p, ctypes.c_int])
-_sig("s2x_vision_set_gemm_variant", [_p, ctypes.c_int])
-_sig("s2x_vision_set_lanes", [_p, ctypes.c_int])
 _sig("s2x_vision_encode_rgb_batch_dev", [_p, _p, _p, _i32, _i32, _f32, _p, _p, _i32, _p])
-GEMM_F16_MFMA, GEMM_I8_MFMA = 0, 1
 _sig("s2x_text_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_vision_encode", [_p, _p, _i32, _i32, _i32, _p])
 _sig("s2x_vision_encode_batch_dev", [_p, _p, _i32, _i32, _i32, _i32, _p])

@@ -57,8 +57,8 @@ int s2x_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ldx,
 /* a2  Q8_0 weights, repacked once for the MFMA GEMM                          */
 /* A raw Q8_0 matrix W (K_pad, N) is N rows of K_pad/32 34-byte block_q8_0    */
 /* (fp16 d then int8 qs[32]; bench/microbench_mmq.cpp:322-343).  The repack  */
-/* is lossless: an int8 plane (N rows of K_pad) and an f32 scale plane       */
-/* (N rows of K_pad/32, fp16 values widened exactly).                         */
+/* is lossless: an int8 plane (N rows of K_pad) and the fp16 scales          */
+/* transposed (K_pad/32 rows of N).                                           */
 /* ------------------------------------------------------------------------ */
 typedef struct s2x_weight s2x_weight;
 
@@ -78,19 +78,28 @@ int64_t s2x_weight_n(const s2x_weight *w);
 
 /* ------------------------------------------------------------------------ */
 /* a3  Q8_0 x Q8_1 GEMM on int8 MFMA                                          */
-/* Y[m*N+n] = sum over 32-blocks kb, in order, of                              */
+/* Y[m*ldy+n] = epilogue(acc), acc = sum over 32-blocks kb, in order, of       */
 /*   acc = fmaf((float)I_kb, d_w * d_x, acc),  I_kb = sum q_w*q_x (exact)     */
-/* then the epilogue.                                                          */
 /* Replaces ggml-cuda mul_mat_q<Q8_0> behind GGML_OP_MUL_MAT(Q8_0, F32) and   */
 /* siglip2_custom_mmq::launch_custom_mmq (src/cuda/siglip2_custom_mmq.cuh:    */
 /* 96-103); the epilogues replace the fused tails of                          */
-/* src/cuda/siglip2_megakernel.cuh:117-132.                                   */
+/* src/cuda/siglip2_megakernel.cuh:117-132 (bias + GELU, bias + residual) and */
+/* the GELU output's re-quantization for the next GEMM.                       */
+/* The activation is Q8_1 as s2x_quantize_q8_1 writes it: qs (M rows of K_pad */
+/* int8, 16-byte aligned) and ds (M rows of K_pad/32 (fp16 d, fp16 s)).       */
+/* One kernel serves every entry point below and the encoders.                */
 /* ------------------------------------------------------------------------ */
 typedef enum {
     S2X_EPI_NONE = 0,        /* y = acc                                      */
     S2X_EPI_BIAS = 1,        /* y = acc + bias[n]                            */
     S2X_EPI_BIAS_GELU = 2,   /* y = gelu_tanh(acc + bias[n])                 */
-    S2X_EPI_BIAS_RESID = 3   /* y = (acc + bias[n]) + resid[r(m)*ld_resid+n] */
+    S2X_EPI_BIAS_RESID = 3,  /* y = (acc + bias[n]) + resid[r(m)*ld_resid+n] */
+    S2X_EPI_GELU_Q81 = 4     /* no y: gelu_tanh(acc + bias[n]) quantized to  */
+                             /* Q8_1 over rows of q_kpad values (columns     */
+                             /* N..q_kpad-1 zero): q_out (M rows of q_kpad   */
+                             /* int8, 16-byte aligned) and q_ds (M rows of   */
+                             /* q_kpad/32 words), = s2x_quantize_q8_1 of the */
+                             /* BIAS_GELU output, bit for bit                */
 } s2x_epilogue_kind;
 
 typedef struct {
@@ -99,6 +108,9 @@ typedef struct {
     const float *resid;       /* BIAS_RESID only; may alias y             */
     int64_t      ld_resid;    /* row stride of resid in floats            */
     int64_t      resid_rows;  /* 0: r(m) = m; > 0: r(m) = m % resid_rows  */
+    void        *q_out;       /* GELU_Q81 only                            */
+    void        *q_ds;        /* GELU_Q81 only                            */
+    int64_t      q_kpad;      /* GELU_Q81: N <= q_kpad < N + 32, % 32 == 0 */
 } s2x_epilogue;
 
 int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds,
@@ -116,9 +128,24 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N,
                          void *stream);
 
 /* Debug view of the GEMM's integer stage: out[m*N+n] = I_kb (the exact
- * int32 block dot of block `kb`) from the same MFMA data path. */
+ * int32 block dot of block `kb`) from the same kernel's MFMA data path. */
 int s2x_block_dots(const s2x_weight *w, const void *qs, int64_t M, int64_t kb,
                    int32_t *out, void *stream);
+
+/* QKV projection fused with the attention staging: the Q8_0 x Q8_1 product
+ * with W_qkv (N = 3*n_head*d_head, rows [q;k;v]) plus qkv_bias, rounded to
+ * f16 and written straight into the staging workspace `ws` in the layout
+ * s2x_attn_prep produces (ws of s2x_attn_workspace_size() bytes).  Equals
+ * s2x_mul_mat_q8_0_q8_1 followed by s2x_attn_prep, bit for bit; replaces
+ * that pair and the reference's launch_fused_qkv_prep
+ * (src/cuda/siglip2_megakernel.cuh:75-100) after its MUL_MAT.  Rows of the
+ * GEMM are the packed segment rows (M = sum of seg_len).  The padding slots
+ * of ws are cleared first. */
+int s2x_mul_mat_qkv_attn_prep(const s2x_weight *w, const void *qs, const void *ds,
+                              int64_t M, const float *qkv_bias,
+                              const int32_t *seg_start_dev, const int32_t *seg_len_dev,
+                              int64_t n_seg, int64_t max_len, int64_t n_head,
+                              int64_t d_head, void *ws, size_t ws_bytes, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* a4  LayerNorm(+affine), alone and fused with the Q8_1 quantizer           */
@@ -311,20 +338,6 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream);
 /* Attention precision: 0 (default) = f16-MFMA flash attention with f32
  * softmax and an exact f16 hi/lo split of P; 1 = s2x_attn_fp64. */
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
-/* GEMM kernel of the towers: S2X_GEMM_I8_MFMA (default; int8 quants,
- * v_mfma_i32_32x32x32_i8 block dots, the dx*dw scale tile on an f16 MFMA,
- * one VALU convert + fma per element and block) or S2X_GEMM_F16_MFMA (the
- * same kernel over f16-coded quants: block dots on two f16 MFMAs, one VALU
- * fma).  Both give the same bits. */
-enum { S2X_GEMM_F16_MFMA = 0, S2X_GEMM_I8_MFMA = 1 };
-int s2x_vision_set_gemm_variant(s2x_vision *v, int variant);
-/* Concurrency of a batch (f16 GEMM + flash attention path): the encoder
- * blocks run as n (1..4, default 1) independent row ranges of whole images
- * on streams of their own, forked from and joined back into the encoder's
- * stream.  Results do not depend on n.  No counterpart in the reference
- * (its CPU path runs one image at a time). */
-int s2x_vision_set_lanes(s2x_vision *v, int n);
-
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */
 int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h,

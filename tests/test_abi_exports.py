@@ -41,7 +41,7 @@ def test_host_only_entry_points():
     import s2x
     assert s2x.version().startswith("s2x")
     assert s2x.lib.s2x_status_string(0) == b"ok"
-    assert s2x.lib.s2x_weight_bytes(1152, 3456) >= 1152 * 3456 + 36 * 3456 * 4
+    assert s2x.lib.s2x_weight_bytes(1152, 3456) >= 1152 * 3456 + 36 * 3456 * 2
     assert s2x.lib.s2x_weight_bytes(33, 1) == 0  # K not a multiple of 32
     ws = s2x.lib.s2x_mul_mat_workspace_size(4320, 1152, 729)
     assert ws >= 4320 * 1152 + 729 * 4320 + 729 * 135 * 4

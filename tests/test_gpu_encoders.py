@@ -126,42 +126,6 @@ def test_small_vision_rgb_batch_equals_preprocessed(small_vision, pooling):
     assert np.array_equal(host(out), want)
 
 
-def test_small_vision_gemm_variants_same_bits(small_vision):
-    # the int8-quant and f16-quant GEMMs compute the same per-block integers
-    # and the same fma chain, so the whole tower must agree bit for bit
-    v, _ = small_vision
-    px = synth.pixels(2, 27 * 27, seed=77)
-    outs = []
-    for variant in (s2x.GEMM_F16_MFMA, s2x.GEMM_I8_MFMA):
-        s2x.call("s2x_vision_set_gemm_variant", v.h, variant)
-        outs.append(v.batch(px, 2, 27, 27, s2x.POOL_PROBE))
-    assert np.array_equal(outs[0], outs[1])
-    assert s2x.lib.s2x_vision_set_gemm_variant(v.h, 7) == 1
-
-
-def test_small_vision_lanes_same_bits(small_vision):
-    # the blocks of a batch split into 1..4 row ranges of whole images on
-    # streams of their own: every lane count, with either GEMM format, must
-    # give the bits of the single-lane run
-    v, _ = small_vision
-    n_img = 6
-    px = synth.pixels(n_img, 16 * 16, seed=78)
-    s2x.call("s2x_vision_set_lanes", v.h, 1)
-    ref = v.batch(px, n_img, 16, 16, s2x.POOL_PROBE)
-    try:
-        for variant in (s2x.GEMM_F16_MFMA, s2x.GEMM_I8_MFMA):
-            s2x.call("s2x_vision_set_gemm_variant", v.h, variant)
-            for lanes in (1, 2, 3, 4):
-                s2x.call("s2x_vision_set_lanes", v.h, lanes)
-                got = v.batch(px, n_img, 16, 16, s2x.POOL_PROBE)
-                assert np.array_equal(got, ref), (variant, lanes)
-    finally:
-        s2x.call("s2x_vision_set_lanes", v.h, 1)
-        s2x.call("s2x_vision_set_gemm_variant", v.h, s2x.GEMM_I8_MFMA)
-    assert s2x.lib.s2x_vision_set_lanes(v.h, 0) == 1
-    assert s2x.lib.s2x_vision_set_lanes(v.h, 5) == 1
-
-
 def test_vision_rejects_bad_shapes(small_vision):
     v, _ = small_vision
     px = np.zeros((4, 768), np.float32)
