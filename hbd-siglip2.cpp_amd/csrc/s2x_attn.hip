@@ -166,6 +166,7 @@ constexpr int FA_VP = FA_KT + 8;       // V^T tile pitch (halves): 16-byte rows,
 constexpr int FA_ONES = 88;            // V^T padding row held at 1.0: O^T row 88 = sum of P
 constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
 constexpr int FA_WAVES = 12;  // waves (32 queries each) per workgroup
+constexpr float P_SHIFT = 15.0f;  // log2 of the largest P of a row (<= 65504 as f16)
 
 template <bool P_SPLIT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attn(
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
     for (int j = 0; j < 3; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
-    float m_run = -INFINITY;
+    float m_run = -INFINITY, mc_run = -INFINITY;
 
     const int n_tiles = (len + FA_KT - 1) / FA_KT;
 
@@ -325,10 +326,18 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
 #pragma unroll
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[sub][r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32));
+        // P = 2^(s scale_log2 - mc) with mc = m scale_log2 - P_SHIFT: the
+        // largest P of a row is 2^P_SHIFT, not 1, so that the f16 pair below
+        // keeps ~22 significant bits for P down to 2^-13 of the row maximum
+        // (unshifted, the lo half turns f16-subnormal below 2^-4 and its
+        // truncation biases every small P downward).  O and its P sum carry
+        // the same factor, which cancels in O / sum.  alpha compares the two
+        // exponent offsets actually used, so no rounding of mc enters it.
         const float m_new = fmaxf(m_run, mt);  // in raw score units (scale > 0)
-        const float mc = m_new == -INFINITY ? 0.0f : m_new * scale_log2;
-        const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
+        const float mc = m_new == -INFINITY ? 0.0f : fmaf(m_new, scale_log2, -P_SHIFT);
+        const float alpha = __builtin_amdgcn_exp2f(mc_run - mc);  // 0 before the first key
         m_run = m_new;
+        mc_run = m_new == -INFINITY ? -INFINITY : mc;
         // alpha is exactly 1 where the running max did not move: skip the
         // rescale when that holds for the whole wave (the common case once
         // the first tiles have set the max)

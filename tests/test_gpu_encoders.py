@@ -242,6 +242,61 @@ def test_so400m_vision_naflex_vs_oracle(orc, so400m_vision):
 
 
 @pytest.mark.timeout(600)
+def test_so400m_vision_batch32_workload(orc, so400m_vision):
+    """32 images x 729 patches (GEMM M = 23,328), the throughput workload:
+    each image's embedding equals that image encoded alone, bit for bit, and
+    the first and last match the oracle."""
+    v, om = so400m_vision
+    n = 32
+    px = synth.pixels(n, 729, seed=4000)
+    say("so400m vision 32 x 729")
+    b = v.batch(px, n, 27, 27, s2x.POOL_PROBE)
+    for i in (0, 13, 31):
+        one = v.batch(px[i * 729:(i + 1) * 729], 1, 27, 27, s2x.POOL_PROBE)
+        assert np.array_equal(b[i], one[0]), f"image {i}"
+    for i in (0, 31):
+        r = orc.vision_encode(om, px[i * 729:(i + 1) * 729], 27, 27, pooling=1)
+        c = cos(b[i], r)
+        say(f"  image {i}: cosine {c:.7f}")
+        assert c >= 0.9999
+
+
+NAFLEX_GRIDS = {256: [(16, 16), (8, 32), (32, 8)], 576: [(24, 24), (16, 36), (36, 16), (18, 32)],
+                729: [(27, 27)], 1024: [(32, 32), (16, 64), (64, 16)]}
+
+
+@pytest.mark.timeout(600)
+def test_so400m_vision_naflex16_workload(orc, so400m_vision):
+    """NaFlex ragged batch: 16 images, 4 each of 256, 576, 729 and 1024
+    patches in seeded order, grids of several aspect ratios, padded to 1024
+    patches.  Each embedding equals the image encoded alone, bit for bit;
+    the widest and a 256-patch image match the oracle."""
+    v, om = so400m_vision
+    rng = np.random.default_rng(5000)
+    counts = rng.permutation([256, 576, 729, 1024] * 4)
+    shapes = [NAFLEX_GRIDS[c][rng.integers(len(NAFLEX_GRIDS[c]))] for c in counts]
+    say(f"so400m vision NaFlex 16: {shapes}")
+    padded = np.zeros((16, 1024, 768), np.float32)
+    pix = []
+    for i, (h, w) in enumerate(shapes):
+        p = synth.pixels(1, h * w, seed=5100 + i)
+        padded[i, :h * w] = p
+        pix.append(p)
+    out = v.ragged(padded.reshape(-1, 768), shapes, 1024, s2x.POOL_PROBE)
+    for i, (h, w) in enumerate(shapes):
+        one = v.batch(pix[i], 1, h, w, s2x.POOL_PROBE)[0]
+        assert np.array_equal(out[i], one), f"image {i} ({h}x{w})"
+    wide = [i for i, s in enumerate(shapes) if s[0] != s[1] and s[0] * s[1] == 1024]
+    small = [i for i, s in enumerate(shapes) if s[0] * s[1] == 256]
+    for i in (wide + [int(np.argmax(counts))])[:1] + small[:1]:
+        h, w = shapes[i]
+        r = orc.vision_encode(om, pix[i], h, w, pooling=1)
+        c = cos(out[i], r)
+        say(f"  image {i} ({h}x{w}): cosine {c:.7f}")
+        assert c >= 0.9999
+
+
+@pytest.mark.timeout(600)
 def test_so400m_text_5x64_vs_oracle(orc):
     say("generating so400m text weights")
     hm = synth.text_model(synth.SO400M_TEXT, seed=0)

@@ -346,7 +346,9 @@ def _attn_case(orc, lens, n_head=16, dh=72, key_valid=None, seed=10):
 def test_attention_segments(orc):
     e = _attn_case(orc, [729, 1, 64, 130, 255, 128])
     say(f"attention max err / max|out| = {e:.2e}")
-    assert e < 4e-3
+    # Q, K, V rounded to f16 on both sides; the scores, the softmax and the
+    # f16 hi+lo probability pair keep the rest near f32 (measured 7.3e-7)
+    assert e < 1e-5
 
 
 def test_attention_key_mask(orc):
@@ -354,7 +356,7 @@ def test_attention_key_mask(orc):
     kv = np.ones(264, np.uint8)
     kv[40:64] = 0
     kv[64 + 150:] = 0
-    assert _attn_case(orc, lens, key_valid=kv, seed=11) < 4e-3
+    assert _attn_case(orc, lens, key_valid=kv, seed=11) < 1e-5
 
 
 @pytest.mark.parametrize("masked", [False, True])
