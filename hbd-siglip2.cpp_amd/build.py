@@ -25,6 +25,7 @@ SOURCES = [
     "s2x_attn.hip",
     "s2x_misc.hip",
     "s2x_naflex.hip",
+    "s2x_static.hip",
     "s2x_abi.cpp",
     "s2x_encoders.cpp",
     "s2x_gguf.cpp",

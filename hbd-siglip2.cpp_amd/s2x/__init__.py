@@ -119,6 +119,7 @@ _sig("s2x_weight_n", [_p], _i64)
 _sig("s2x_mul_mat_q8_0_q8_1", [_p, _p, _p, _i64, _p, _i64, ctypes.POINTER(Epilogue), _p])
 _sig("s2x_mul_mat_workspace_size", [_i64, _i64, _i64], _sz)
 _sig("s2x_mul_mat_q8_0_f32", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _sz, _p])
+_sig("s2x_mul_mat_q8_0_f32_static", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p])
 _sig("s2x_block_dots", [_p, _p, _i64, _i64, _p, _p])
 _sig("s2x_mul_mat_qkv_attn_prep", [_p, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz,
                                    _p])

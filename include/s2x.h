@@ -8,7 +8,9 @@
  * from s2x_last_error() on the calling thread.  Launch functions are
  * asynchronous on `stream`; they neither allocate nor synchronise unless
  * stated.  The library keeps no global mutable state besides the per-thread
- * error message, so concurrent calls on different streams are safe.
+ * error message and the scratch array of s2x_mul_mat_q8_0_f32_static, so
+ * concurrent calls on different streams are safe, except calls of that one
+ * entry point on the same GPU.
  *
  * Layouts use the reference's ggml order (innermost first): an activation
  * X (K, M) is M rows of K floats (row stride ldx floats), a GEMM output
@@ -126,6 +128,22 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N,
                          const float *x, int64_t K, int64_t ldx, int64_t M,
                          float *y, void *workspace, size_t ws_bytes,
                          void *stream);
+
+/* Allocation-free variant of s2x_mul_mat_q8_0_f32: same arguments without
+ * the workspace, same results bit for bit.  No counterpart in the reference;
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * workspace is a static device array of S2X_STATIC_SCRATCH_BYTES that each
+ * GPU the library runs on holds until the process ends.  A shape whose
+ * s2x_mul_mat_workspace_size() exceeds it returns S2X_ERR_UNSUPPORTED before
+ * any launch (64 MiB: the so400m fc2 shape, K_pad 4320 x N 1152, up to
+ * M = 12,720 rows, the K = 1152 shapes up to M = 47,713).  Every call on a
+ * GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+#define S2X_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int s2x_mul_mat_q8_0_f32_static(const void *w_raw, int64_t K_pad, int64_t N,
+                                const float *x, int64_t K, int64_t ldx,
+                                int64_t M, float *y, void *stream);
 
 /* Debug view of the GEMM's integer stage: out[m*N+n] = I_kb (the exact
  * int32 block dot of block `kb`) from the same kernel's MFMA data path. */
