@@ -2,15 +2,20 @@
 patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
-                    [--cpu-images 3] [--no-cpu]
+                    [--cpu-images 3] [--cpu-threads T] [--no-cpu] [--no-extra]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
 Q8_0 x Q8_1 MFMA GEMM): algorithmic int8 ops (2*M*N*K_logical, padding not
 counted) over the GEMM launch durations measured with HIP events on the
 encoder's stream during the timed steps, against MI355X's dense int8 peak.
-`cpu_baseline` times the CPU oracle (this repository's C restatement of
-ggml's CPU Q8_0 path) on a bounded sample of the same workload.
+The same line carries the other workloads of the path as extra keys:
+`batch1` (one 729-patch image per encode: latency and the GEMM rate at
+M = 729), `gemm_shapes` (the four vision-layer GEMMs alone at M = 729 and
+M = 23,328: quantize + GEMM per iteration, p50 of HIP-event times) and
+`text_5x64` (the text tower, 5 prompts x 64 tokens).  `cpu_baseline` times
+the CPU oracle (this repository's C restatement of ggml's CPU Q8_0 path) on
+a bounded sample of the tower and on the four GEMMs at 1 and T threads.
 """
 import argparse
 import ctypes
@@ -20,13 +25,18 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
+# OpenMP threads of the CPU baseline one per core (set before any OpenMP
+# runtime starts)
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
 sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
-KERNEL = ("k_gemm (Q8_0 x Q8_1 GEMM, persistent 256x128 tiles: int8 quants and scales by LDS DMA, "
-          "v_mfma_i32_32x32x32_i8 block dots, dx*dw scale tile on v_mfma_f32_32x32x8_f16, one "
-          "convert + fma per element and block; priced against the int8 peak)")
+KERNEL = ("k_gemm (Q8_0 x Q8_1 GEMM, 128x128 tiles of 8 waves, two workgroups per CU: int8 "
+          "quants and scales by LDS DMA in 4-block stages, v_mfma_i32_32x32x32_i8 block dots, "
+          "dx*dw scale tile on v_mfma_f32_32x32x8_f16, one convert + fma per element and block; "
+          "priced against the int8 peak)")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_vision_b32_traffic.json")
 
 
@@ -44,14 +54,38 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def pct(v, p):
+    v = sorted(v)
+    return v[min(len(v) - 1, int(round((len(v) - 1) * p)))]
+
+
+GEMM_SHAPES = [("qkv", 3456, 1152, 1152), ("out", 1152, 1152, 1152), ("fc1", 4304, 1152, 1152),
+               ("fc2", 1152, 4304, 4320)]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=150)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--cpu-images", type=int, default=3)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (default: OMP_NUM_THREADS or all cores)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the headline: skip the batch-1, per-shape GEMM and text lines")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (a plain copy kernel "
                          "for calibrating HBM byte counters) and exit")
@@ -92,19 +126,24 @@ def main():
     hm = synth.vision_model(cfg, seed=0)
     v = ctypes.c_void_p()
     s2x.call("s2x_vision_create", ctypes.byref(hm.struct), ctypes.byref(v))
-    stream = torch.cuda.ExternalStream  # noqa: F841 (the encoder owns its stream)
     px = synth.pixels(B, n_pos, seed=1234)
     pd = torch.from_numpy(px).to("cuda:0")
     out = torch.empty((B, cfg.hidden), dtype=torch.float32, device="cuda:0")
 
-    def step():
-        s2x.call("s2x_vision_encode_batch_dev", v, ctypes.c_void_p(pd.data_ptr()), B, gh, gw,
+    def step(n_img=B):
+        s2x.call("s2x_vision_encode_batch_dev", v, ctypes.c_void_p(pd.data_ptr()), n_img, gh, gw,
                  s2x.POOL_PROBE, ctypes.c_void_p(out.data_ptr()))
 
     def sync():
         # the encoder's stream: a zero-length stats query synchronises it
         s2x.call("s2x_vision_gemm_stats", v, None, None, None, 0)
         torch.cuda.synchronize()
+
+    def gemm_stats():
+        ms, ops, launches = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        s2x.call("s2x_vision_gemm_stats", v, ctypes.byref(ms), ctypes.byref(ops),
+                 ctypes.byref(launches), 1)
+        return ms.value, ops.value, launches.value
 
     log("bench: warmup")
     for _ in range(args.warmup):
@@ -119,40 +158,31 @@ def main():
         step()
     sync()
     t1 = time.perf_counter()
-    ms = ctypes.c_double()
-    ops = ctypes.c_double()
-    launches = ctypes.c_int64()
-    s2x.call("s2x_vision_gemm_stats", v, ctypes.byref(ms), ctypes.byref(ops),
-             ctypes.byref(launches), 1)
+    g_ms, g_ops, g_launches = gemm_stats()
     s2x.call("s2x_vision_gemm_timing", v, 0)
     emb = out.cpu().numpy()
     assert np.isfinite(emb).all()
-    s2x.lib.s2x_vision_destroy(v)
 
     ms_step = (t1 - t0) * 1000.0 / args.steps
     ips = B / (ms_step / 1000.0)
-    gemm_tops = ops.value / (ms.value / 1000.0) / 1e12
-    avg_launch_ms = ms.value / max(1, launches.value)
-    log(f"bench: {ms_step:.2f} ms/step, {ips:.1f} images/s, GEMM {gemm_tops:.1f} TOPS over "
-        f"{launches.value} launches (avg {avg_launch_ms * 1000:.1f} us), "
-        f"GEMM share of step {ms.value / args.steps / ms_step * 100:.1f}%")
+    gemm_tops = g_ops / (g_ms / 1000.0) / 1e12
+    avg_launch_ms = g_ms / max(1, g_launches)
+    log(f"bench: {ms_step:.2f} ms/step ({t1 - t0:.2f} s timed), {ips:.1f} images/s, GEMM "
+        f"{gemm_tops:.1f} TOPS over {g_launches} launches (avg {avg_launch_ms * 1000:.1f} us), "
+        f"GEMM share of step {g_ms / args.steps / ms_step * 100:.1f}%")
+
+    extra = {}
+    if not args.no_extra:
+        extra["batch1"] = bench_batch1(step, sync, gemm_stats, v, s2x, np)
+        s2x.lib.s2x_vision_destroy(v)
+        extra["gemm_shapes"] = bench_gemm_shapes(np, torch, s2x, synth)
+        extra["text_5x64"] = bench_text(np, s2x, synth)
+    else:
+        s2x.lib.s2x_vision_destroy(v)
 
     cpu = None
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import pyoracle
-        om = pyoracle.vision_model(hm)
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        log(f"bench: CPU baseline (oracle, {threads} threads, {args.cpu_images} image(s))")
-        c0 = time.perf_counter()
-        for i in range(args.cpu_images):
-            pyoracle.vision_encode(om, px[i * n_pos:(i + 1) * n_pos], gh, gw, pooling=1,
-                                   nthreads=threads)
-        c1 = time.perf_counter()
-        cpu = {"value": round(args.cpu_images / (c1 - c0), 4), "unit": "images/s",
-               "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_images} image(s) of the same 27x27 so400m probe-pooled "
-                         f"workload, batch 1, {c1 - c0:.1f} s"}
+        cpu = cpu_baseline(args, hm, px, n_pos, gh, gw)
 
     rec = {
         "metric": METRIC,
@@ -176,10 +206,167 @@ def main():
                      "traffic": traffic_per_launch(),
                      "kernel": KERNEL,
                      "avg_launch_ms": round(avg_launch_ms, 4),
-                     "launches": int(launches.value)},
+                     "launches": int(g_launches)},
         "cpu_baseline": cpu,
     }
+    rec.update(extra)
     print(json.dumps(rec), flush=True)
+
+
+def bench_batch1(step, sync, gemm_stats, v, s2x, np, iters=60):
+    """Config 1: one 27x27 image per encode, pixels resident in HBM; wall
+    time of each synchronised encode, and the GEMM rate at M = 729."""
+    for _ in range(5):
+        step(1)
+    sync()
+    gemm_stats()
+    s2x.call("s2x_vision_gemm_timing", v, 1)
+    lat = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        step(1)
+        sync()
+        lat.append((time.perf_counter() - t0) * 1000.0)
+    g_ms, g_ops, g_launches = gemm_stats()
+    s2x.call("s2x_vision_gemm_timing", v, 0)
+    tops = g_ops / (g_ms / 1000.0) / 1e12
+    p50 = pct(lat, 0.5)
+    log(f"bench: batch 1: p50 {p50:.3f} ms, p99 {pct(lat, 0.99):.3f} ms, GEMM {tops:.1f} TOPS "
+        f"at M = 729 ({g_ms / iters:.3f} ms of GEMM per image)")
+    return {"workload": "SigLIP2-so400m vision tower, 1 image x 729 patches, probe pooling",
+            "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
+            "ms_min": round(min(lat), 3), "images_per_s": round(1000.0 / p50, 1),
+            "iters": iters, "gemm_tops": round(tops, 1),
+            "gemm_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "gemm_ms_per_image": round(g_ms / iters, 3)}
+
+
+def bench_gemm_shapes(np, torch, s2x, synth, warm=20, iters=200):
+    """Config 2: the four vision-layer GEMMs on their own, Q8_0 W (prepared
+    once) x F32 X ~ N(0, 1): each iteration quantizes X to Q8_1 and runs the
+    GEMM (one GGML_OP_MUL_MAT), timed per iteration with HIP events on the
+    stream both run on; at M = 729 and at the batch-32 row count."""
+    st = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(st.cuda_stream)
+    res = {}
+    for M in (729, 23328):
+        for lab, N, K, Kp in GEMM_SHAPES:
+            rng = np.random.default_rng(N * 7 + K)
+            raw = synth.quantize_q8_0(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02), Kp)
+            w = ctypes.c_void_p()
+            s2x.call("s2x_weight_create", raw.ctypes.data, 1, Kp, N, None, ctypes.byref(w))
+            x = torch.randn(M, K, device="cuda:0")
+            qs = torch.empty((M, Kp), dtype=torch.int8, device="cuda:0")
+            ds = torch.empty((M, Kp // 32), dtype=torch.int32, device="cuda:0")
+            y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+            a = [ctypes.c_void_p(t.data_ptr()) for t in (x, qs, ds, y)]
+
+            def quant():
+                s2x.call("s2x_quantize_q8_1", a[0], K, M, K, Kp, a[1], a[2], sp)
+
+            def gemm():
+                s2x.call("s2x_mul_mat_q8_0_q8_1", w, a[1], a[2], M, a[3], N, None, sp)
+
+            n_it = iters if M <= 729 else iters // 4
+            for _ in range(warm):
+                quant()
+                gemm()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+                   torch.cuda.Event(enable_timing=True)) for _ in range(n_it)]
+            torch.cuda.synchronize()
+            for e0, e1, e2 in ev:
+                e0.record(st)
+                quant()
+                e1.record(st)
+                gemm()
+                e2.record(st)
+            torch.cuda.synchronize()
+            q_us = [e0.elapsed_time(e1) * 1000.0 for e0, e1, _ in ev]
+            g_us = [e1.elapsed_time(e2) * 1000.0 for _, e1, e2 in ev]
+            s2x.lib.s2x_weight_destroy(w)
+            ops = 2.0 * M * N * K
+            g50, q50 = pct(g_us, 0.5), pct(q_us, 0.5)
+            tops = ops / (g50 * 1e-6) / 1e12
+            res[f"{lab}_m{M}"] = {"M": M, "N": N, "K": K, "gemm_us_p50": round(g50, 2),
+                                  "quantize_us_p50": round(q50, 2),
+                                  "mul_mat_us_p50": round(g50 + q50, 2),
+                                  "gemm_tops": round(tops, 1),
+                                  "frac": round(tops / INT8_PEAK_TOPS, 4), "iters": n_it}
+            log(f"bench: GEMM {lab} M={M}: {g50:.1f} us ({tops:.1f} TOPS, frac "
+                f"{tops / INT8_PEAK_TOPS:.3f}) + quantize {q50:.1f} us")
+    return res
+
+
+def bench_text(np, s2x, synth, warm=3, iters=20):
+    """Config 3: so400m text tower, 5 prompts x 64 tokens (EOS-padded
+    tails), host ids in, host embeddings out (the reference's encode_batch
+    contract, synchronous)."""
+    log("bench: generating so400m text weights (seeded)")
+    hm = synth.text_model(synth.SO400M_TEXT, seed=0)
+    t = ctypes.c_void_p()
+    s2x.call("s2x_text_create", ctypes.byref(hm.struct), ctypes.byref(t))
+    ids, _ = synth.text_tokens(5, 64)
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.empty((5, synth.SO400M_TEXT.proj), np.float32)
+
+    def enc():
+        s2x.call("s2x_text_encode_batch", t, ids.ctypes.data, 64, 5, out.ctypes.data)
+
+    for _ in range(warm):
+        enc()
+    lat = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        enc()
+        lat.append((time.perf_counter() - t0) * 1000.0)
+    s2x.lib.s2x_text_destroy(t)
+    assert np.isfinite(out).all()
+    p50 = pct(lat, 0.5)
+    log(f"bench: text 5 x 64: p50 {p50:.3f} ms")
+    return {"workload": "SigLIP2-so400m text tower, 5 prompts x 64 tokens, last-token pooling "
+                        "+ head, host ids in / host embeddings out",
+            "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
+            "ms_min": round(min(lat), 3), "iters": iters}
+
+
+def cpu_baseline(args, hm, px, n_pos, gh, gw):
+    """The oracle (this repository's C restatement of the reference's CPU
+    Q8_0 path, OpenMP, AVX2 auto-vectorised) on the host cores: a bounded
+    sample of the batch-1 tower at the stated thread count, and the four
+    config-2 GEMMs (quantize + GEMM) at M = 729 on 1 thread and on all."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    from s2x import synth
+    threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    om = pyoracle.vision_model(hm)
+    log(f"bench: CPU baseline (oracle, {threads} threads, {args.cpu_images} image(s))")
+    c0 = time.perf_counter()
+    for i in range(args.cpu_images):
+        pyoracle.vision_encode(om, px[i * n_pos:(i + 1) * n_pos], gh, gw, pooling=1,
+                               nthreads=threads)
+    c1 = time.perf_counter()
+    gemms = {}
+    for lab, N, K, Kp in GEMM_SHAPES:
+        rng = np.random.default_rng(N * 7 + K)
+        raw = synth.quantize_q8_0(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02), Kp)
+        x = np.random.default_rng(5).standard_normal((729, K), dtype=np.float32)
+        for nt in (1, threads):
+            g0 = time.perf_counter()
+            pyoracle.mul_mat_q8_0_f32(raw, Kp, N, x, nthreads=nt)
+            dt = time.perf_counter() - g0
+            gemms[f"{lab}_m729_t{nt}"] = {"ms": round(dt * 1000.0, 1),
+                                          "tops": round(2.0 * 729 * N * K / dt / 1e12, 4)}
+    ips = args.cpu_images / (c1 - c0)
+    log(f"bench: CPU tower {ips:.3f} images/s at {threads} threads; GEMMs {gemms}")
+    return {"value": round(ips, 4), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "pinning": f"OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')} "
+                       f"OMP_PLACES={os.environ.get('OMP_PLACES')}",
+            "sample": f"{args.cpu_images} image(s) of the same 27x27 so400m probe-pooled "
+                      f"workload, batch 1, {c1 - c0:.1f} s; config-2 GEMMs (quantize + GEMM) "
+                      f"at M = 729 on 1 and {threads} threads",
+            "gemm_shapes": gemms}
 
 
 def bench_preproc(args, np, torch, s2x):

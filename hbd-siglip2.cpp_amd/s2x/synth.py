@@ -10,6 +10,8 @@ Every tensor draws from its own numpy Generator seeded with (seed, index),
 so a tensor's bytes do not depend on which other tensors were generated.
 """
 import ctypes
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -56,16 +58,8 @@ SO400M_VISION = VisionConfig()
 SO400M_TEXT = TextConfig()
 
 
-def quantize_q8_0(w, k_pad=None):
-    """Rows of w (n, k) float32 -> raw Q8_0 bytes (n, k_pad/32 * 34), uint8.
-
-    ggml quantize_row_q8_0_ref: amax over the block, d = amax/127 (f32),
-    id = 1/d (0 if d == 0), q = roundf(x * id) (half away from zero),
-    d stored as fp16 (round to nearest even)."""
-    w = np.ascontiguousarray(w, dtype=np.float32)
+def _quantize_rows(w, k_pad):
     n, k = w.shape
-    k_pad = k if k_pad is None else k_pad
-    assert k_pad % QK == 0 and k_pad >= k
     if k_pad != k:
         w = np.concatenate([w, np.zeros((n, k_pad - k), np.float32)], axis=1)
     b = w.reshape(n, k_pad // QK, QK)
@@ -73,12 +67,39 @@ def quantize_q8_0(w, k_pad=None):
     d = (amax / np.float32(127.0)).astype(np.float32)
     with np.errstate(divide="ignore"):
         idv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
-    v = (b * idv[:, :, None]).astype(np.float32).astype(np.float64)
-    q = np.trunc(v + np.copysign(0.5, v)).astype(np.int8)
+    v = b * idv[:, :, None]  # f32 products, as x * id in the C reference
+    # roundf: half away from zero (v - trunc(v) is exact in f32)
+    t = np.trunc(v)
+    q = np.where(np.abs(v - t) >= np.float32(0.5), t + np.sign(v), t).astype(np.int8)
     out = np.empty((n, k_pad // QK, 34), np.uint8)
     out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, k_pad // QK, 2)
     out[:, :, 2:] = q.view(np.uint8)
     return out.reshape(n, -1)
+
+
+def quantize_q8_0(w, k_pad=None):
+    """Rows of w (n, k) float32 -> raw Q8_0 bytes (n, k_pad/32 * 34), uint8.
+
+    ggml quantize_row_q8_0_ref: amax over the block, d = amax/127 (f32),
+    id = 1/d (0 if d == 0), q = roundf(x * id) (half away from zero),
+    d stored as fp16 (round to nearest even).  Rows are done in chunks on a
+    few threads (numpy releases the GIL in these loops)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    k_pad = k if k_pad is None else k_pad
+    assert k_pad % QK == 0 and k_pad >= k
+    out = np.empty((n, k_pad // QK * 34), np.uint8)
+    step = 4096
+
+    def job(r0):
+        out[r0:r0 + step] = _quantize_rows(w[r0:r0 + step], k_pad)
+
+    if n <= step:
+        job(0)
+    else:
+        with ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:
+            list(ex.map(job, range(0, n, step)))
+    return out
 
 
 def _rng(seed, idx):
@@ -135,6 +156,13 @@ def _layer(seed, base, H, F, F_pad):
     }
 
 
+def _layers(seed, n_layer, H, F, F_pad):
+    """Every layer's tensors (each from its own seeded streams, so the
+    values do not depend on the order the threads run in)."""
+    with ThreadPoolExecutor(min(4, os.cpu_count() or 1)) as ex:
+        return list(ex.map(lambda l: _layer(seed, 1000 + 100 * l, H, F, F_pad), range(n_layer)))
+
+
 def vision_model(cfg=SO400M_VISION, seed=0):
     """Seeded vision tower weights; .struct is an s2x.VisionWeights."""
     from . import LayerWeights, VisionWeights
@@ -161,8 +189,7 @@ def vision_model(cfg=SO400M_VISION, seed=0):
     t["hup_b"] = _normal(seed, 18, (F,), 0.02)
     t["hdown_w"] = _linear(seed, 19, F, H, Fp)
     t["hdown_b"] = _normal(seed, 20, (H,), 0.02)
-    for l in range(cfg.n_layer):
-        m.layers.append(_layer(seed, 1000 + 100 * l, H, F, Fp))
+    m.layers = _layers(seed, cfg.n_layer, H, F, Fp)
     larr = (LayerWeights * max(1, cfg.n_layer))()
     for l, L in enumerate(m.layers):
         for k in LAYER_KEYS:
@@ -190,8 +217,7 @@ def text_model(cfg=SO400M_TEXT, seed=0):
     t["final_ln_b"] = _normal(seed, 4, (H,), 0.02)
     t["head_w"] = _linear(seed, 5, H, cfg.proj)
     t["head_b"] = _normal(seed, 6, (cfg.proj,), 0.02)
-    for l in range(cfg.n_layer):
-        m.layers.append(_layer(seed, 1000 + 100 * l, H, F, Fp))
+    m.layers = _layers(seed, cfg.n_layer, H, F, Fp)
     larr = (LayerWeights * max(1, cfg.n_layer))()
     for l, L in enumerate(m.layers):
         for k in LAYER_KEYS:
