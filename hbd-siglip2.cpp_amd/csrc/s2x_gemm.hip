@@ -7,13 +7,17 @@
 // I_kb is the exact int32 dot of the 32 quants of block kb; dw and dx are the
 // fp16 block scales (src/cuda/siglip2_custom_mmq.cu:259-267 is the same
 // per-block rescale).  Per 32 x 32 output subtile and K block:
-//   * I   = one v_mfma_i32_32x32x32_i8 (exact);
+//   * I   = one v_mfma_i32_32x32x32_i8 (exact) accumulating onto the bits of
+//           the float 1.5 * 2^23, then one v_mfma_f32_32x32x8_f16 that
+//           subtracts 1.5 * 2^23 (-2048 x 6144 in k-slot 0): (float)I,
+//           exactly, without a VALU convert;
 //   * s   = dx[i] * dw[j] as one v_mfma_f32_32x32x8_f16 whose A holds dx in
 //           k-slot 0 and B holds dw in k-slot 0, every other slot zero: each
 //           output is one exact f16 x f16 product in f32;
-//   * acc = fmaf((float)I, s, acc) on the VALU (convert + fma).
-// The VALU part (32 instructions per subtile and block, 128 SIMD cycles) is
-// the arithmetic bound of this formulation: a quarter of the int8 MFMA peak.
+//   * acc = fmaf(I, s, acc) on the VALU.
+// Three MFMAs (96 matrix-pipe cycles) against 16 VALU instructions (64
+// cycles): the matrix pipe bounds this formulation at a third of the int8
+// MFMA peak.
 //
 // Work decomposition.  128 x 128 output tiles, one per workgroup of 8 / TM
 // waves (each 32 TM x 64: TM x 2 subtiles), two workgroups per CU so that
@@ -56,6 +60,8 @@ struct Cfg {
     static constexpr int TM = TM_, BM = 128, NS = 2;
     static constexpr int NWAVE = 8 / TM, NT = NWAVE * WAVE;
     static constexpr bool PF = TM == 2;
+    // waves per SIMD of two resident workgroups: <= 512 / WPE VGPRs a wave
+    static constexpr int WPE = 2 * NWAVE / 4;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
     static constexpr int XS = WQ + KS * BN * 32;  // [KS][BM] u32 X ds words
@@ -121,7 +127,7 @@ struct Frag {
 };
 
 template <class C, int EPI>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm(
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE))) void k_gemm(
     const uint8_t *__restrict__ xq, const uint32_t *__restrict__ xds, int64_t ld_ds,
     const uint8_t *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ldT, int M, int N,
     int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
@@ -239,27 +245,24 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         for (int b = 0; b < 2; ++b) F[i].sw[b] = v2i{0, 0};
     }
 
-    // One K block, subtile k = 2a + b.  Step k issues subtile k's two MFMAs
-    // into result slot k & 1, each followed by half of the rescale of the
-    // previous subtile (k - 1, or the last subtile of the previous block for
-    // k = 0), so every MFMA result is read two MFMAs after its issue and the
-    // matrix pipe and the VALU overlap within the wave.  The last subtile's
-    // rescale stays pending into the next block (flush() after the last
-    // block).  The pending slot starts as I = 0, s = 0: fmaf(0, 0, +0) = +0.
-    // Each acc element still receives its fmas in block order.
+    // One K block, subtile k = 2a + b, in three MFMAs and 16 fmas:
+    //   D = X.W^T + 0x4B400000 (int8 MFMA whose accumulator starts at the
+    //       bits of the float 1.5 * 2^23, whose ulp is 1: D read as a float
+    //       is 12582912 + I exactly, |I| <= 32 * 128 * 128 < 2^22);
+    //   I = D - 12582912 (an f16 MFMA adding -2048 x 6144 from k-slot 0 to
+    //       the accumulator D: exact, so I is (float)I_kb);
+    //   s = dx[i] * dw[j] (the scale tile);
+    //   acc = fmaf(I, s, acc) on the VALU.
+    // The matrix pipe (3 x 32 cycles) rather than the VALU (16 x 4 cycles)
+    // bounds a subtile-block; the convert-on-VALU form it replaces needed 32
+    // VALU instructions (128 cycles).  Results are consumed right away (no
+    // slot ring inside the wave, which keeps the kernel at <= 128 VGPRs and
+    // 4 waves per SIMD): the SIMD's other waves cover the MFMA latency.
     constexpr int NSUB = 2 * TM;
-    v16i I[2];
-    v16f S[2];
-    auto rescale = [&](int slot, int pa, int pb) {
-        float c[16];
+    v16i magic;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) c[r] = (float)I[slot][r];
-        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[pa][pb][r] = fmaf(c[r], S[slot][r], acc[pa][pb][r]);
-        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-    };
+    for (int r = 0; r < 16; ++r) magic[r] = 0x4B400000;
+    const v2i cA = {lh ? 0 : 0xE800, 0}, cB = {lh ? 0 : 0x6E00, 0};  // f16 -2048, 6144 in slot 0
     auto compute = [&](const Frag<TM> &f, int kb) {
         const v16f zf = {};
         const v16i zi = {};
@@ -284,23 +287,18 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #pragma unroll
             for (int k = 0; k < NSUB; ++k) {
                 const int a = k >> 1, b = k & 1;
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                I[k & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], zi, 0, 0, 0);
-                const int p = (k + NSUB - 1) % NSUB;  // previous subtile, in the other slot
-                S[k & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.sx[a]),
-                                                                __builtin_bit_cast(v4h, f.sw[b]), zf, 0, 0, 0);
-                rescale((k + 1) & 1, p >> 1, p & 1);
+                const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], magic, 0, 0, 0);
+                const v16f I = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, cA),
+                                                                    __builtin_bit_cast(v4h, cB),
+                                                                    __builtin_bit_cast(v16f, D), 0, 0, 0);
+                const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.sx[a]),
+                                                                    __builtin_bit_cast(v4h, f.sw[b]), zf, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], S[r], acc[a][b][r]);
             }
         }
         // one scheduling region per block: nothing moves across blocks
         __builtin_amdgcn_sched_barrier(0);
-    };
-    auto flush = [&] {
-        if constexpr (EPI != EPI_DUMP_I) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                acc[TM - 1][1][r] = fmaf((float)I[1][r], S[1][r], acc[TM - 1][1][r]);
-        }
     };
 
     // the zero pads after each block's W scales (never written by the DMA)
@@ -321,11 +319,6 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        I[1][r] = 0;
-        S[1][r] = 0.0f;
-    }
 
     issue(0);
     arrive(0);
@@ -398,7 +391,6 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             }
         }
     }
-    flush();
 
     {
         // ------------------------------------------------------------------
