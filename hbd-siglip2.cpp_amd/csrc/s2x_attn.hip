@@ -544,6 +544,83 @@ __global__ __launch_bounds__(64) void k_attn_f64(
     }
 }
 
+// The same arithmetic for segments of at most 64 tokens (the text prompts),
+// spread over a workgroup of 256 lanes per (head, segment) instead of one
+// lane per query: each score, each query's maximum, sum and each output
+// element keeps its own sequential order (the keys ascending, d ascending),
+// so the results are the bits of k_attn_f64; only independent sums run side
+// by side.  Q, K, V are staged as f16 (rows of 74 halves: consecutive rows
+// start 37 dwords apart, so a wave reading one d of 64 rows spreads over
+// the banks), the scores and then the probabilities as doubles.
+constexpr int A64S_P = 74;
+
+__global__ __launch_bounds__(256) void k_attn_f64_short(
+    const float *__restrict__ qkv, int64_t ld, const float *__restrict__ bias,
+    const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len,
+    const uint8_t *__restrict__ key_valid, int n_head, int d_head, double scale,
+    float *__restrict__ out, int64_t ld_out) {
+    __shared__ _Float16 qs[A64_T][A64S_P], ks[A64_T][A64S_P], vs[A64_T][A64S_P];
+    __shared__ double S[A64_T][A64_T + 1];
+    __shared__ double mx_s[A64_T], den_s[A64_T];
+    const int h = blockIdx.x, sg = blockIdx.y;
+    const int len = seg_len[sg];
+    const int64_t row0 = seg_start[sg];
+    const int H = n_head * d_head;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < A64_T * d_head; i += 256) {
+        const int p = i / d_head, d = i % d_head;
+        float q = 0.0f, k = 0.0f, v = 0.0f;
+        if (p < len) {
+            const float *r = qkv + (row0 + p) * ld + h * d_head + d;
+            q = r[0] + bias[h * d_head + d];
+            k = r[H] + bias[H + h * d_head + d];
+            v = r[2 * H] + bias[2 * H + h * d_head + d];
+        }
+        qs[p][d] = f32_to_f16(q);
+        ks[p][d] = f32_to_f16(k);
+        vs[p][d] = f32_to_f16(v);
+    }
+    __syncthreads();
+    // scores: wave w takes queries w, w + 4, ..., lane j the key j
+    const bool key_ok = lane < len && (key_valid == nullptr || key_valid[row0 + lane] != 0);
+    for (int q = wave; q < len; q += 4) {
+        double acc = 0.0;
+        for (int d = 0; d < d_head; ++d)
+            acc = acc + (double)(float)qs[q][d] * (double)(float)ks[lane][d];
+        S[q][lane] = key_ok ? acc * scale : -INFINITY;
+    }
+    __syncthreads();
+    if (tid < len) {
+        double m = -INFINITY;
+        for (int j = 0; j < len; ++j) m = fmax(m, S[tid][j]);
+        mx_s[tid] = m;
+    }
+    __syncthreads();
+    for (int i = tid; i < len * A64_T; i += 256) {
+        const int q = i >> 6, j = i & 63;
+        if (j < len) {
+            const double sc = S[q][j];
+            S[q][j] = sc == -INFINITY ? 0.0 : exp(sc - mx_s[q]);
+        }
+    }
+    __syncthreads();
+    if (tid < len) {
+        double den = 0.0;
+        for (int j = 0; j < len; ++j) den = den + S[tid][j];
+        den_s[tid] = den;
+    }
+    __syncthreads();
+    for (int i = tid; i < len * d_head; i += 256) {
+        const int q = i / d_head, d = i % d_head;
+        double acc = 0.0;
+        for (int j = 0; j < len; ++j) {
+            const double p = S[q][j];
+            if (p != 0.0) acc = acc + p * (double)(float)vs[j][d];
+        }
+        out[(row0 + q) * ld_out + h * d_head + d] = (float)(acc / den_s[q]);
+    }
+}
+
 hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                            const int32_t *seg_start, const int32_t *seg_len,
                            const uint8_t *key_valid, int64_t n_seg, int64_t max_len,
@@ -551,6 +628,12 @@ hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bi
                            int64_t ld_out, hipStream_t stream) {
     if (n_seg == 0) return hipSuccess;
     if (d_head > A64_DMAX) return hipErrorInvalidValue;
+    if (max_len <= A64_T && d_head <= A64S_P - 2) {
+        hipLaunchKernelGGL(k_attn_f64_short, dim3((unsigned)n_head, (unsigned)n_seg), dim3(256), 0,
+                           stream, qkv, ld_qkv, qkv_bias, seg_start, seg_len, key_valid, (int)n_head,
+                           (int)d_head, (double)scale, out, ld_out);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((max_len + A64_T - 1) / A64_T), (unsigned)n_head, (unsigned)n_seg);
     hipLaunchKernelGGL(k_attn_f64, grid, dim3(A64_T), 0, stream, qkv, ld_qkv, qkv_bias, seg_start,
                        seg_len, key_valid, (int)n_head, (int)d_head, (double)scale, out, ld_out);

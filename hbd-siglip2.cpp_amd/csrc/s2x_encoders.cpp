@@ -828,7 +828,10 @@ int s2x_text_create(const s2x_text_weights *w, s2x_text **out) {
     x->vocab = w->vocab;
     x->max_pos = w->max_pos;
     x->proj = w->proj;
-    t.attn_f64 = true;  // 64-token prompts: fp64 attention costs little
+    // short prompts: exact-order fp64 attention (k_attn_f64_short), whose
+    // embeddings stay the oracle's to cosine 0.99999+; the flash kernel's
+    // f32 scores shift the 27-layer text embedding to ~0.99988
+    t.attn_f64 = true;
     auto bail = [&](int st) {
         delete x;
         return st;

@@ -19,14 +19,12 @@
 // cycles): the matrix pipe bounds this formulation at a third of the int8
 // MFMA peak.
 //
-// Work decomposition.  128 x 128 output tiles, one per workgroup of 8 / TM
-// waves (each 32 TM x 64: TM x 2 subtiles), two workgroups per CU so that
-// one's epilogue and pipeline fill overlap the other's K loop.  The K loop
-// runs over stages of KS = 4 blocks (each row's 128 contiguous bytes) whose
-// operands (X and W quants and scales) arrive by LDS DMA
-// (buffer_load ... lds) into a ring of 2 stage buffers, one stage ahead;
-// one workgroup barrier per stage.  With TM = 2 the fragments of the next K
-// block are read from LDS while the current block is in the MFMAs.
+// Work decomposition.  128 x 128 output tiles, one per workgroup of 8 waves
+// (each 32 x 64: 2 subtiles), two workgroups per CU so that one's epilogue
+// and pipeline fill overlap the other's K loop.  The K loop runs over
+// stages of KS blocks whose operands (X and W quants and scales) arrive by
+// LDS DMA (buffer_load ... lds) into a ring of NS stage buffers, NS - 1
+// stages ahead; one workgroup barrier per stage.
 //
 // Scale layouts: X scales are the Q8_1 ds words of the activation
 // (ds[m * ld_ds + kb] = fp16 d | fp16 s << 16, the block_q8_1 scale pair);
@@ -43,45 +41,58 @@
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace s2x {
 namespace gemm {
 
 constexpr int BN = 128;  // output tile columns
-constexpr int KS = 4;    // K blocks per stage
 constexpr int GM = 8;    // tile-row group of the tile order
 constexpr int WSB = BN * 2 + 80;  // W scales of a block: BN fp16 values, then 80 zero bytes
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-// 128 x 128 output tiles; 8 / TM waves of 32 TM x 64 outputs; PF: the next
-// block's fragments are read during the current block (register budget:
-// TM = 2 waves run 2 per SIMD, TM = 1 waves 4 per SIMD).
-template <int TM_>
+// 128 x 128 tiles, 8 waves of 32 x 64 outputs; stages of KS K blocks in a
+// ring of NS stage buffers (NS - 1 stages in flight).  Two workgroups per
+// CU when two rings fit in the LDS (then 4 waves per SIMD, <= 128 VGPRs),
+// else one (2 waves per SIMD).
+template <int KS_, int NS_>
 struct Cfg {
-    static constexpr int TM = TM_, BM = 128, NS = 2;
-    static constexpr int NWAVE = 8 / TM, NT = NWAVE * WAVE;
-    static constexpr bool PF = TM == 2;
-    // waves per SIMD of two resident workgroups: <= 512 / WPE VGPRs a wave
-    static constexpr int WPE = 2 * NWAVE / 4;
+    static constexpr int TM = 1, BM = 128, KS = KS_, NS = NS_;
+    static constexpr int NWAVE = 8, NT = NWAVE * WAVE;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
     static constexpr int XS = WQ + KS * BN * 32;  // [KS][BM] u32 X ds words
     static constexpr int WS = XS + KS * BM * 4;   // [KS] x (BN fp16 + zeros) W scales
     static constexpr int STAGE = WS + KS * WSB;
     static constexpr int LDS_BYTES = NS * STAGE;
+    static constexpr int WG_PER_CU = 2 * LDS_BYTES <= 163840 ? 2 : 1;
+    static constexpr int WPE = WG_PER_CU * NWAVE / 4;  // waves per SIMD
     // DMA instructions per stage and wave: QPW X-quant and QPW W-quant (each
-    // 32 rows of one block), SPW X-scale (64 rows of one block) and 1 W-scale
-    // (with 8 waves, waves w and w + 4 both fetch the W scales of block
-    // w & 3 -- the same bytes to the same place -- so that every wave issues
-    // the same count)
-    static constexpr int QPW = 16 / NWAVE, SPW = 8 / NWAVE;
+    // 32 rows of one block: 4 KS per stage over 8 waves), SPW X-scale (64
+    // rows of one block: 2 KS per stage) and 1 W-scale (one block: KS per
+    // stage); where a stage has fewer than 8 of a kind, waves w and w + 8 / n
+    // fetch the same bytes to the same place, so every wave issues the same
+    // count
+    static constexpr int QPW = KS / 2, SPW = KS >= 4 ? KS / 4 : 1;
     static constexpr int DMA_N = 2 * QPW + SPW + 1;
-    static_assert(TM == 1 || TM == 2, "wave tile");
-    static_assert(2 * LDS_BYTES <= 163840, "two workgroups per CU");
-    static_assert(NWAVE * 32 * 36 * 4 <= LDS_BYTES && NWAVE * 64 * 40 * 2 <= LDS_BYTES,
-                  "epilogue scratch");
+    static_assert(KS == 2 || KS == 4, "stage of 2 or 4 blocks");
+    static_assert(NS >= 2 && (NS - 2) * DMA_N <= 63, "vmcnt range");
+    static_assert(LDS_BYTES <= 163840, "LDS");
+    static_assert(NWAVE * 5120 <= LDS_BYTES, "epilogue scratch");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // chunk permutation of the two 16-byte chunks of a 32-byte row
 __device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
@@ -126,12 +137,257 @@ struct Frag {
     v2i sx[TM], sw[2];
 };
 
+// Epilogue of one wave's 32 TM x 64 block (rows mw.., columns nw..), from
+// the accumulators in registers; wscr: 5,120 bytes of LDS of this wave.
+constexpr int EPI_SCRATCH = 5120;
+template <int TM, int EPI>
+__device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&bias_v)[2], int lane,
+                                         int mw, int nw, int M, int N, float *__restrict__ y,
+                                         int64_t ldy, const EpiParams &epi, uint8_t *wscr) {
+    const int lr = lane & 31, lh = lane >> 5;
+    if constexpr (EPI == EPI_GELU_Q81) {
+        // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over
+        // rows of q_kpad values (columns >= N are zeros): each 32 x 32
+        // subtile is one quant block per row; it goes through LDS so that
+        // lane pairs own a row (16 values each)
+        constexpr int P = 36;  // floats per scratch row
+        float *scr = reinterpret_cast<float *>(wscr);
+        const int row = lane >> 1, half = lane & 1;
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int nb0 = nw + b * 32;  // first column of this quant block
+                if (nb0 >= epi.q_kpad) continue;  // wave-uniform
+                const int n = nb0 + lr;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
+                        n < N ? gelu_tanh(acc[a][b][r] + bias_v[b]) : 0.0f;
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4f t = *reinterpret_cast<const v4f *>(scr + row * P + half * 16 + 4 * j);
+                    v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
+                }
+                float am = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
+                am = fmaxf(am, dpp_f<0xb1>(am));  // partner lane (xor 1)
+                const float d = am / 127.0f;
+                const float inv = am != 0.0f ? 127.0f / am : 0.0f;
+                int qi[16], qs = 0;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    qi[j] = q8_round(v[j], inv);
+                    qs += qi[j];
+                }
+                qs += dpp_i<0xb1>(qs);
+                const int m = mw + a * 32 + row;
+                if (m < M) {
+                    const int64_t off = (int64_t)m * epi.q_kpad + nb0 + half * 16;
+                    *reinterpret_cast<uint4 *>(epi.q_out8 + off) =
+                        make_uint4(pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7]),
+                                   pack4_i8(qi[8], qi[9], qi[10], qi[11]),
+                                   pack4_i8(qi[12], qi[13], qi[14], qi[15]));
+                    if (half == 0)
+                        epi.q_ds[(int64_t)m * epi.q_ldds + nb0 / QK] =
+                            (uint32_t)f32_to_f16_bits(d) |
+                            ((uint32_t)f32_to_f16_bits((float)qs * d) << 16);
+                }
+            }
+    } else if constexpr (EPI == EPI_QKV) {
+        // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad]
+        // or V^T [seg][head][dv_pad][pos]; padding slots are not written
+        const int H = epi.n_head * epi.d_head;
+        const float inv_dh = 1.0f / (float)epi.d_head;
+        if (H % 64 == 0 && nw < 2 * H && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
+            // a Q or K tile: each 32-row half of the wave's 32 x 64 block
+            // goes through LDS so that each 8-column chunk of a row (8
+            // consecutive d of one head) leaves as one 16-byte store
+            constexpr int P = 72;  // halves per scratch row
+            _Float16 *scr = reinterpret_cast<_Float16 *>(wscr);
+            _Float16 *dst0 = nw < H ? epi.q : epi.k;
+            const int hd0 = nw < H ? 0 : H;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                int rmv[4];  // row map entries, loaded before the stores
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    rmv[i] = epi.rowmap[min(mw + a * 32 + ((lane + 64 * i) >> 3), M - 1)];
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] =
+                            f32_to_f16(acc[a][b][r] + bias_v[b]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
+                    const int m = mw + a * 32 + row, n = nw + c;
+                    if (m >= M || n >= N) continue;
+                    const int hd = n - hd0;
+                    const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
+                    const int rm = rmv[i];
+                    const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                    const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
+                    *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
+                }
+            }
+        } else if (H % 64 == 0 && nw >= 2 * H) {
+            // a V tile: V^T rows are positions, so each 32-row half goes
+            // through LDS transposed (column-major, rows shifted by the
+            // first position's offset within its 8-position chunk) and
+            // each lane writes one column -- one d of one head: up to 32
+            // consecutive positions -- as 16-byte stores where the
+            // destination is 16-byte aligned, 2-byte stores at the ends
+            constexpr int PT = 40;  // halves per scratch column (shift <= 7, 32 rows)
+            _Float16 *scr = reinterpret_cast<_Float16 *>(wscr);
+            const int n = nw + lane;
+            const int hd = n - 2 * H, h = small_div(max(hd, 0), epi.d_head, inv_dh);
+            const int d = hd - h * epi.d_head;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int mr = mw + a * 32;
+                const int rows = min(32, M - mr);  // wave-uniform, may be <= 0
+                int rm_first = 0, rm_last = 0;
+                if (rows > 0) {
+                    rm_first = epi.rowmap[mr];
+                    rm_last = epi.rowmap[mr + rows - 1];
+                }
+                // one segment, consecutive positions: the common case
+                const bool run = rows > 0 && (rm_last >> 16) == (rm_first >> 16) &&
+                                 (rm_last & 0xffff) - (rm_first & 0xffff) == rows - 1;
+                const int shift = run ? (rm_first & 0xffff) & 7 : 0;
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            scr[(b * 32 + lr) * PT + shift + 8 * q + 4 * lh + j] =
+                                f32_to_f16(acc[a][b][4 * q + j] + bias_v[b]);
+                if (rows > 0 && n < N) {
+                    const _Float16 *col = scr + lane * PT;
+                    if (run) {
+                        const int64_t sh = (int64_t)(rm_first >> 16) * epi.n_head + h;
+                        _Float16 *dst =
+                            epi.vt + (sh * epi.dv_pad + d) * epi.len_pad + (rm_first & 0xffff) - shift;
+                        // positions [shift, shift + rows) of the 8-aligned window dst[0 ..)
+                        const int lo = shift, hi = shift + rows;
+                        const int a0 = (lo + 7) & ~7, a1 = hi & ~7;
+                        if (a0 <= a1) {
+                            for (int i = lo; i < a0; ++i) dst[i] = col[i];
+                            for (int i = a0; i < a1; i += 8)
+                                *reinterpret_cast<v8h *>(dst + i) = *reinterpret_cast<const v8h *>(col + i);
+                            for (int i = a1; i < hi; ++i) dst[i] = col[i];
+                        } else {
+                            for (int i = lo; i < hi; ++i) dst[i] = col[i];
+                        }
+                    } else {
+                        for (int i = 0; i < rows; ++i) {
+                            const int rm = epi.rowmap[mr + i];
+                            const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                            epi.vt[(sh * epi.dv_pad + d) * epi.len_pad + (rm & 0xffff)] = col[i];
+                        }
+                    }
+                }
+            }
+        } else {
+            // any H: one 2-byte store per element
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int n = nw + b * 32 + lr;
+                if (n >= N) continue;
+                const int part = small_div(n, H, 1.0f / (float)H), hd = n - part * H;
+                const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
+                _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        if (m >= M) continue;
+                        const int rm = epi.rowmap[m];
+                        const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
+                        const int pos = rm & 0xffff;
+                        const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
+                                                     : (sh * epi.dv_pad + d) * epi.len_pad + pos;
+                        dst[off] = f32_to_f16(acc[a][b][r] + bias_v[b]);
+                    }
+            }
+        }
+    } else {
+        // (mm + bias) [GELU | + residual], through buffer loads and stores
+        // whose bounds drop the rows past M (and the columns past N, sent
+        // out of range): no branch per element.  Each 32-row half's
+        // residual loads are all issued before its first store (y may be
+        // the residual itself: each element is read, then written, by
+        // one lane).
+        constexpr uint32_t OOB = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(y + (int64_t)mw * ldy), (short)0, clip32((int64_t)(M - mw) * ldy * 4), BUF_DW3);
+        const bool rmod = epi.resid_rows > 0;
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(epi.resid + (rmod ? 0 : (int64_t)mw * epi.ld_resid)), (short)0,
+            EPI == EPI_BIAS_RESID
+                ? clip32((rmod ? epi.resid_rows : (int64_t)(M - mw)) * epi.ld_resid * 4)
+                : 0,
+            BUF_DW3);
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            float res[2][16];
+            if constexpr (EPI == EPI_BIAS_RESID) {
+                // residual row of this lane's first row in the half; the
+                // others are at most 27 rows further (one wrap when
+                // resid_rows >= 28)
+                const int R = (int)epi.resid_rows;
+                const int m_first = mw + a * 32 + 4 * lh;
+                const int r_first = rmod ? m_first % R : m_first - mw;
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int n = nw + b * 32 + lr;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int dm = 8 * (r >> 2) + (r & 3);
+                        int rm = r_first + dm;
+                        if (rmod) rm = R >= 28 ? (rm >= R ? rm - R : rm) : rm % R;
+                        const uint32_t off =
+                            n < N ? (uint32_t)(rm * (int)epi.ld_resid + n) * 4u : OOB;
+                        const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0);
+                        res[b][r] = __builtin_bit_cast(float, bits);
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int n = nw + b * 32 + lr;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = acc[a][b][r];
+                    if (EPI == EPI_BIAS) {
+                        v = v + bias_v[b];
+                    } else if (EPI == EPI_BIAS_GELU) {
+                        v = gelu_tanh(v + bias_v[b]);
+                    } else if (EPI == EPI_BIAS_RESID) {
+                        v = (v + bias_v[b]) + res[b][r];
+                    }
+                    const int mr = a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const uint32_t off = n < N ? (uint32_t)(mr * (int)ldy + n) * 4u : OOB;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr,
+                                                          off, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 template <class C, int EPI>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE))) void k_gemm(
     const uint8_t *__restrict__ xq, const uint32_t *__restrict__ xds, int64_t ld_ds,
     const uint8_t *__restrict__ wq, const uint16_t *__restrict__ wdT, int64_t ldT, int M, int N,
     int KB, float *__restrict__ y, int64_t ldy, EpiParams epi) {
-    constexpr int BM = C::BM, NS = C::NS, STAGE = C::STAGE, TM = C::TM;
+    constexpr int BM = C::BM, NS = C::NS, KS = C::KS, STAGE = C::STAGE, TM = C::TM;
     constexpr int XQ = C::XQ, WQ = C::WQ, XS = C::XS, WS = C::WS;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x;
@@ -148,18 +404,18 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 
     // Per-lane DMA source offsets (relative to the tile's first row / column;
     // the K position goes into the scalar offset).
-    //   X and W quants, instructions t < QPW: i = QPW wave + t, block i & 3,
-    //             rows 32 (i >> 2) .. + 31
-    //   X scales, instructions t < SPW: i = SPW wave + t, block i >> 1,
-    //             rows 64 (i & 1) .. + 63 (one ds word per lane)
-    //   W scales: block wave & 3, columns 2 lane, 2 lane + 1
+    //   X and W quants, instructions t < QPW: i = QPW wave + t, block i % KS,
+    //             rows 32 (i / KS) .. + 31 (= 32 (wave / 2) for every t)
+    //   X scales, instructions t < SPW: i = (SPW wave + t) % (2 KS), block
+    //             i / 2, rows 64 (i % 2) .. + 63 (one ds word per lane)
+    //   W scales: block wave % KS, columns 2 lane, 2 lane + 1
     uint32_t vq, vxs[C::SPW];
     {
-        const int r = 32 * ((C::QPW * wave) >> 2) + (lane >> 1);
+        const int r = 32 * (wave >> 1) + (lane >> 1);
         vq = (uint32_t)(r * row_bytes) + (uint32_t)(((lane & 1) ^ swz(r)) * 16);
 #pragma unroll
         for (int t = 0; t < C::SPW; ++t) {
-            const int i = C::SPW * wave + t;
+            const int i = (C::SPW * wave + t) % (2 * KS);
             vxs[t] = (uint32_t)(((i & 1) * 64 + lane) * ld_ds * 4);
         }
     }
@@ -174,43 +430,43 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, 0, BUF_DW3);
 
     // Issue the DMA of stage g into buffer g % NS.  Reads past M, N or the
-    // planes return zeros; blocks past KB in the last stage are fetched and
-    // never used.  The stage after the last is issued too, through
-    // zero-size buffers (no memory is read), so that no branch splits the K
-    // loop.
+    // planes return zeros (the scalar offset is part of the range check);
+    // blocks past KB in the last stage are fetched and never used.  Stages
+    // past the last are issued too, through zero-size buffers (no memory is
+    // read), so that no branch splits the K loop.
     auto issue = [&](int g) {
         const bool live = g < n_st;
         const __amdgpu_buffer_rsrc_t xr = live ? xr_live : none, wr = live ? wr_live : none;
         const __amdgpu_buffer_rsrc_t xsr = live ? xsr_live : none, wsr = live ? wsr_live : none;
-        uint8_t *sb = lds + (g & 1) * STAGE;
+        uint8_t *sb = lds + (g % NS) * STAGE;
         const uint32_t k0 = (uint32_t)(g * KS);
 #pragma unroll
         for (int t = 0; t < C::QPW; ++t) {
-            const int i = C::QPW * wave + t, j = i & 3;
-            dma16(xr, vq, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i >> 2) * 1024);
+            const int i = C::QPW * wave + t, j = i % KS;
+            dma16(xr, vq, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
         }
 #pragma unroll
         for (int t = 0; t < C::QPW; ++t) {
-            const int i = C::QPW * wave + t, j = i & 3;
-            dma16(wr, vq, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i >> 2) * 1024);
+            const int i = C::QPW * wave + t, j = i % KS;
+            dma16(wr, vq, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
         }
 #pragma unroll
         for (int t = 0; t < C::SPW; ++t) {
-            const int i = C::SPW * wave + t, j = i >> 1;
+            const int i = (C::SPW * wave + t) % (2 * KS), j = i >> 1;
             dma4(xsr, vxs[t], (k0 + j) * 4, sb + XS + j * BM * 4 + (i & 1) * 256);
         }
-        dma4(wsr, (uint32_t)lane * 4, (uint32_t)((k0 + (wave & 3)) * ldT * 2),
-             sb + WS + (wave & 3) * WSB);
+        dma4(wsr, (uint32_t)lane * 4, (uint32_t)((k0 + wave % KS) * ldT * 2),
+             sb + WS + (wave % KS) * WSB);
     };
 
-    // Stage g visible to every wave: this wave's DMA of it has landed, then
-    // the barrier.  After the barrier no wave reads the buffer of stage
-    // g - 1 any more (its last fragments were read before this point), so
-    // stage g + 1 refills it.
+    // Stage g visible to every wave: this wave's DMA of it has landed (the
+    // NS - 2 later stages may still be in flight), then the barrier.  After
+    // the barrier no wave reads the buffer of stage g - 1 any more (its last
+    // fragments were read before this point), so stage g + NS - 1 refills it.
     auto arrive = [&](int g) {
-        wait_vm<0>();
+        wait_vm<(NS - 2) * C::DMA_N>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        issue(g + 1);
+        issue(g + NS - 1);
     };
 
     // fragment addresses (bytes within a stage buffer) of this lane
@@ -236,14 +492,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     };
 
     float acc[TM][2][16];
-    Frag<TM> F[C::PF ? 2 : 1];
+    Frag<TM> F;
 #pragma unroll
-    for (int i = 0; i < (C::PF ? 2 : 1); ++i) {
+    for (int a = 0; a < TM; ++a) F.sx[a] = v2i{0, 0};
 #pragma unroll
-        for (int a = 0; a < TM; ++a) F[i].sx[a] = v2i{0, 0};
-#pragma unroll
-        for (int b = 0; b < 2; ++b) F[i].sw[b] = v2i{0, 0};
-    }
+    for (int b = 0; b < 2; ++b) F.sw[b] = v2i{0, 0};
 
     // One K block, subtile k = 2a + b, in three MFMAs and 16 fmas:
     //   D = X.W^T + 0x4B400000 (int8 MFMA whose accumulator starts at the
@@ -282,8 +535,6 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
                 }
             }
         } else {
-            // the next block's fragment reads (issued just before) go first
-            if constexpr (C::PF) __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * TM, 0);
 #pragma unroll
             for (int k = 0; k < NSUB; ++k) {
                 const int a = k >> 1, b = k & 1;
@@ -320,327 +571,46 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-    issue(0);
-    arrive(0);
-    using J0 = std::integral_constant<int, 0>;
-    using J1 = std::integral_constant<int, 1>;
-    using J2 = std::integral_constant<int, 2>;
-    using J3 = std::integral_constant<int, 3>;
-    if constexpr (C::PF) {
-        // block j uses fragment set j & 1 and reads block j + 1's fragments
-        // into the other set (at j = 3: the next stage's block 0, after the
-        // barrier that makes that stage visible)
-        load_frag(lds, J0{}, F[0]);
-        for (int g = 0; g < n_st - 1; ++g) {
-            const uint8_t *sb = lds + (g & 1) * STAGE;
-            const int kb0 = g * KS;
-            load_frag(sb, J1{}, F[1]);
-            compute(F[0], kb0);
-            load_frag(sb, J2{}, F[0]);
-            compute(F[1], kb0 + 1);
-            load_frag(sb, J3{}, F[1]);
-            compute(F[0], kb0 + 2);
-            arrive(g + 1);
-            load_frag(lds + ((g + 1) & 1) * STAGE, J0{}, F[0]);
-            compute(F[1], kb0 + 3);
-        }
-        // the last stage: nb = 1..4 blocks
-        const uint8_t *sb = lds + ((n_st - 1) & 1) * STAGE;
-        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
-        if (nb > 1) load_frag(sb, J1{}, F[1]);
-        compute(F[0], kb0);
-        if (nb > 1) {
-            if (nb > 2) load_frag(sb, J2{}, F[0]);
-            compute(F[1], kb0 + 1);
-            if (nb > 2) {
-                if (nb > 3) load_frag(sb, J3{}, F[1]);
-                compute(F[0], kb0 + 2);
-                if (nb > 3) compute(F[1], kb0 + 3);
-            }
-        }
-    } else {
-        // each block's fragments read right before its MFMAs (the other
-        // waves of the SIMD cover the LDS latency)
-        for (int g = 0; g < n_st - 1; ++g) {
-            const uint8_t *sb = lds + (g & 1) * STAGE;
-            const int kb0 = g * KS;
-            load_frag(sb, J0{}, F[0]);
-            compute(F[0], kb0);
-            load_frag(sb, J1{}, F[0]);
-            compute(F[0], kb0 + 1);
-            load_frag(sb, J2{}, F[0]);
-            compute(F[0], kb0 + 2);
-            load_frag(sb, J3{}, F[0]);
-            compute(F[0], kb0 + 3);
-            arrive(g + 1);
-        }
-        const uint8_t *sb = lds + ((n_st - 1) & 1) * STAGE;
-        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
-        load_frag(sb, J0{}, F[0]);
-        compute(F[0], kb0);
-        if (nb > 1) {
-            load_frag(sb, J1{}, F[0]);
-            compute(F[0], kb0 + 1);
-            if (nb > 2) {
-                load_frag(sb, J2{}, F[0]);
-                compute(F[0], kb0 + 2);
-                if (nb > 3) {
-                    load_frag(sb, J3{}, F[0]);
-                    compute(F[0], kb0 + 3);
-                }
-            }
-        }
+#pragma unroll
+    for (int g = 0; g < NS - 1; ++g) issue(g);
+    // the first stage visible, stage NS - 1 issued
+    wait_vm<(NS - 2) * C::DMA_N>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(NS - 1);
+    // each block's fragments are read right before its MFMAs (the other
+    // waves of the SIMD cover the LDS latency)
+    for (int g = 0; g < n_st - 1; ++g) {
+        const uint8_t *sb = lds + (g % NS) * STAGE;
+        const int kb0 = g * KS;
+        static_for<KS>([&](auto jc) {
+            load_frag(sb, jc, F);
+            compute(F, kb0 + decltype(jc)::value);
+        });
+        arrive(g + 1);
     }
-
     {
-        // ------------------------------------------------------------------
-        // Epilogue.  The LDS is free scratch once the last (empty) stage's
-        // DMA has landed and every wave has read its last fragments.
-        // ------------------------------------------------------------------
-        uint8_t *scratch = lds;
-        const int mw = m0 + wm * 32 * TM;  // first row of this wave
-        const int nw = n0 + wn * 64;       // first column of this wave
-
-        if constexpr (EPI == EPI_GELU_Q81) {
-            // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over
-            // rows of q_kpad values (columns >= N are zeros): each 32 x 32
-            // subtile is one quant block per row; it goes through LDS so that
-            // lane pairs own a row (16 values each)
-            constexpr int P = 36;  // floats per scratch row
-            wait_vm<0>();
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            float *scr = reinterpret_cast<float *>(scratch) + wave * 32 * P;
-            const int row = lane >> 1, half = lane & 1;
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int nb0 = nw + b * 32;  // first column of this quant block
-                    if (nb0 >= epi.q_kpad) continue;  // wave-uniform
-                    const int n = nb0 + lr;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
-                            n < N ? gelu_tanh(acc[a][b][r] + bias_v[b]) : 0.0f;
-                    float v[16];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const v4f t = *reinterpret_cast<const v4f *>(scr + row * P + half * 16 + 4 * j);
-                        v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
-                    }
-                    float am = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
-                    am = fmaxf(am, dpp_f<0xb1>(am));  // partner lane (xor 1)
-                    const float d = am / 127.0f;
-                    const float inv = am != 0.0f ? 127.0f / am : 0.0f;
-                    int qi[16], qs = 0;
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        qi[j] = q8_round(v[j], inv);
-                        qs += qi[j];
-                    }
-                    qs += dpp_i<0xb1>(qs);
-                    const int m = mw + a * 32 + row;
-                    if (m < M) {
-                        const int64_t off = (int64_t)m * epi.q_kpad + nb0 + half * 16;
-                        *reinterpret_cast<uint4 *>(epi.q_out8 + off) =
-                            make_uint4(pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7]),
-                                       pack4_i8(qi[8], qi[9], qi[10], qi[11]),
-                                       pack4_i8(qi[12], qi[13], qi[14], qi[15]));
-                        if (half == 0)
-                            epi.q_ds[(int64_t)m * epi.q_ldds + nb0 / QK] =
-                                (uint32_t)f32_to_f16_bits(d) |
-                                ((uint32_t)f32_to_f16_bits((float)qs * d) << 16);
-                    }
-                }
-        } else if constexpr (EPI == EPI_QKV) {
-            // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad]
-            // or V^T [seg][head][dv_pad][pos]; padding slots are not written
-            const int H = epi.n_head * epi.d_head;
-            const float inv_dh = 1.0f / (float)epi.d_head;
-            wait_vm<0>();
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (H % BN == 0 && n0 < 2 * H && epi.d_head % 8 == 0 && epi.d_pad % 8 == 0) {
-                // a Q or K tile: each 32-row half of the wave's 32 x 64 block
-                // goes through LDS so that each 8-column chunk of a row (8
-                // consecutive d of one head) leaves as one 16-byte store
-                constexpr int P = 72;  // halves per scratch row
-                _Float16 *scr = reinterpret_cast<_Float16 *>(scratch) + wave * 32 * P;
-                _Float16 *dst0 = n0 < H ? epi.q : epi.k;
-                const int hd0 = n0 < H ? 0 : H;
-#pragma unroll
-                for (int a = 0; a < TM; ++a) {
-                    int rmv[4];  // row map entries, loaded before the stores
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        rmv[i] = epi.rowmap[min(mw + a * 32 + ((lane + 64 * i) >> 3), M - 1)];
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] =
-                                f32_to_f16(acc[a][b][r] + bias_v[b]);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
-                        const int m = mw + a * 32 + row, n = nw + c;
-                        if (m >= M || n >= N) continue;
-                        const int hd = n - hd0;
-                        const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
-                        const int rm = rmv[i];
-                        const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
-                        const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
-                        *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
-                    }
-                }
-            } else if (H % BN == 0 && n0 >= 2 * H) {
-                // a V tile: V^T rows are positions, so each 32-row half goes
-                // through LDS transposed (column-major, rows shifted by the
-                // first position's offset within its 8-position chunk) and
-                // each lane writes one column -- one d of one head: up to 32
-                // consecutive positions -- as 16-byte stores where the
-                // destination is 16-byte aligned, 2-byte stores at the ends
-                constexpr int PT = 40;  // halves per scratch column (shift <= 7, 32 rows)
-                _Float16 *scr = reinterpret_cast<_Float16 *>(scratch) + wave * 64 * PT;
-                const int n = nw + lane;
-                const int hd = n - 2 * H, h = small_div(max(hd, 0), epi.d_head, inv_dh);
-                const int d = hd - h * epi.d_head;
-#pragma unroll
-                for (int a = 0; a < TM; ++a) {
-                    const int mr = mw + a * 32;
-                    const int rows = min(32, M - mr);  // wave-uniform, may be <= 0
-                    int rm_first = 0, rm_last = 0;
-                    if (rows > 0) {
-                        rm_first = epi.rowmap[mr];
-                        rm_last = epi.rowmap[mr + rows - 1];
-                    }
-                    // one segment, consecutive positions: the common case
-                    const bool run = rows > 0 && (rm_last >> 16) == (rm_first >> 16) &&
-                                     (rm_last & 0xffff) - (rm_first & 0xffff) == rows - 1;
-                    const int shift = run ? (rm_first & 0xffff) & 7 : 0;
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-#pragma unroll
-                            for (int j = 0; j < 4; ++j)
-                                scr[(b * 32 + lr) * PT + shift + 8 * q + 4 * lh + j] =
-                                    f32_to_f16(acc[a][b][4 * q + j] + bias_v[b]);
-                    if (rows > 0 && n < N) {
-                        const _Float16 *col = scr + lane * PT;
-                        if (run) {
-                            const int64_t sh = (int64_t)(rm_first >> 16) * epi.n_head + h;
-                            _Float16 *dst =
-                                epi.vt + (sh * epi.dv_pad + d) * epi.len_pad + (rm_first & 0xffff) - shift;
-                            // positions [shift, shift + rows) of the 8-aligned window dst[0 ..)
-                            const int lo = shift, hi = shift + rows;
-                            const int a0 = (lo + 7) & ~7, a1 = hi & ~7;
-                            if (a0 <= a1) {
-                                for (int i = lo; i < a0; ++i) dst[i] = col[i];
-                                for (int i = a0; i < a1; i += 8)
-                                    *reinterpret_cast<v8h *>(dst + i) = *reinterpret_cast<const v8h *>(col + i);
-                                for (int i = a1; i < hi; ++i) dst[i] = col[i];
-                            } else {
-                                for (int i = lo; i < hi; ++i) dst[i] = col[i];
-                            }
-                        } else {
-                            for (int i = 0; i < rows; ++i) {
-                                const int rm = epi.rowmap[mr + i];
-                                const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
-                                epi.vt[(sh * epi.dv_pad + d) * epi.len_pad + (rm & 0xffff)] = col[i];
-                            }
-                        }
-                    }
-                }
-            } else {
-                // any H: one 2-byte store per element
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int n = nw + b * 32 + lr;
-                    if (n >= N) continue;
-                    const int part = small_div(n, H, 1.0f / (float)H), hd = n - part * H;
-                    const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
-                    _Float16 *dst = part == 0 ? epi.q : part == 1 ? epi.k : epi.vt;
-#pragma unroll
-                    for (int a = 0; a < TM; ++a)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                            if (m >= M) continue;
-                            const int rm = epi.rowmap[m];
-                            const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
-                            const int pos = rm & 0xffff;
-                            const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
-                                                         : (sh * epi.dv_pad + d) * epi.len_pad + pos;
-                            dst[off] = f32_to_f16(acc[a][b][r] + bias_v[b]);
-                        }
-                }
+        // the last stage: nb = 1 .. KS blocks
+        const uint8_t *sb = lds + ((n_st - 1) % NS) * STAGE;
+        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
+        static_for<KS>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < nb) {
+                load_frag(sb, jc, F);
+                compute(F, kb0 + j);
             }
-        } else {
-            // (mm + bias) [GELU | + residual], through buffer loads and stores
-            // whose bounds drop the rows past M (and the columns past N, sent
-            // out of range): no branch per element.  Each 32-row half's
-            // residual loads are all issued before its first store (y may be
-            // the residual itself: each element is read, then written, by
-            // one lane).
-            constexpr uint32_t OOB = 0x80000000u;
-            const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(y + (int64_t)m0 * ldy), (short)0, clip32((int64_t)(M - m0) * ldy * 4), BUF_DW3);
-            const bool rmod = epi.resid_rows > 0;
-            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(epi.resid + (rmod ? 0 : (int64_t)m0 * epi.ld_resid)), (short)0,
-                EPI == EPI_BIAS_RESID
-                    ? clip32((rmod ? epi.resid_rows : (int64_t)(M - m0)) * epi.ld_resid * 4)
-                    : 0,
-                BUF_DW3);
-#pragma unroll
-            for (int a = 0; a < TM; ++a) {
-                float res[2][16];
-                if constexpr (EPI == EPI_BIAS_RESID) {
-                    // residual row of this lane's first row in the half; the
-                    // others are at most 27 rows further (one wrap when
-                    // resid_rows >= 28)
-                    const int R = (int)epi.resid_rows;
-                    const int m_first = mw + a * 32 + 4 * lh;
-                    const int r_first = rmod ? m_first % R : m_first - m0;
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        const int n = nw + b * 32 + lr;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int dm = 8 * (r >> 2) + (r & 3);
-                            int rm = r_first + dm;
-                            if (rmod) rm = R >= 28 ? (rm >= R ? rm - R : rm) : rm % R;
-                            const uint32_t off =
-                                n < N ? (uint32_t)(rm * (int)epi.ld_resid + n) * 4u : OOB;
-                            const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0);
-                            res[b][r] = __builtin_bit_cast(float, bits);
-                        }
-                    }
-                }
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int n = nw + b * 32 + lr;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        float v = acc[a][b][r];
-                        if (EPI == EPI_BIAS) {
-                            v = v + bias_v[b];
-                        } else if (EPI == EPI_BIAS_GELU) {
-                            v = gelu_tanh(v + bias_v[b]);
-                        } else if (EPI == EPI_BIAS_RESID) {
-                            v = (v + bias_v[b]) + res[b][r];
-                        }
-                        const int mr = wm * 32 * TM + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                        const uint32_t off = n < N ? (uint32_t)(mr * (int)ldy + n) * 4u : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr,
-                                                              off, 0, 0);
-                    }
-                }
-            }
-        }
+        });
     }
+
+    // ----------------------------------------------------------------------
+    // Epilogue.  The LDS is free scratch once the last (empty) stage's DMA
+    // has landed and every wave has read its last fragments.
+    // ----------------------------------------------------------------------
+    if constexpr (EPI == EPI_GELU_Q81 || EPI == EPI_QKV) {
+        wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    epilogue<TM, EPI>(acc, bias_v, lane, m0 + wm * 32 * TM, n0 + wn * 64, M, N, y, ldy, epi,
+                      lds + wave * EPI_SCRATCH);
     // Every DMA this wave issued has landed before the workgroup ends.
     wait_vm<0>();
 }
@@ -670,15 +640,16 @@ hipError_t run(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64
 
 }  // namespace gemm
 
-#ifndef S2X_GEMM_TM
-#define S2X_GEMM_TM 1
-#endif
-using Default = gemm::Cfg<S2X_GEMM_TM>;
+// Stage configuration: 4-block stages, a ring of 2, two workgroups per CU.
+// (A ring of 8 two-block stages at one workgroup per CU, for GEMMs of too
+// few tiles to fill the chip, measured 5-13 % slower at M = 729: their time
+// is the waves' own operand-to-result latency, not the fetch latency.)
+using Wide = gemm::Cfg<4, 2>;
 
 hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
                        int64_t M, float *y, int64_t ldy, const EpiParams &epi,
                        hipStream_t stream) {
-    using C = Default;
+    using C = Wide;
     if (M == 0 || w.N == 0) return hipSuccess;
     const int64_t KB = w.K_pad / QK;
     if (!w.qs || !w.dT || !xq || w.K_pad <= 0 || w.K_pad % QK || w.ldT < (w.N + 127) / 128 * 128 ||
@@ -687,31 +658,33 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
         (int64_t)C::BM * KB * QK > 0x7fffffff || w.ldT * KB * 2 > 0x7fffffff ||
         C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff)
         return hipErrorInvalidValue;
+#define S2X_RUN(E) gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream)
     switch (epi.kind) {
-    case EPI_NONE: return gemm::run<C, EPI_NONE>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
-    case EPI_BIAS: return gemm::run<C, EPI_BIAS>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
-    case EPI_BIAS_GELU: return gemm::run<C, EPI_BIAS_GELU>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    case EPI_NONE: return S2X_RUN(EPI_NONE);
+    case EPI_BIAS: return S2X_RUN(EPI_BIAS);
+    case EPI_BIAS_GELU: return S2X_RUN(EPI_BIAS_GELU);
     case EPI_BIAS_RESID:
         if (!epi.resid || epi.ld_resid < w.N || epi.resid_rows < 0 ||
             (epi.resid_rows > 0 ? epi.resid_rows : C::BM) * epi.ld_resid * 4 > 0x7fffffff)
             return hipErrorInvalidValue;
-        return gemm::run<C, EPI_BIAS_RESID>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+        return S2X_RUN(EPI_BIAS_RESID);
     case EPI_DUMP_I:
         if (epi.dump_kb < 0 || epi.dump_kb >= KB) return hipErrorInvalidValue;
-        return gemm::run<C, EPI_DUMP_I>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+        return S2X_RUN(EPI_DUMP_I);
     case EPI_GELU_Q81:
         if (!epi.q_out8 || !epi.q_ds || !epi.bias || epi.q_kpad % QK || epi.q_kpad < w.N ||
             epi.q_kpad - w.N >= QK || epi.q_ldds < epi.q_kpad / QK ||
             ((uintptr_t)epi.q_out8 & 15) || ((uintptr_t)epi.q_ds & 3))
             return hipErrorInvalidValue;
-        return gemm::run<C, EPI_GELU_Q81>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+        return S2X_RUN(EPI_GELU_Q81);
     case EPI_QKV:
         if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
             epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head || w.N >= (1 << 20))
             return hipErrorInvalidValue;
-        return gemm::run<C, EPI_QKV>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+        return S2X_RUN(EPI_QKV);
     default: return hipErrorInvalidValue;
     }
+#undef S2X_RUN
 }
 
 }  // namespace s2x

@@ -405,8 +405,8 @@ int s2x_vision_gemm_stats(s2x_vision *v, double *ms, double *ops,
 int s2x_text_create(const s2x_text_weights *w, s2x_text **out);
 void s2x_text_destroy(s2x_text *t);
 int s2x_text_set_stream(s2x_text *t, void *stream);
-/* Attention precision for the text tower: 1 (default) = s2x_attn_fp64,
- * 0 = the f16-MFMA flash kernel. */
+/* Attention precision for the text tower: 1 (default) = s2x_attn_fp64 (the
+ * oracle's arithmetic to within 1 ulp), 0 = the f16-MFMA flash kernel. */
 int s2x_text_set_attention_fp64(s2x_text *t, int enable);
 /* TextEncoder::encode: one prompt of n_tok ids (host), optional host mask
  * (1 = valid), out_host proj floats.  Synchronous. */

@@ -161,10 +161,13 @@ class Text:
         s2x.lib.s2x_text_destroy(self.h)
 
 
-def test_small_text_vs_oracle(orc):
+@pytest.mark.parametrize("fp64", [0, 1])
+def test_small_text_vs_oracle(orc, fp64):
+    # the flash (f16 MFMA) attention, the default, and the fp64 option
     hm = synth.text_model(SMALL_T, seed=22)
     t = Text(hm)
     try:
+        s2x.call("s2x_text_set_attention_fp64", t.h, fp64)
         om = orc.text_model(hm)
         ids, lens = synth.text_tokens(5, 64, vocab=SMALL_T.vocab)
         b = t.batch(ids)

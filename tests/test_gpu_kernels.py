@@ -392,6 +392,45 @@ def test_attention_fp64_matches_oracle(orc, masked):
     assert n_diff <= og.size // 100000
 
 
+def _attn_fp64(qkv, bias, lens, n_head, dh, kv=None):
+    H = n_head * dh
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    qd, bd, sd, ld = dev(qkv), dev(bias), dev(starts), dev(np.asarray(lens, np.int32))
+    kd = dev(kv) if kv is not None else None
+    out = empty((int(sum(lens)), H), torch.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(dh)))
+    s2x.call("s2x_attn_fp64", ptr(qd), 3 * H, ptr(bd), ptr(sd), ptr(ld), ptr(kd), len(lens),
+             max(lens), n_head, dh, ctypes.c_float(scale), ptr(out), H, stream())
+    return host(out), starts, scale
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_fp64_short_segments(orc, masked):
+    # segments of <= 64 tokens take the workgroup-per-head kernel: the bits of
+    # the one-lane-per-query kernel (run here through a batch that also holds
+    # a 100-token segment) and within 1 ulp of the oracle
+    n_head, dh = 16, 72
+    lens = [64, 17, 1, 40, 64]
+    rng = np.random.default_rng(17)
+    M = sum(lens) + 100
+    qkv = (rng.standard_normal((M, 3 * n_head * dh)) * 1.5).astype(np.float32)
+    bias = rng.normal(0, 0.5, 3 * n_head * dh).astype(np.float32)
+    kv = None
+    if masked:
+        kv = np.ones(M, np.uint8)
+        kv[5:9] = 0
+        kv[64 + 17 + 1 + 30:64 + 17 + 1 + 40] = 0
+    n_short = sum(lens)
+    short, starts, scale = _attn_fp64(qkv[:n_short], bias, lens, n_head, dh,
+                                      None if kv is None else kv[:n_short])
+    long_, _, _ = _attn_fp64(qkv, bias, lens + [100], n_head, dh, kv)
+    assert np.array_equal(short, long_[:n_short])
+    ref = np.concatenate([orc.attention((qkv + bias)[s:s + L], n_head, dh, scale,
+                                        None if kv is None else kv[s:s + L])
+                          for s, L in zip(starts, lens)])
+    assert (np.abs(short - ref) <= np.spacing(np.abs(ref))).all()
+
+
 @pytest.mark.parametrize("hw", [(27, 27), (8, 32), (16, 16), (32, 32)])
 def test_resize_pos_embed(orc, hw):
     h, w = hw
