@@ -166,6 +166,14 @@ static int check_epi(const s2x_epilogue *epi, int64_t N, EpiParams &p) {
         p.q_kpad = epi->q_kpad;
         p.q_ldds = epi->q_kpad / QK_;
         return S2X_OK;
+    case S2X_EPI_GELU_F16:
+        if (!epi->bias || !epi->q_out || epi->q_kpad % QK_ || epi->q_kpad < N ||
+            epi->q_kpad - N >= QK_ || !aligned(epi->q_out, 2))
+            return fail(S2X_ERR_INVALID_ARG, "epilogue GELU_F16: bias/q_out/q_kpad invalid");
+        p.kind = EPI_GELU_F16;
+        p.h_out = (_Float16 *)epi->q_out;
+        p.h_ld = p.h_kpad = epi->q_kpad;
+        return S2X_OK;
     default: return fail(S2X_ERR_INVALID_ARG, "epilogue: unknown kind %d", epi->kind);
     }
 }
@@ -188,7 +196,7 @@ int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds, i
     EpiParams p;
     st = check_epi(epi, w->view.N, p);
     if (st != S2X_OK) return st;
-    if (p.kind != EPI_GELU_Q81 && (!y || ldy < w->view.N || !aligned(y, 4)))
+    if (p.kind != EPI_GELU_Q81 && p.kind != EPI_GELU_F16 && (!y || ldy < w->view.N || !aligned(y, 4)))
         return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1: y null/misaligned or ldy=%lld < N=%lld",
                     (long long)ldy, (long long)w->view.N);
     if (M == 0) return S2X_OK;
@@ -232,6 +240,49 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N, const floa
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
     e = launch_gemm(wv, o.qs, o.ds, o.ld_ds, M, y, N, p, s);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
+}
+
+static MulMatWs mul_mat_f16_ws_layout(int64_t K, int64_t N, int64_t M) {
+    const int64_t K_pad = round_up_i(K, QK_);
+    MulMatWs L;
+    L.w_off = 0;
+    L.xq_off = (size_t)round_up_i(N * K_pad * 2, 256);
+    L.ds_off = L.xq_off;
+    L.total = L.xq_off + (size_t)round_up_i(M * K_pad * 2, 256);
+    return L;
+}
+
+size_t s2x_mul_mat_f16_workspace_size(int64_t K, int64_t N, int64_t M) {
+    if (K <= 0 || N <= 0 || M < 0) return 0;
+    return mul_mat_f16_ws_layout(K, N, M).total;
+}
+
+int s2x_mul_mat_f16_f32(const void *w_raw, int64_t K, int64_t N, const float *x, int64_t ldx,
+                        int64_t M, float *y, void *workspace, size_t ws_bytes, void *stream) {
+    if (K <= 0 || N <= 0 || M < 0 || ldx < K)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_f16_f32: bad shape K=%lld N=%lld M=%lld ldx=%lld",
+                    (long long)K, (long long)N, (long long)M, (long long)ldx);
+    if (M == 0) return S2X_OK;
+    if (M > (1 << 30) || N > (1 << 30) || K > (1 << 24))
+        return fail(S2X_ERR_UNSUPPORTED, "mul_mat_f16_f32: shape too large");
+    if (!w_raw || !x || !y || !workspace)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_f16_f32: null pointer");
+    const MulMatWs L = mul_mat_f16_ws_layout(K, N, M);
+    if (ws_bytes < L.total)
+        return fail(S2X_ERR_WORKSPACE, "mul_mat_f16_f32: workspace %zu < %zu bytes", ws_bytes, L.total);
+    if (!aligned(workspace, 256) || !aligned(w_raw, 2) || !aligned(x, 4) || !aligned(y, 4))
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_f16_f32: misaligned pointer");
+    const int64_t K_pad = round_up_i(K, QK_);
+    uint8_t *ws = (uint8_t *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    _Float16 *w16 = (_Float16 *)(ws + L.w_off), *x16 = (_Float16 *)(ws + L.xq_off);
+    hipError_t e = launch_repack_f16(w_raw, K, N, K_pad, w16, s);
+    if (e != hipSuccess) return hip_fail(e, "repack launch");
+    e = launch_f32_to_f16(x, K, M, ldx, K_pad, x16, s);
+    if (e != hipSuccess) return hip_fail(e, "convert launch");
+    EpiParams p{EPI_NONE, nullptr, nullptr, 0, 0, 0};
+    e = launch_gemm_f16(w16, K_pad, N, x16, M, y, N, p, s);
     return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
 }
 

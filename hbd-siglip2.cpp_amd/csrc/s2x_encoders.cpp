@@ -118,15 +118,45 @@ int upload_q8(const void *raw, int64_t K_pad, int64_t N, hipStream_t s, s2x_weig
     return weight_upload(raw, true, K_pad, N, s, w);
 }
 
+// F16 matrix (N rows of K halves, host) -> device rows of K_pad halves, zero
+// past K
+int upload_f16(const void *raw, int64_t K, int64_t K_pad, int64_t N, _Float16 **dev,
+               const char *what) {
+    *dev = nullptr;
+    if (!raw) return fail(S2X_ERR_INVALID_ARG, "missing tensor %s", what);
+    const size_t bytes = sizeof(_Float16) * (size_t)(N * K_pad);
+    if (hipMalloc(reinterpret_cast<void **>(dev), bytes) != hipSuccess)
+        return fail(S2X_ERR_OOM, "hipMalloc for %s failed", what);
+    S2X_HIP_TRY(hipMemset(*dev, 0, bytes));
+    S2X_HIP_TRY(hipMemcpy2D(*dev, (size_t)K_pad * 2, raw, (size_t)K * 2, (size_t)K * 2, (size_t)N,
+                            hipMemcpyHostToDevice));
+    return S2X_OK;
+}
+
+// ffn_down: a Q8_0 weight, or F16 rows (the converter's type for K % 32 != 0)
+struct DownW {
+    s2x_weight *q8 = nullptr;
+    _Float16 *f16 = nullptr;  // N rows of K_pad halves
+    void release() {
+        s2x_weight_destroy(q8);
+        if (f16) (void)hipFree(f16);
+    }
+    int upload(const void *raw, bool as_f16, int64_t K, int64_t K_pad, int64_t N, hipStream_t s,
+               const char *what) {
+        return as_f16 ? upload_f16(raw, K, K_pad, N, &f16, what) : upload_q8(raw, K_pad, N, s, &q8, what);
+    }
+};
+
 struct DevLayer {
-    s2x_weight *qkv = nullptr, *o = nullptr, *up = nullptr, *down = nullptr;
+    s2x_weight *qkv = nullptr, *o = nullptr, *up = nullptr;
+    DownW down;
     float *ln1_w = nullptr, *ln1_b = nullptr, *qkv_b = nullptr, *o_b = nullptr;
     float *ln2_w = nullptr, *ln2_b = nullptr, *up_b = nullptr, *down_b = nullptr;
     void release() {
         s2x_weight_destroy(qkv);
         s2x_weight_destroy(o);
         s2x_weight_destroy(up);
-        s2x_weight_destroy(down);
+        down.release();
         for (float *p : {ln1_w, ln1_b, qkv_b, o_b, ln2_w, ln2_b, up_b, down_b})
             if (p) (void)hipFree(p);
     }
@@ -185,8 +215,10 @@ struct Tower {
     hipStream_t own = nullptr, stream = nullptr;
     // x: residual stream f32 [M][H]; qs / ds: Q8_1 of the current GEMM input
     // ([M][kmax] int8, [M][kmax/32] ds words); qs2 / ds2: the fc1 epilogue's
-    // Q8_1 output (fc2 input, K = F_pad)
-    DevBuf x, qs, ds, qs2, ds2, qkv, att, attn_ws, seg, rowmap;
+    // Q8_1 output (fc2 input, K = F_pad); h16: its f16 output instead, for
+    // an F16 ffn_down ([M][F_pad] halves)
+    DevBuf x, qs, ds, qs2, ds2, h16, qkv, att, attn_ws, seg, rowmap;
+    bool down_f16 = false;
     GemmTiming timing;
     // attention in fp64 (k_attn_f64, from an f32 QKV GEMM output) instead of
     // the f16-MFMA flash kernel fed by the QKV GEMM's attention-layout epilogue
@@ -219,7 +251,7 @@ struct Tower {
             S2X_TRY(upload_f32(s.ln2_b, H, &d.ln2_b, "ln2.bias"));
             S2X_TRY(upload_q8(s.up_w, H, F, stream, &d.up, "ffn_up.weight"));
             S2X_TRY(upload_f32(s.up_b, F, &d.up_b, "ffn_up.bias"));
-            S2X_TRY(upload_q8(s.down_w, F_pad, H, stream, &d.down, "ffn_down.weight"));
+            S2X_TRY(d.down.upload(s.down_w, down_f16, F, F_pad, H, stream, "ffn_down.weight"));
             S2X_TRY(upload_f32(s.down_b, H, &d.down_b, "ffn_down.bias"));
         }
         return S2X_OK;
@@ -244,6 +276,30 @@ struct Tower {
             timing.pending.push_back({a, b, 2.0 * (double)M * (double)w->view.N * (double)k_logical});
         }
         return S2X_OK;
+    }
+
+    // The MLP of a block or of the MAP head on M rows whose LN2 + Q8_1 is in
+    // qs / ds: fc1 (+bias, GELU, and Q8_1 -- or f16 for an F16 ffn_down --
+    // of the result), then fc2 (+bias + resid) into y.
+    int ffn(const s2x_weight *up, const float *up_b, const DownW &down, const float *down_b,
+            int64_t M, float *y, const float *resid) {
+        if (down.f16) {
+            EpiParams ep{EPI_GELU_F16, up_b, nullptr, 0, 0, 0};
+            ep.h_out = h16.as<_Float16>();
+            ep.h_ld = ep.h_kpad = F_pad;
+            S2X_TRY(gemm(up, M, nullptr, 0, ep, H));
+            const hipError_t e = launch_gemm_f16(down.f16, F_pad, H, h16.as<_Float16>(), M, y, H,
+                                                 EpiParams{EPI_BIAS_RESID, down_b, resid, H, 0, 0},
+                                                 stream);
+            return e == hipSuccess ? S2X_OK : hip_fail(e, "f16 gemm launch");
+        }
+        EpiParams ep{EPI_GELU_Q81, up_b, nullptr, 0, 0, 0};
+        ep.q_out8 = qs2.as<int8_t>();
+        ep.q_ds = ds2.as<uint32_t>();
+        ep.q_kpad = F_pad;
+        ep.q_ldds = F_pad / QK_;
+        S2X_TRY(gemm(up, M, nullptr, 0, ep, H));
+        return gemm(down.q8, M, y, H, EpiParams{EPI_BIAS_RESID, down_b, resid, H, 0, 0}, F, true);
     }
 
     // Q8_1 planes of the GEMM input buffers for rows of K_pad values
@@ -273,8 +329,12 @@ struct Tower {
         S2X_TRY(ensure(x, sizeof(float) * (size_t)(M * H), stream));
         S2X_TRY(ensure(qs, (size_t)(M * kmax), stream));
         S2X_TRY(ensure(ds, sizeof(uint32_t) * (size_t)(M * (kmax / QK_)), stream));
-        S2X_TRY(ensure(qs2, (size_t)(M * F_pad), stream));
-        S2X_TRY(ensure(ds2, sizeof(uint32_t) * (size_t)(M * (F_pad / QK_)), stream));
+        if (down_f16) {
+            S2X_TRY(ensure(h16, sizeof(_Float16) * (size_t)(M * F_pad), stream));
+        } else {
+            S2X_TRY(ensure(qs2, (size_t)(M * F_pad), stream));
+            S2X_TRY(ensure(ds2, sizeof(uint32_t) * (size_t)(M * (F_pad / QK_)), stream));
+        }
         S2X_TRY(ensure(att, sizeof(float) * (size_t)(M * H), stream));
         if (attn_f64)
             S2X_TRY(ensure(qkv, sizeof(float) * (size_t)(M * 3 * H), stream));
@@ -359,13 +419,7 @@ struct Tower {
             S2X_TRY(quantize(att.as<float>(), H, M, H, H));
             S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
             S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
-            EpiParams up{EPI_GELU_Q81, L.up_b, nullptr, 0, 0, 0};
-            up.q_out8 = qs2.as<int8_t>();
-            up.q_ds = ds2.as<uint32_t>();
-            up.q_kpad = F_pad;
-            up.q_ldds = F_pad / QK_;
-            S2X_TRY(gemm(L.up, M, nullptr, 0, up, H));
-            S2X_TRY(gemm(L.down, M, xp, H, EpiParams{EPI_BIAS_RESID, L.down_b, xp, H, 0, 0}, F, true));
+            S2X_TRY(ffn(L.up, L.up_b, L.down, L.down_b, M, xp, xp));
         }
         return S2X_OK;
     }
@@ -395,7 +449,8 @@ using namespace s2x;
 struct s2x_vision {
     Tower t;
     int64_t patch_dim = 0, n_side = 0;
-    s2x_weight *patch = nullptr, *hkv = nullptr, *ho = nullptr, *hup = nullptr, *hdown = nullptr;
+    s2x_weight *patch = nullptr, *hkv = nullptr, *ho = nullptr, *hup = nullptr;
+    DownW hdown;
     float *patch_b = nullptr, *pos_embd = nullptr, *post_ln_w = nullptr, *post_ln_b = nullptr;
     float *probe_q = nullptr, *hkv_b = nullptr, *ho_b = nullptr, *hln_w = nullptr,
           *hln_b = nullptr, *hup_b = nullptr, *hdown_b = nullptr;
@@ -403,7 +458,8 @@ struct s2x_vision {
     DevBuf pix, pos_packed, kv, hq, ha, hout, hid, nf_ws;
 
     ~s2x_vision() {
-        for (s2x_weight *w : {patch, hkv, ho, hup, hdown}) s2x_weight_destroy(w);
+        for (s2x_weight *w : {patch, hkv, ho, hup}) s2x_weight_destroy(w);
+        hdown.release();
         for (float *p : {patch_b, pos_embd, post_ln_w, post_ln_b, probe_q, hkv_b, ho_b, hln_w,
                          hln_b, hup_b, hdown_b})
             if (p) (void)hipFree(p);
@@ -469,14 +525,7 @@ struct s2x_vision {
         S2X_TRY(t.quantize(hq.as<float>(), H, n_img, H, H));
         S2X_TRY(t.gemm(ho, n_img, ha.as<float>(), H, EpiParams{EPI_BIAS, ho_b, nullptr, 0, 0, 0}, H));
         S2X_TRY(t.layernorm_q(ha.as<float>(), n_img, hln_w, hln_b, nullptr));
-        EpiParams up{EPI_GELU_Q81, hup_b, nullptr, 0, 0, 0};
-        up.q_out8 = t.qs2.as<int8_t>();
-        up.q_ds = t.ds2.as<uint32_t>();
-        up.q_kpad = t.F_pad;
-        up.q_ldds = t.F_pad / QK_;
-        S2X_TRY(t.gemm(hup, n_img, nullptr, 0, up, H));
-        S2X_TRY(t.gemm(hdown, n_img, out_dev, H, EpiParams{EPI_BIAS_RESID, hdown_b, ha.as<float>(), H, 0, 0}, t.F, true));
-        return S2X_OK;
+        return t.ffn(hup, hup_b, hdown, hdown_b, n_img, out_dev, ha.as<float>());
     }
 };
 
@@ -489,6 +538,8 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
     S2X_TRY(check_dims(w->hidden, w->inter, w->inter_pad, w->n_head, w->n_layer));
     if (w->patch_dim <= 0 || w->patch_dim % 32 != 0 || w->n_side <= 0)
         return fail(S2X_ERR_INVALID_ARG, "vision_create: bad patch_dim/n_side");
+    if (w->down_f16 != 0 && w->down_f16 != 1)
+        return fail(S2X_ERR_INVALID_ARG, "vision_create: down_f16 must be 0 or 1");
     s2x_vision *v = new s2x_vision();
     Tower &t = v->t;
     t.H = w->hidden;
@@ -498,6 +549,7 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
     t.d_head = t.H / t.n_head;
     t.n_layer = w->n_layer;
     t.eps = w->eps;
+    t.down_f16 = w->down_f16 != 0;
     v->patch_dim = w->patch_dim;
     v->n_side = w->n_side;
     auto bail = [&](int st) {
@@ -536,7 +588,7 @@ int s2x_vision_create(const s2x_vision_weights *w, s2x_vision **out) {
         (st = upload_f32(w->hln_b, H, &v->hln_b, "head.ln.bias")) ||
         (st = upload_q8(w->hup_w, H, F, s, &v->hup, "head.ffn_up.weight")) ||
         (st = upload_f32(w->hup_b, F, &v->hup_b, "head.ffn_up.bias")) ||
-        (st = upload_q8(w->hdown_w, F_pad, H, s, &v->hdown, "head.ffn_down.weight")) ||
+        (st = v->hdown.upload(w->hdown_w, t.down_f16, F, F_pad, H, s, "head.ffn_down.weight")) ||
         (st = upload_f32(w->hdown_b, H, &v->hdown_b, "head.ffn_down.bias")))
         return bail(st);
     // The probe query is image independent: q = mm(W_q, probe) + b_q, once.
@@ -816,6 +868,8 @@ int s2x_text_create(const s2x_text_weights *w, s2x_text **out) {
     S2X_TRY(check_dims(w->hidden, w->inter, w->inter_pad, w->n_head, w->n_layer));
     if (w->vocab <= 0 || w->max_pos <= 0 || w->proj <= 0 || !w->tok_embd)
         return fail(S2X_ERR_INVALID_ARG, "text_create: bad vocab/max_pos/proj");
+    if (w->down_f16 != 0 && w->down_f16 != 1)
+        return fail(S2X_ERR_INVALID_ARG, "text_create: down_f16 must be 0 or 1");
     s2x_text *x = new s2x_text();
     Tower &t = x->t;
     t.H = w->hidden;
@@ -825,6 +879,7 @@ int s2x_text_create(const s2x_text_weights *w, s2x_text **out) {
     t.d_head = t.H / t.n_head;
     t.n_layer = w->n_layer;
     t.eps = w->eps;
+    t.down_f16 = w->down_f16 != 0;
     x->vocab = w->vocab;
     x->max_pos = w->max_pos;
     x->proj = w->proj;

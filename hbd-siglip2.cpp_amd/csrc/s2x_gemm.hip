@@ -196,6 +196,23 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                             ((uint32_t)f32_to_f16_bits((float)qs * d) << 16);
                 }
             }
+    } else if constexpr (EPI == EPI_GELU_F16) {
+        // GELU(mm + bias) rounded to f16, rows of h_kpad halves (columns
+        // N .. h_kpad - 1 zero): the f16 activation of an F16 weight
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int n = nw + b * 32 + lr;
+                if (n >= epi.h_kpad) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    if (m < M)
+                        epi.h_out[(int64_t)m * epi.h_ld + n] =
+                            n < N ? f32_to_f16(gelu_tanh(acc[a][b][r] + bias_v[b])) : (_Float16)0.0f;
+                }
+            }
     } else if constexpr (EPI == EPI_QKV) {
         // (mm + bias) in f32, then f16, into Q / K [seg][head][pos][d_pad]
         // or V^T [seg][head][dv_pad][pos]; padding slots are not written
@@ -638,6 +655,152 @@ hipError_t run(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// F16 weight x f16 activation, f32 accumulation (GGML_OP_MUL_MAT with an
+// F16 weight, as the reference's converter stores ffn_down: K = 4304 is
+// not a multiple of 32).  Same tiles, waves, tile order and LDS-DMA ring as
+// k_gemm; a K block is 32 halves (64-byte rows, four 16-byte chunks, chunk
+// c of row r at position c ^ ((r >> 2) & 3)), two v_mfma_f32_32x32x16_f16
+// per subtile accumulate straight into the outputs: no scales, no VALU.
+// ---------------------------------------------------------------------------
+struct CfgH {
+    static constexpr int BM = 128, KS = 2, NS = 2, NWAVE = 8, NT = NWAVE * WAVE;
+    static constexpr int XQ = 0, WQ = XQ + KS * BM * 64, STAGE = WQ + KS * BN * 64;
+    static constexpr int LDS_BYTES = NS * STAGE;  // 64 KiB: two workgroups per CU
+    static constexpr int DMA_N = 2 * (KS * BM / 16) / NWAVE;  // 16 rows of a block per instruction
+    static_assert(NWAVE * EPI_SCRATCH <= LDS_BYTES, "epilogue scratch");
+};
+
+__device__ __forceinline__ int swz4(int r) { return (r >> 2) & 3; }
+
+template <int EPI>
+__global__ __launch_bounds__(CfgH::NT) __attribute__((amdgpu_waves_per_eu(4))) void k_gemm_f16(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ wh, int M, int N, int KB,
+    float *__restrict__ y, int64_t ldy, EpiParams epi) {
+    using C = CfgH;
+    constexpr int BM = C::BM, KS = C::KS, STAGE = C::STAGE, XQ = C::XQ, WQ = C::WQ;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(xcd_linear(blockIdx.x, gridDim.x), m_tiles, n_tiles, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int n_st = (KB + KS - 1) / KS;
+    const int64_t row_bytes = (int64_t)KB * 64;
+
+    // DMA: a stage is KS blocks x 128 rows of X and of W, 16 rows of one
+    // block per instruction (lane: row lane / 4, chunk position lane % 4);
+    // waves 0-3 fetch X, 4-7 W, instruction t of wave w: block t % KS, rows
+    // 16 (G (w % 4) + t / KS) .. + 15, G = DMA_N / KS row groups per wave
+    const int kind = wave >> 2;
+    const __amdgpu_buffer_rsrc_t src_live = kind == 0
+        ? __builtin_amdgcn_make_buffer_rsrc((void *)(xh + (int64_t)m0 * row_bytes), (short)0,
+                                            clip32((int64_t)(M - m0) * row_bytes), BUF_DW3)
+        : __builtin_amdgcn_make_buffer_rsrc((void *)(wh + (int64_t)n0 * row_bytes), (short)0,
+                                            clip32((int64_t)(N - n0) * row_bytes), BUF_DW3);
+    const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)xh, (short)0, 0, BUF_DW3);
+    uint32_t voff[C::DMA_N];
+#pragma unroll
+    for (int t = 0; t < C::DMA_N; ++t) {
+        const int r = 16 * (C::DMA_N / KS * (wave & 3) + t / KS) + (lane >> 2);
+        voff[t] = (uint32_t)(r * row_bytes) + (uint32_t)(((lane & 3) ^ swz4(r)) * 16);
+    }
+    auto issue = [&](int g) {
+        const __amdgpu_buffer_rsrc_t src = g < n_st ? src_live : none;
+        uint8_t *sb = lds + (g & 1) * STAGE + (kind == 0 ? XQ : WQ);
+        const uint32_t k0 = (uint32_t)(g * KS);
+#pragma unroll
+        for (int t = 0; t < C::DMA_N; ++t) {
+            const int j = t % KS, grp = C::DMA_N / KS * (wave & 3) + t / KS;
+            dma16(src, voff[t], (k0 + j) * 64, sb + j * BM * 64 + grp * 1024);
+        }
+    };
+    auto arrive = [&](int g) {
+        wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(g + 1);
+    };
+
+    const int xrow = wm * 32 + lr;
+    int a_off[2], b_off[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        a_off[h] = XQ + xrow * 64 + (((2 * h + lh) ^ swz4(xrow)) * 16);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int wc = wn * 64 + b * 32 + lr;
+            b_off[b][h] = WQ + wc * 64 + (((2 * h + lh) ^ swz4(wc)) * 16);
+        }
+    }
+    v16f acc_v[2] = {};
+    auto block = [&](const uint8_t *sb, int j) {
+        v8h a[2], bq[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            a[h] = *reinterpret_cast<const v8h *>(sb + a_off[h] + j * BM * 64);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                bq[b][h] = *reinterpret_cast<const v8h *>(sb + b_off[b][h] + j * BN * 64);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc_v[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[h], bq[b][h], acc_v[b], 0, 0, 0);
+    };
+
+    issue(0);
+    arrive(0);
+    for (int g = 0; g < n_st - 1; ++g) {
+        const uint8_t *sb = lds + (g & 1) * STAGE;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) block(sb, j);
+        arrive(g + 1);
+    }
+    {
+        const uint8_t *sb = lds + ((n_st - 1) & 1) * STAGE;
+        const int nb = KB - (n_st - 1) * KS;
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            if (j < nb) block(sb, j);
+    }
+
+    float acc[1][2][16];
+    float bias_v[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int n = n0 + wn * 64 + b * 32 + lr;
+        bias_v[b] = EPI != EPI_NONE && n < N ? epi.bias[n] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][b][r] = acc_v[b][r];
+    }
+    epilogue<1, EPI>(acc, bias_v, lane, m0 + wm * 32, n0 + wn * 64, M, N, y, ldy, epi,
+                     lds + wave * EPI_SCRATCH);
+    wait_vm<0>();
+}
+
+template <int EPI>
+hipError_t run_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16 *x16, int64_t M,
+                   float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    auto kern = k_gemm_f16<EPI>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 CfgH::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int64_t tiles = ((M + CfgH::BM - 1) / CfgH::BM) * ((N + BN - 1) / BN);
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CfgH::NT), CfgH::LDS_BYTES, stream,
+                       reinterpret_cast<const uint8_t *>(x16), reinterpret_cast<const uint8_t *>(w16),
+                       (int)M, (int)N, (int)(K_pad / QK), y, ldy, epi);
+    return hipGetLastError();
+}
+
 }  // namespace gemm
 
 // Stage configuration: 4-block stages, a ring of 2, two workgroups per CU.
@@ -677,6 +840,11 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
             ((uintptr_t)epi.q_out8 & 15) || ((uintptr_t)epi.q_ds & 3))
             return hipErrorInvalidValue;
         return S2X_RUN(EPI_GELU_Q81);
+    case EPI_GELU_F16:
+        if (!epi.h_out || !epi.bias || epi.h_kpad % QK || epi.h_kpad < w.N ||
+            epi.h_kpad - w.N >= QK || epi.h_ld < epi.h_kpad)
+            return hipErrorInvalidValue;
+        return S2X_RUN(EPI_GELU_F16);
     case EPI_QKV:
         if (!epi.q || !epi.k || !epi.vt || !epi.rowmap || !epi.bias || epi.n_head <= 0 ||
             epi.d_head <= 0 || w.N != 3 * (int64_t)epi.n_head * epi.d_head || w.N >= (1 << 20))
@@ -685,6 +853,26 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
     default: return hipErrorInvalidValue;
     }
 #undef S2X_RUN
+}
+
+hipError_t launch_gemm_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16 *x16,
+                           int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                           hipStream_t stream) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if (!w16 || !x16 || !y || K_pad <= 0 || K_pad % QK || M > (1 << 30) || N > (1 << 30) ||
+        ((uintptr_t)w16 & 15) || ((uintptr_t)x16 & 15) || (int64_t)gemm::CfgH::BM * K_pad * 2 > 0x7fffffff ||
+        gemm::CfgH::BM * ldy * 4 > 0x7fffffff)
+        return hipErrorInvalidValue;
+    switch (epi.kind) {
+    case EPI_NONE: return gemm::run_f16<EPI_NONE>(w16, K_pad, N, x16, M, y, ldy, epi, stream);
+    case EPI_BIAS: return gemm::run_f16<EPI_BIAS>(w16, K_pad, N, x16, M, y, ldy, epi, stream);
+    case EPI_BIAS_RESID:
+        if (!epi.resid || epi.ld_resid < N || epi.resid_rows < 0 ||
+            (epi.resid_rows > 0 ? epi.resid_rows : gemm::CfgH::BM) * epi.ld_resid * 4 > 0x7fffffff)
+            return hipErrorInvalidValue;
+        return gemm::run_f16<EPI_BIAS_RESID>(w16, K_pad, N, x16, M, y, ldy, epi, stream);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace s2x

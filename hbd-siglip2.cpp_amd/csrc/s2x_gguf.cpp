@@ -6,10 +6,15 @@
 // read-only, its metadata and tensor directory parsed, and the tensors bound
 // by the converter's names (scripts/convert_siglip2_to_gguf.py:7-35) into
 // s2x_vision_weights / s2x_text_weights.  Q8_0 and F32 tensors are used in
-// place; F16 vectors are widened to F32, and F16 / F32 matrices are
-// quantized to Q8_0 on load (ggml's quantize_row_q8_0_ref rule) with K
-// zero-padded to a multiple of 32, as the reference loader's F16 -> Q8_0
-// branch does (src/gguf_loader.cpp:290-330).
+// place; F16 vectors are widened to F32.  ffn_down matrices stored as F16
+// -- what the converter writes for them in a q8_0 file, K = 4304 not being a
+// multiple of 32 (scripts/convert_siglip2_to_gguf.py:241-290) -- stay F16
+// and run as F16 x F32 products, as the reference's encoders keep the
+// on-disk type (src/siglip2_vision.cpp:496-556, dup_meta).  Any other F16 /
+// F32 matrix (a file converted to f16 or f32 throughout) is quantized to
+// Q8_0 on load (ggml's quantize_row_q8_0_ref rule, K zero-padded to a
+// multiple of 32), where the reference would multiply in F16 / F32: this
+// library's GEMMs for those matrices are the Q8_0 ones.
 //
 // File layout (GGUF v2/v3): magic "GGUF", u32 version, u64 tensor count,
 // u64 metadata count; metadata entries (string key, u32 type, value);
@@ -365,17 +370,45 @@ int bind_q8(s2x_gguf *g, const std::string &name, int64_t K, int64_t K_pad, int6
     return S2X_OK;
 }
 
+// ffn_down: an F16 matrix (K = F in ne0) is used in place as F16 rows
+// (*is_f16 = 1); Q8_0 / F32 go through bind_q8 (*is_f16 = 0).
+int bind_down(s2x_gguf *g, const std::string &name, int64_t F, int64_t F_pad, int64_t N,
+              const void **out, int *is_f16) {
+    auto it = g->tensors.find(name);
+    if (it == g->tensors.end()) return fail(S2X_ERR_INVALID_ARG, "gguf: missing tensor %s", name.c_str());
+    const TensorInfo &t = it->second;
+    if (t.type != T_F16) {
+        *is_f16 = 0;
+        return bind_q8(g, name, F, F_pad, N, out);
+    }
+    const int64_t ne0 = t.ne[0], ne1 = t.nelem() / t.ne[0];
+    if (ne0 != F || ne1 != N)
+        return fail(S2X_ERR_INVALID_ARG, "gguf: F16 %s has shape (%lld, %lld), expected (%lld, %lld)",
+                    name.c_str(), (long long)ne0, (long long)ne1, (long long)F, (long long)N);
+    if (reinterpret_cast<uintptr_t>(t.data) % 2 != 0) {
+        uint8_t *c = g->own((size_t)(N * F * 2));
+        std::memcpy(c, t.data, (size_t)(N * F * 2));
+        *out = c;
+    } else {
+        *out = t.data;
+    }
+    *is_f16 = 1;
+    return S2X_OK;
+}
+
 std::string blk(const char *tower, int il, const char *suffix) {
     return std::string(tower) + ".blk." + std::to_string(il) + "." + suffix;
 }
 
+// down_f16: set from the first layer's ffn_down; every other ffn_down of the
+// tower must have the same type
 int bind_layers(s2x_gguf *g, const char *tower, int64_t n_layer, int64_t H, int64_t F,
-                int64_t F_pad, std::vector<s2x_layer_weights> &layers) {
+                int64_t F_pad, std::vector<s2x_layer_weights> &layers, int32_t *down_f16) {
     layers.assign((size_t)n_layer, s2x_layer_weights{});
     for (int64_t il = 0; il < n_layer; ++il) {
         s2x_layer_weights &L = layers[(size_t)il];
         const int i = (int)il;
-        int st;
+        int st, f16 = 0;
         if ((st = bind_vec(g, blk(tower, i, "ln1.weight"), H, &L.ln1_w)) ||
             (st = bind_vec(g, blk(tower, i, "ln1.bias"), H, &L.ln1_b)) ||
             (st = bind_q8(g, blk(tower, i, "attn_qkv.weight"), H, H, 3 * H, &L.qkv_w)) ||
@@ -386,9 +419,12 @@ int bind_layers(s2x_gguf *g, const char *tower, int64_t n_layer, int64_t H, int6
             (st = bind_vec(g, blk(tower, i, "ln2.bias"), H, &L.ln2_b)) ||
             (st = bind_q8(g, blk(tower, i, "ffn_up.weight"), H, H, F, &L.up_w)) ||
             (st = bind_vec(g, blk(tower, i, "ffn_up.bias"), F, &L.up_b)) ||
-            (st = bind_q8(g, blk(tower, i, "ffn_down.weight"), F, F_pad, H, &L.down_w)) ||
+            (st = bind_down(g, blk(tower, i, "ffn_down.weight"), F, F_pad, H, &L.down_w, &f16)) ||
             (st = bind_vec(g, blk(tower, i, "ffn_down.bias"), H, &L.down_b)))
             return st;
+        if (il == 0) *down_f16 = f16;
+        if (f16 != *down_f16)
+            return fail(S2X_ERR_UNSUPPORTED, "gguf: %s ffn_down types differ between layers", tower);
     }
     return S2X_OK;
 }
@@ -478,10 +514,14 @@ int s2x_gguf_vision_weights(s2x_gguf *g, s2x_vision_weights *w) {
         (st = bind_vec(g, "v.head.ln.bias", H, &v.hln_b)) ||
         (st = bind_q8(g, "v.head.ffn_up.weight", H, H, F, &v.hup_w)) ||
         (st = bind_vec(g, "v.head.ffn_up.bias", F, &v.hup_b)) ||
-        (st = bind_q8(g, "v.head.ffn_down.weight", F, F_pad, H, &v.hdown_w)) ||
         (st = bind_vec(g, "v.head.ffn_down.bias", H, &v.hdown_b)) ||
-        (st = bind_layers(g, "v", layers, H, F, F_pad, g->vision_layers)))
+        (st = bind_layers(g, "v", layers, H, F, F_pad, g->vision_layers, &v.down_f16)))
         return st;
+    int head_f16 = 0;
+    if ((st = bind_down(g, "v.head.ffn_down.weight", F, F_pad, H, &v.hdown_w, &head_f16)))
+        return st;
+    if (head_f16 != v.down_f16)
+        return fail(S2X_ERR_UNSUPPORTED, "gguf: v.head.ffn_down type differs from the layers'");
     v.layers = g->vision_layers.data();
     *w = v;
     return S2X_OK;
@@ -522,7 +562,7 @@ int s2x_gguf_text_weights(s2x_gguf *g, s2x_text_weights *w) {
         (st = bind_vec(g, "t.final_ln.bias", H, &t.final_ln_b)) ||
         (st = bind_q8(g, "t.head.weight", H, H, proj, &t.head_w)) ||
         (st = bind_vec(g, "t.head.bias", proj, &t.head_b)) ||
-        (st = bind_layers(g, "t", layers, H, F, F_pad, g->text_layers)))
+        (st = bind_layers(g, "t", layers, H, F, F_pad, g->text_layers, &t.down_f16)))
         return st;
     t.layers = g->text_layers.data();
     *w = t;

@@ -38,6 +38,7 @@ enum EpiKind {
     EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_BIAS_RESID = 3, EPI_DUMP_I = 4,
     EPI_QKV = 5,       // (mm + bias) -> f16 Q / K / V^T in the attention layout
     EPI_GELU_Q81 = 6,  // GELU(mm + bias) quantized to Q8_1 (int8 quants + ds words)
+    EPI_GELU_F16 = 7,  // GELU(mm + bias) rounded to f16 (rows of h_kpad halves)
 };
 
 struct EpiParams {
@@ -57,6 +58,9 @@ struct EpiParams {
     int8_t   *q_out8;
     uint32_t *q_ds;
     int64_t   q_kpad, q_ldds;
+    // EPI_GELU_F16: f16 rows [M][h_ld], columns N..h_kpad-1 written as zero
+    _Float16 *h_out;
+    int64_t   h_ld, h_kpad;
 };
 
 // a1: F32 -> Q8_1 into the planes of `out`.
@@ -73,6 +77,20 @@ hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t 
 hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
                        int64_t M, float *y, int64_t ldy, const EpiParams &epi,
                        hipStream_t stream);
+
+// F16 weights (the converter's type for matrices whose K is not a multiple
+// of 32, e.g. ffn_down): Y = W16 x f16(X) with f32 accumulation on f16 MFMA.
+// w16: N rows of K_pad halves, x16: M rows of K_pad halves (both zero past
+// K, 16-byte aligned rows); epilogues NONE, BIAS, BIAS_RESID.
+hipError_t launch_gemm_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16 *x16,
+                           int64_t M, float *y, int64_t ldy, const EpiParams &epi,
+                           hipStream_t stream);
+// f32 rows (K valid of ldx) -> f16 rows of K_pad halves, zeros past K
+hipError_t launch_f32_to_f16(const float *x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
+                             _Float16 *y, hipStream_t stream);
+// raw F16 weight rows (N rows of K halves, device) -> N rows of K_pad halves
+hipError_t launch_repack_f16(const void *raw, int64_t K, int64_t N, int64_t K_pad, _Float16 *w16,
+                             hipStream_t stream);
 
 // a4: LayerNorm (+ Q8_1).  q may be null (no quantized output), y may be
 // null (no f32 output); at least one is set.

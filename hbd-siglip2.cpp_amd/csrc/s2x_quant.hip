@@ -115,6 +115,58 @@ hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t 
 }
 
 // ---------------------------------------------------------------------------
+// F16 operands of the F16-weight GEMM: f32 activation rows -> f16 (round to
+// nearest even, as ggml's F32 -> F16 of the vec_dot operand), and raw F16
+// weight rows copied into rows of K_pad halves; both zero past K.  One
+// thread per 4 output halves.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_f32_to_f16(const float *__restrict__ x, int64_t K,
+                                                    int64_t M, int64_t ldx, int64_t K_pad,
+                                                    _Float16 *__restrict__ y) {
+    const int64_t q = K_pad / 4;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= M * q) return;
+    const int64_t m = i / q, k0 = (i % q) * 4;
+    const float *r = x + m * ldx;
+    _Float16 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = k0 + j < K ? f32_to_f16(r[k0 + j]) : (_Float16)0.0f;
+    *reinterpret_cast<uint2 *>(y + m * K_pad + k0) = __builtin_bit_cast(uint2, v);
+}
+
+__global__ __launch_bounds__(256) void k_repack_f16(const uint16_t *__restrict__ raw, int64_t K,
+                                                    int64_t N, int64_t K_pad,
+                                                    uint16_t *__restrict__ w) {
+    const int64_t q = K_pad / 4;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * q) return;
+    const int64_t n = i / q, k0 = (i % q) * 4;
+    uint16_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = k0 + j < K ? raw[n * K + k0 + j] : (uint16_t)0;
+    *reinterpret_cast<uint2 *>(w + n * K_pad + k0) = __builtin_bit_cast(uint2, v);
+}
+
+hipError_t launch_f32_to_f16(const float *x, int64_t K, int64_t M, int64_t ldx, int64_t K_pad,
+                             _Float16 *y, hipStream_t stream) {
+    const int64_t n = M * (K_pad / 4);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, K,
+                       M, ldx, K_pad, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_f16(const void *raw, int64_t K, int64_t N, int64_t K_pad, _Float16 *w16,
+                             hipStream_t stream) {
+    const int64_t n = N * (K_pad / 4);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const uint16_t *>(raw), K, N, K_pad,
+                       reinterpret_cast<uint16_t *>(w16));
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // a4: LayerNorm(+affine)(+Q8_1).  One wave per row, the row held in
 // registers: a two-pass mean / variance (double sums) from wave butterflies, then
 // y = ((x - mean) * scale) * w + b rounded after each operation

@@ -20,7 +20,7 @@ __all__ = [
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "libs2x.so")
 
-EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_GELU_Q81 = 0, 1, 2, 3, 4
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_GELU_Q81, EPI_GELU_F16 = 0, 1, 2, 3, 4, 5
 POOL_MEAN, POOL_PROBE = 0, 1
 
 if not os.path.exists(LIB_PATH):
@@ -85,7 +85,7 @@ class VisionWeights(ctypes.Structure):
         ("post_ln_b", _p), ("probe", _p), ("hq_w", _p), ("hk_w", _p), ("hv_w", _p),
         ("ho_w", _p), ("hq_b", _p), ("hk_b", _p), ("hv_b", _p), ("ho_b", _p),
         ("hln_w", _p), ("hln_b", _p), ("hup_w", _p), ("hup_b", _p), ("hdown_w", _p),
-        ("hdown_b", _p), ("layers", ctypes.POINTER(LayerWeights)),
+        ("hdown_b", _p), ("layers", ctypes.POINTER(LayerWeights)), ("down_f16", _i32),
     ]
 
 
@@ -95,7 +95,7 @@ class TextWeights(ctypes.Structure):
         ("n_layer", _i32), ("vocab", _i32), ("max_pos", _i32), ("proj", _i32),
         ("eps", _f32), ("tok_embd", _p), ("pos_embd", _p), ("final_ln_w", _p),
         ("final_ln_b", _p), ("head_w", _p), ("head_b", _p),
-        ("layers", ctypes.POINTER(LayerWeights)),
+        ("layers", ctypes.POINTER(LayerWeights)), ("down_f16", _i32),
     ]
 
 
@@ -120,6 +120,8 @@ _sig("s2x_mul_mat_q8_0_q8_1", [_p, _p, _p, _i64, _p, _i64, ctypes.POINTER(Epilog
 _sig("s2x_mul_mat_workspace_size", [_i64, _i64, _i64], _sz)
 _sig("s2x_mul_mat_q8_0_f32", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _sz, _p])
 _sig("s2x_mul_mat_q8_0_f32_static", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p])
+_sig("s2x_mul_mat_f16_workspace_size", [_i64, _i64, _i64], _sz)
+_sig("s2x_mul_mat_f16_f32", [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _sz, _p])
 _sig("s2x_block_dots", [_p, _p, _i64, _i64, _p, _p])
 _sig("s2x_mul_mat_qkv_attn_prep", [_p, _p, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz,
                                    _p])

@@ -122,6 +122,7 @@ class HostModel:
     tensors: dict = field(default_factory=dict)
     layers: list = field(default_factory=list)
     struct: object = None
+    down_f16: bool = False  # ffn_down matrices as F16 rows
     _keep: list = field(default_factory=list)
 
     def ptr(self, a):
@@ -139,7 +140,16 @@ LAYER_KEYS = ["ln1_w", "ln1_b", "qkv_w", "qkv_b", "o_w", "o_b", "ln2_w", "ln2_b"
               "up_w", "up_b", "down_w", "down_b"]
 
 
-def _layer(seed, base, H, F, F_pad):
+def _down(seed, idx, F, H, F_pad, f16):
+    """ffn_down: Q8_0 with K padded to F_pad, or (f16) F16 rows of F halves
+    from the same N(0, 0.02) draw (the reference converter's type for K % 32
+    != 0)."""
+    if f16:
+        return _normal(seed, idx, (H, F), 0.02).astype(np.float16)
+    return _linear(seed, idx, F, H, F_pad)
+
+
+def _layer(seed, base, H, F, F_pad, f16=False):
     return {
         "ln1_w": _normal(seed, base + 0, (H,), 0.02, 1.0),
         "ln1_b": _normal(seed, base + 1, (H,), 0.02),
@@ -151,20 +161,21 @@ def _layer(seed, base, H, F, F_pad):
         "ln2_b": _normal(seed, base + 7, (H,), 0.02),
         "up_w": _linear(seed, base + 8, H, F),
         "up_b": _normal(seed, base + 9, (F,), 0.02),
-        "down_w": _linear(seed, base + 10, F, H, F_pad),
+        "down_w": _down(seed, base + 10, F, H, F_pad, f16),
         "down_b": _normal(seed, base + 11, (H,), 0.02),
     }
 
 
-def _layers(seed, n_layer, H, F, F_pad):
+def _layers(seed, n_layer, H, F, F_pad, f16=False):
     """Every layer's tensors (each from its own seeded streams, so the
     values do not depend on the order the threads run in)."""
     with ThreadPoolExecutor(min(4, os.cpu_count() or 1)) as ex:
-        return list(ex.map(lambda l: _layer(seed, 1000 + 100 * l, H, F, F_pad), range(n_layer)))
+        return list(ex.map(lambda l: _layer(seed, 1000 + 100 * l, H, F, F_pad, f16), range(n_layer)))
 
 
-def vision_model(cfg=SO400M_VISION, seed=0):
-    """Seeded vision tower weights; .struct is an s2x.VisionWeights."""
+def vision_model(cfg=SO400M_VISION, seed=0, down_f16=False):
+    """Seeded vision tower weights; .struct is an s2x.VisionWeights.
+    down_f16: ffn_down matrices (layers and MAP head) as F16."""
     from . import LayerWeights, VisionWeights
     H, F, Fp = cfg.hidden, cfg.inter, cfg.inter_pad
     m = HostModel(cfg)
@@ -187,9 +198,10 @@ def vision_model(cfg=SO400M_VISION, seed=0):
     t["hln_b"] = _normal(seed, 16, (H,), 0.02)
     t["hup_w"] = _linear(seed, 17, H, F)
     t["hup_b"] = _normal(seed, 18, (F,), 0.02)
-    t["hdown_w"] = _linear(seed, 19, F, H, Fp)
+    t["hdown_w"] = _down(seed, 19, F, H, Fp, down_f16)
     t["hdown_b"] = _normal(seed, 20, (H,), 0.02)
-    m.layers = _layers(seed, cfg.n_layer, H, F, Fp)
+    m.layers = _layers(seed, cfg.n_layer, H, F, Fp, down_f16)
+    m.down_f16 = down_f16
     larr = (LayerWeights * max(1, cfg.n_layer))()
     for l, L in enumerate(m.layers):
         for k in LAYER_KEYS:
@@ -201,12 +213,14 @@ def vision_model(cfg=SO400M_VISION, seed=0):
     for k, v in t.items():
         setattr(s, k, m.ptr(v))
     s.layers = ctypes.cast(larr, ctypes.POINTER(LayerWeights))
+    s.down_f16 = int(down_f16)
     m.struct = s
     return m
 
 
-def text_model(cfg=SO400M_TEXT, seed=0):
-    """Seeded text tower weights; .struct is an s2x.TextWeights."""
+def text_model(cfg=SO400M_TEXT, seed=0, down_f16=False):
+    """Seeded text tower weights; .struct is an s2x.TextWeights.
+    down_f16: ffn_down matrices as F16."""
     from . import LayerWeights, TextWeights
     H, F, Fp = cfg.hidden, cfg.inter, cfg.inter_pad
     m = HostModel(cfg)
@@ -217,7 +231,8 @@ def text_model(cfg=SO400M_TEXT, seed=0):
     t["final_ln_b"] = _normal(seed, 4, (H,), 0.02)
     t["head_w"] = _linear(seed, 5, H, cfg.proj)
     t["head_b"] = _normal(seed, 6, (cfg.proj,), 0.02)
-    m.layers = _layers(seed, cfg.n_layer, H, F, Fp)
+    m.layers = _layers(seed, cfg.n_layer, H, F, Fp, down_f16)
+    m.down_f16 = down_f16
     larr = (LayerWeights * max(1, cfg.n_layer))()
     for l, L in enumerate(m.layers):
         for k in LAYER_KEYS:
@@ -230,6 +245,7 @@ def text_model(cfg=SO400M_TEXT, seed=0):
     for k, v in t.items():
         setattr(s, k, m.ptr(v))
     s.layers = ctypes.cast(larr, ctypes.POINTER(LayerWeights))
+    s.down_f16 = int(down_f16)
     m.struct = s
     return m
 

@@ -96,12 +96,16 @@ typedef enum {
     S2X_EPI_BIAS = 1,        /* y = acc + bias[n]                            */
     S2X_EPI_BIAS_GELU = 2,   /* y = gelu_tanh(acc + bias[n])                 */
     S2X_EPI_BIAS_RESID = 3,  /* y = (acc + bias[n]) + resid[r(m)*ld_resid+n] */
-    S2X_EPI_GELU_Q81 = 4     /* no y: gelu_tanh(acc + bias[n]) quantized to  */
+    S2X_EPI_GELU_Q81 = 4,    /* no y: gelu_tanh(acc + bias[n]) quantized to  */
                              /* Q8_1 over rows of q_kpad values (columns     */
                              /* N..q_kpad-1 zero): q_out (M rows of q_kpad   */
                              /* int8, 16-byte aligned) and q_ds (M rows of   */
                              /* q_kpad/32 words), = s2x_quantize_q8_1 of the */
                              /* BIAS_GELU output, bit for bit                */
+    S2X_EPI_GELU_F16 = 5     /* no y: f16(gelu_tanh(acc + bias[n])) in M rows */
+                             /* of q_kpad halves at q_out (columns N..q_kpad */
+                             /* -1 zero; q_ds unused): the activation of an  */
+                             /* F16 weight (s2x_mul_mat_f16_f32's X in f16)  */
 } s2x_epilogue_kind;
 
 typedef struct {
@@ -110,9 +114,9 @@ typedef struct {
     const float *resid;       /* BIAS_RESID only; may alias y             */
     int64_t      ld_resid;    /* row stride of resid in floats            */
     int64_t      resid_rows;  /* 0: r(m) = m; > 0: r(m) = m % resid_rows  */
-    void        *q_out;       /* GELU_Q81 only                            */
+    void        *q_out;       /* GELU_Q81, GELU_F16                        */
     void        *q_ds;        /* GELU_Q81 only                            */
-    int64_t      q_kpad;      /* GELU_Q81: N <= q_kpad < N + 32, % 32 == 0 */
+    int64_t      q_kpad;      /* GELU_*: N <= q_kpad < N + 32, % 32 == 0   */
 } s2x_epilogue;
 
 int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds,
@@ -128,6 +132,20 @@ int s2x_mul_mat_q8_0_f32(const void *w_raw, int64_t K_pad, int64_t N,
                          const float *x, int64_t K, int64_t ldx, int64_t M,
                          float *y, void *workspace, size_t ws_bytes,
                          void *stream);
+
+/* Drop-in GGML_OP_MUL_MAT(W: F16 (K, N), X: F32 (K, M)) -> Y: F32 (N, M),
+ * the reference's path for weights its converter stores as F16 (matrices
+ * whose K is not a multiple of 32: ffn_down, scripts/convert_siglip2_to_
+ * gguf.py:241-290, kept F16 by src/siglip2_vision.cpp:496-556).  X is
+ * rounded to f16 (as ggml converts the F32 operand of an F16 dot) and the
+ * products accumulate in f32 on f16 MFMA.  w_raw: N rows of K halves on the
+ * device.  K is zero-padded to a multiple of 32 inside `workspace`
+ * (s2x_mul_mat_f16_workspace_size() bytes, 256-byte aligned).  No
+ * allocation. */
+size_t s2x_mul_mat_f16_workspace_size(int64_t K, int64_t N, int64_t M);
+int s2x_mul_mat_f16_f32(const void *w_raw, int64_t K, int64_t N, const float *x,
+                        int64_t ldx, int64_t M, float *y, void *workspace,
+                        size_t ws_bytes, void *stream);
 
 /* Allocation-free variant of s2x_mul_mat_q8_0_f32: same arguments without
  * the workspace, same results bit for bit.  No counterpart in the reference;
@@ -287,7 +305,10 @@ int s2x_get_rows_q8_0(const void *table_raw, int64_t K, int64_t n_rows_table,
 /* a10  encoders (replace siglip2::VisionEncoder / TextEncoder,               */
 /* src/siglip2_vision.h:37-68, src/siglip2_text.h:25-75).                     */
 /* Weights come from host memory: raw Q8_0 blocks for every matrix, f32 for  */
-/* biases, LayerNorms, position embeddings and the probe.                     */
+/* biases, LayerNorms, position embeddings and the probe -- except, with     */
+/* down_f16 = 1, the ffn_down matrices (layers and MAP head): F16 rows (H    */
+/* rows of F halves), the type the reference's converter writes for a K not  */
+/* a multiple of 32 and its encoder keeps (src/siglip2_vision.cpp:496-556).  */
 /* ------------------------------------------------------------------------ */
 typedef struct {
     const float *ln1_w, *ln1_b;
@@ -295,7 +316,7 @@ typedef struct {
     const void  *o_w;    const float *o_b;     /* Q8_0 (H, H)                */
     const float *ln2_w, *ln2_b;
     const void  *up_w;   const float *up_b;    /* Q8_0 (H, F)                */
-    const void  *down_w; const float *down_b;  /* Q8_0 (F_pad, H)            */
+    const void  *down_w; const float *down_b;  /* Q8_0 (F_pad, H) or F16 (F, H) */
 } s2x_layer_weights;
 
 typedef struct {
@@ -310,8 +331,9 @@ typedef struct {
     const float *hq_b, *hk_b, *hv_b, *ho_b;
     const float *hln_w, *hln_b;
     const void  *hup_w; const float *hup_b;     /* Q8_0 (H, F)            */
-    const void  *hdown_w; const float *hdown_b; /* Q8_0 (F_pad, H)        */
+    const void  *hdown_w; const float *hdown_b; /* as the layers' down_w  */
     const s2x_layer_weights *layers;            /* n_layer entries        */
+    int32_t down_f16;                           /* 0: Q8_0, 1: F16 ffn_down */
 } s2x_vision_weights;
 
 typedef struct {
@@ -322,6 +344,7 @@ typedef struct {
     const float *final_ln_w, *final_ln_b;
     const void  *head_w; const float *head_b;   /* Q8_0 (H, proj)         */
     const s2x_layer_weights *layers;
+    int32_t down_f16;                           /* 0: Q8_0, 1: F16 ffn_down */
 } s2x_text_weights;
 
 /* ------------------------------------------------------------------------ */

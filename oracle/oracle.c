@@ -253,6 +253,27 @@ void orc_mul_mat_q8_0_f32(const void *w, int64_t K_pad, int64_t N,
     free(ds);
 }
 
+void orc_mul_mat_f16_f32(const uint16_t *w, int64_t K, int64_t N, const float *x,
+                         int64_t ldx, int64_t M, float *y, int nthreads) {
+    const int nt = orc_threads(nthreads);
+    double *xh = (double *)malloc(sizeof(double) * (size_t)(M * K));
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t k = 0; k < K; ++k) xh[m * K + k] = (double)fp16r(x[m * ldx + k]);
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (int64_t n = 0; n < N; ++n) {
+        double *wr = (double *)malloc(sizeof(double) * (size_t)K);
+        for (int64_t k = 0; k < K; ++k) wr[k] = (double)orc_fp16_to_fp32(w[n * K + k]);
+        for (int64_t m = 0; m < M; ++m) {
+            const double *xr = xh + m * K;
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc += xr[k] * wr[k];
+            y[m * N + n] = (float)acc;
+        }
+        free(wr);
+    }
+    free(xh);
+}
+
 /* ------------------------------------------------------------------------ */
 /* LayerNorm / GELU                                                          */
 /* ------------------------------------------------------------------------ */
@@ -575,9 +596,21 @@ static void linear(const void *w, const float *bias, int64_t K, int64_t K_pad,
             for (int64_t n = 0; n < N; ++n) y[m * N + n] = y[m * N + n] + bias[n];
 }
 
+/* the down projection: Q8_0 with K padded to F_pad, or F16 rows of F */
+static void linear_down(const void *w, const float *bias, int64_t F, int64_t F_pad, int64_t N,
+                        const float *x, int64_t M, float *y, int down_f16, int nthreads) {
+    if (!down_f16) {
+        linear(w, bias, F, F_pad, N, x, F, M, y, nthreads);
+        return;
+    }
+    orc_mul_mat_f16_f32((const uint16_t *)w, F, N, x, F, M, y, nthreads);
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) y[m * N + n] = y[m * N + n] + bias[n];
+}
+
 void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
                        int32_t n_head, float eps, float *x, int64_t n_pos,
-                       const uint8_t *key_valid, int nthreads) {
+                       const uint8_t *key_valid, int down_f16, int nthreads) {
     const int64_t d_head = H / n_head;
     const float kq_scale = 1.0f / sqrtf((float)d_head);
     float *h = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
@@ -595,7 +628,7 @@ void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
     orc_layernorm(x, n_pos, H, H, L->ln2_w, L->ln2_b, eps, h, H);
     linear(L->up_w, L->up_b, H, H, F, h, H, n_pos, u, nthreads);
     for (int64_t i = 0; i < n_pos * F; ++i) u[i] = orc_gelu(u[i]);
-    linear(L->down_w, L->down_b, F, F_pad, H, u, F, n_pos, o, nthreads);
+    linear_down(L->down_w, L->down_b, F, F_pad, H, u, n_pos, o, down_f16, nthreads);
     for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
 
     free(h);
@@ -626,7 +659,7 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
 
     for (int32_t l = 0; l < m->n_layer; ++l)
         orc_encoder_block(&m->layers[l], (int32_t)H, (int32_t)F, (int32_t)F_pad,
-                          m->n_head, m->eps, x, n_pos, NULL, nthreads);
+                          m->n_head, m->eps, x, n_pos, NULL, m->down_f16, nthreads);
 
     orc_layernorm(x, n_pos, H, H, m->post_ln_w, m->post_ln_b, m->eps, x, H);
     if (hidden_out) memcpy(hidden_out, x, sizeof(float) * (size_t)(n_pos * H));
@@ -683,7 +716,7 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
         orc_layernorm(a, 1, H, H, m->hln_w, m->hln_b, m->eps, a2, H);
         linear(m->hup_w, m->hup_b, H, H, F, a2, H, 1, u, nthreads);
         for (int64_t i = 0; i < F; ++i) u[i] = orc_gelu(u[i]);
-        linear(m->hdown_w, m->hdown_b, F, F_pad, H, u, F, 1, a2, nthreads);
+        linear_down(m->hdown_w, m->hdown_b, F, F_pad, H, u, 1, a2, m->down_f16, nthreads);
         for (int64_t i = 0; i < H; ++i) out[i] = a[i] + a2[i];
         free(q);
         free(a);
@@ -719,7 +752,7 @@ void orc_text_encode(const orc_text_model *m, const int32_t *tokens,
     }
     for (int32_t l = 0; l < m->n_layer; ++l)
         orc_encoder_block(&m->layers[l], (int32_t)H, m->inter, m->inter_pad,
-                          m->n_head, m->eps, x, n_pos, kv, nthreads);
+                          m->n_head, m->eps, x, n_pos, kv, m->down_f16, nthreads);
     orc_layernorm(x, n_pos, H, H, m->final_ln_w, m->final_ln_b, m->eps, x, H);
     /* last-token pooling + head (src/siglip2_text.cpp:667-675) */
     linear(m->head_w, m->head_b, H, H, m->proj, x + (n_pos - 1) * H, H, 1, out,

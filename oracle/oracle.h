@@ -185,6 +185,9 @@ typedef struct {
     const void  *hup_w; const float *hup_b;     /* K=H, N=F */
     const void  *hdown_w; const float *hdown_b; /* K=F_pad, N=H */
     const orc_layer *layers;
+    /* 1: down_w / hdown_w are F16 rows (N=H rows of K=F halves), the
+     * converter's type for K % 32 != 0; 0: Q8_0 with K padded to F_pad */
+    int32_t down_f16;
 } orc_vision_model;
 
 typedef struct {
@@ -195,13 +198,22 @@ typedef struct {
     const float *final_ln_w, *final_ln_b;
     const void  *head_w; const float *head_b;   /* K=H, N=proj */
     const orc_layer *layers;
+    int32_t down_f16;                           /* as in orc_vision_model */
 } orc_text_model;
 
 /* One pre-LN encoder block in place on x (n_pos rows of H), following
  * build_block (src/siglip2_vision.cpp:181-244). */
 void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
                        int32_t n_head, float eps, float *x, int64_t n_pos,
-                       const uint8_t *key_valid, int nthreads);
+                       const uint8_t *key_valid, int down_f16, int nthreads);
+
+/* GGML_OP_MUL_MAT with an F16 weight W (N rows of K halves) and an F32
+ * activation X (M rows, stride ldx): X rounded to f16 (round to nearest
+ * even, ggml's F32 -> F16 of the vec-dot operand), each product of two f16
+ * values exact in double, summed in double in k order, rounded to f32 once
+ * (any f32 accumulation order lies within K * 2^-24 of it). */
+void orc_mul_mat_f16_f32(const uint16_t *w, int64_t K, int64_t N, const float *x,
+                         int64_t ldx, int64_t M, float *y, int nthreads);
 
 /* Vision tower for ONE image of n_h x n_w patches (src/siglip2_vision.cpp:
  * 601-758).  pooling: 0 = mean, 1 = probe.  out: H floats.

@@ -32,7 +32,7 @@ class OrcVision(ctypes.Structure):
         ("post_ln_b", _p), ("probe", _p), ("hq_w", _p), ("hk_w", _p), ("hv_w", _p),
         ("ho_w", _p), ("hq_b", _p), ("hk_b", _p), ("hv_b", _p), ("ho_b", _p),
         ("hln_w", _p), ("hln_b", _p), ("hup_w", _p), ("hup_b", _p), ("hdown_w", _p),
-        ("hdown_b", _p), ("layers", ctypes.POINTER(OrcLayer)),
+        ("hdown_b", _p), ("layers", ctypes.POINTER(OrcLayer)), ("down_f16", _i32),
     ]
 
 
@@ -42,7 +42,7 @@ class OrcText(ctypes.Structure):
         ("n_layer", _i32), ("vocab", _i32), ("max_pos", _i32), ("proj", _i32),
         ("eps", _f32), ("tok_embd", _p), ("pos_embd", _p), ("final_ln_w", _p),
         ("final_ln_b", _p), ("head_w", _p), ("head_b", _p),
-        ("layers", ctypes.POINTER(OrcLayer)),
+        ("layers", ctypes.POINTER(OrcLayer)), ("down_f16", _i32),
     ]
 
 
@@ -61,6 +61,7 @@ def lib():
             "orc_block_dots": ([_p, _i64, _i64, _p, _i64, _p], None),
             "orc_mul_mat_q8_0_q8_1": ([_p, _i64, _i64, _p, _p, _i64, _p, ctypes.c_int], None),
             "orc_mul_mat_q8_0_f32": ([_p, _i64, _i64, _p, _i64, _i64, _i64, _p, ctypes.c_int], None),
+            "orc_mul_mat_f16_f32": ([_p, _i64, _i64, _p, _i64, _i64, _p, ctypes.c_int], None),
             "orc_layernorm": ([_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64], None),
             "orc_gelu": ([_f32], _f32),
             "orc_tanh_f32": ([_f32], _f32),
@@ -138,6 +139,18 @@ def mul_mat_q8_0_q8_1(w_raw, k_pad, n, qs, ds, nthreads=0):
     lib().orc_mul_mat_q8_0_q8_1(_ptr(np.ascontiguousarray(w_raw)), k_pad, n,
                                 _ptr(np.ascontiguousarray(qs)), _ptr(np.ascontiguousarray(ds)),
                                 M, _ptr(y), nthreads)
+    return y
+
+
+def mul_mat_f16_f32(w16, x, nthreads=0):
+    """w16 (N, K) float16 / uint16 bits, x (M, K) float32 -> (M, N) float32."""
+    w16 = np.ascontiguousarray(w16).view(np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    N = w16.shape[0]
+    assert w16.shape == (N, K)
+    y = np.empty((M, N), np.float32)
+    lib().orc_mul_mat_f16_f32(_ptr(w16), K, N, _ptr(x), K, M, _ptr(y), nthreads)
     return y
 
 
@@ -268,6 +281,7 @@ def vision_model(host):
     for k, v in t.items():
         setattr(s, k, P(v))
     s.layers = ctypes.cast(larr, ctypes.POINTER(OrcLayer))
+    s.down_f16 = int(getattr(host, "down_f16", False))
     return _Model(s, keep)
 
 
@@ -292,6 +306,7 @@ def text_model(host):
     for k, v in t.items():
         setattr(s, k, P(v))
     s.layers = ctypes.cast(larr, ctypes.POINTER(OrcLayer))
+    s.down_f16 = int(getattr(host, "down_f16", False))
     return _Model(s, keep)
 
 

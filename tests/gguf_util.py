@@ -60,6 +60,15 @@ def _f32(name, a, ne):
     return (name, T_F32, ne, np.ascontiguousarray(a, np.float32).tobytes())
 
 
+def _down(name, w, F, Fp, H):
+    """ffn_down as the converter stores it: F16 rows of F halves (a float16
+    array), else Q8_0 with K padded to Fp."""
+    w = np.ascontiguousarray(w)
+    if w.dtype == np.float16:
+        return (name, T_F16, [F, H], w.tobytes())
+    return _q8(name, w, Fp, H)
+
+
 def _layer_tensors(tower, i, L, H, F, Fp):
     p = f"{tower}.blk.{i}."
     return [
@@ -68,7 +77,7 @@ def _layer_tensors(tower, i, L, H, F, Fp):
         _q8(p + "attn_o.weight", L["o_w"], H, H), _f32(p + "attn_o.bias", L["o_b"], [H]),
         _f32(p + "ln2.weight", L["ln2_w"], [H]), _f32(p + "ln2.bias", L["ln2_b"], [H]),
         _q8(p + "ffn_up.weight", L["up_w"], H, F), _f32(p + "ffn_up.bias", L["up_b"], [F]),
-        _q8(p + "ffn_down.weight", L["down_w"], Fp, H), _f32(p + "ffn_down.bias", L["down_b"], [H]),
+        _down(p + "ffn_down.weight", L["down_w"], F, Fp, H), _f32(p + "ffn_down.bias", L["down_b"], [H]),
     ]
 
 
@@ -95,7 +104,7 @@ def vision_tensors(hm):
         ts += [_q8(f"v.head.attn_{s}.weight", t[w], H, H), _f32(f"v.head.attn_{s}.bias", t[b], [H])]
     ts += [_f32("v.head.ln.weight", t["hln_w"], [H]), _f32("v.head.ln.bias", t["hln_b"], [H]),
            _q8("v.head.ffn_up.weight", t["hup_w"], H, F), _f32("v.head.ffn_up.bias", t["hup_b"], [F]),
-           _q8("v.head.ffn_down.weight", t["hdown_w"], Fp, H),
+           _down("v.head.ffn_down.weight", t["hdown_w"], F, Fp, H),
            _f32("v.head.ffn_down.bias", t["hdown_b"], [H])]
     for i, L in enumerate(hm.layers):
         ts += _layer_tensors("v", i, L, H, F, Fp)

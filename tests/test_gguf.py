@@ -1,7 +1,8 @@
 """GGUF reader (host only): a synthetic tower written to a GGUF v3 file under
 the converter's names must come back as the same weight struct -- every
-tensor byte for byte, F16 vectors widened exactly, F16 / F32 matrices
-quantized to Q8_0 by ggml's rule with K zero-padded -- and malformed files
+tensor byte for byte, F16 vectors widened exactly, F16 ffn_down kept as
+F16, other F16 / F32 matrices quantized to Q8_0 by ggml's rule with K
+zero-padded -- and malformed files
 must be rejected with an error, never read past their end."""
 import ctypes
 
@@ -95,21 +96,17 @@ def test_gguf_text_roundtrip(tmp_path):
         s2x.lib.s2x_gguf_close(g)
 
 
-def test_gguf_f16_tensors_converted(tmp_path):
-    """An F16 ffn_down (K = F, unpadded) is quantized on load with ggml's Q8_0
-    rule and K zero-padded to F_pad; an F16 LayerNorm weight is widened."""
-    hm = synth.vision_model(SMALL_V, seed=33)
+def test_gguf_f16_ffn_down_kept(tmp_path):
+    """A converter-made q8_0 file stores every ffn_down (K = 4304 here F, not
+    a multiple of 32) as F16: the reader binds those bytes as F16 rows and
+    sets down_f16, as the reference's encoders keep the on-disk type; an F16
+    LayerNorm weight is widened exactly."""
+    hm = synth.vision_model(SMALL_V, seed=33, down_f16=True)
     kv, ts = vision_tensors(hm)
     c = SMALL_V
-    H, F, Fp = c.hidden, c.inter, c.inter_pad
-    rng = np.random.default_rng(5)
-    w16 = (rng.standard_normal((H, F)) * 0.02).astype(np.float16)
-    w16[0, :32] = 0                      # an all-zero block: d = 0, q = 0
-    w16[1, 5] = np.float16(65504.0)      # the largest fp16
-    ln16 = (1 + 0.02 * rng.standard_normal(H)).astype(np.float16)
+    H, F = c.hidden, c.inter
+    ln16 = (1 + 0.02 * np.random.default_rng(5).standard_normal(H)).astype(np.float16)
     for i, (name, t, ne, data) in enumerate(ts):
-        if name == "v.blk.0.ffn_down.weight":
-            ts[i] = (name, T_F16, [F, H], w16.tobytes())
         if name == "v.blk.1.ln1.weight":
             ts[i] = (name, T_F16, [H], ln16.tobytes())
     path = tmp_path / "v16.gguf"
@@ -119,10 +116,64 @@ def test_gguf_f16_tensors_converted(tmp_path):
     try:
         w = s2x.VisionWeights()
         s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
-        want = synth.quantize_q8_0(w16.astype(np.float32), Fp)
-        assert _bytes(w.layers[0].down_w, want.nbytes) == want.tobytes()
+        assert w.down_f16 == 1
+        for l in range(c.n_layer):
+            assert _bytes(w.layers[l].down_w, 2 * H * F) == hm.layers[l]["down_w"].tobytes()
+        assert _bytes(w.hdown_w, 2 * H * F) == hm.tensors["hdown_w"].tobytes()
         got = np.frombuffer(_bytes(w.layers[1].ln1_w, 4 * H), np.float32)
         assert np.array_equal(got, ln16.astype(np.float32))
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_mixed_ffn_down_rejected(tmp_path):
+    # one F16 ffn_down among Q8_0 ones: no converter writes that
+    hm = synth.vision_model(SMALL_V, seed=35)
+    kv, ts = vision_tensors(hm)
+    H, F = SMALL_V.hidden, SMALL_V.inter
+    w16 = (np.random.default_rng(6).standard_normal((H, F)) * 0.02).astype(np.float16)
+    ts = [(n, T_F16, [F, H], w16.tobytes()) if n == "v.blk.1.ffn_down.weight" else (n, t, ne, d)
+          for n, t, ne, d in ts]
+    path = tmp_path / "mixed.gguf"
+    write_gguf(path, kv, ts)
+    st, g = _open(path)
+    assert st == 0
+    try:
+        w = s2x.VisionWeights()
+        assert s2x.lib.s2x_gguf_vision_weights(g, ctypes.byref(w)) == 2  # S2X_ERR_UNSUPPORTED
+        assert b"ffn_down types differ" in s2x.lib.s2x_last_error()
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_f16_f32_other_matrices_quantized(tmp_path):
+    """An F16 / F32 matrix other than ffn_down (a file converted to f16 or f32
+    throughout) is quantized on load with ggml's Q8_0 rule."""
+    hm = synth.vision_model(SMALL_V, seed=36)
+    kv, ts = vision_tensors(hm)
+    H = SMALL_V.hidden
+    rng = np.random.default_rng(7)
+    w16 = (rng.standard_normal((H, H)) * 0.02).astype(np.float16)
+    w16[0, :32] = 0                      # an all-zero block: d = 0, q = 0
+    w16[1, 5] = np.float16(65504.0)      # the largest fp16
+    w32 = (rng.standard_normal((H, H)) * 0.02).astype(np.float32)
+    for i, (name, t, ne, data) in enumerate(ts):
+        if name == "v.blk.0.attn_o.weight":
+            ts[i] = (name, T_F16, [H, H], w16.tobytes())
+        if name == "v.head.attn_o.weight":
+            ts[i] = (name, 0, [H, H], w32.tobytes())  # GGML_TYPE_F32
+    path = tmp_path / "v16o.gguf"
+    write_gguf(path, kv, ts)
+    st, g = _open(path)
+    assert st == 0, s2x.lib.s2x_last_error()
+    try:
+        w = s2x.VisionWeights()
+        s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+        assert w.down_f16 == 0
+        want = synth.quantize_q8_0(w16.astype(np.float32), H)
+        assert _bytes(w.layers[0].o_w, want.nbytes) == want.tobytes()
+        want = synth.quantize_q8_0(w32, H)
+        assert _bytes(w.ho_w, want.nbytes) == want.tobytes()
     finally:
         s2x.lib.s2x_gguf_close(g)
 

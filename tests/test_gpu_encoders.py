@@ -317,6 +317,77 @@ def test_so400m_text_5x64_vs_oracle(orc):
         t.close()
 
 
+def test_small_towers_f16_ffn_down(orc, tmp_path):
+    """ffn_down as F16 (the converter's layout for K % 32 != 0): both towers
+    against the oracle's F16 linear, batch / single invariance, and the
+    towers created from a GGUF file of that layout give the same bits."""
+    from gguf_util import text_tensors, vision_tensors, write_gguf
+    hm = synth.vision_model(SMALL_V, seed=24, down_f16=True)
+    v = Vision(hm)
+    try:
+        om = orc.vision_model(hm)
+        px = synth.pixels(2, 729, seed=25)
+        b = v.batch(px, 2, 27, 27, s2x.POOL_PROBE)
+        for i in range(2):
+            c = cos(b[i], orc.vision_encode(om, px[i * 729:(i + 1) * 729], 27, 27, pooling=1))
+            say(f"small vision F16 ffn_down image {i}: cosine {c:.7f}")
+            assert c >= 0.9999
+        assert np.array_equal(v.batch(px[729:], 1, 27, 27, s2x.POOL_PROBE)[0], b[1])
+        path = tmp_path / "v16.gguf"
+        write_gguf(path, *vision_tensors(hm))
+        g = ctypes.c_void_p()
+        s2x.call("s2x_gguf_open", str(path).encode(), ctypes.byref(g))
+        try:
+            w = s2x.VisionWeights()
+            s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+            assert w.down_f16 == 1
+            h = ctypes.c_void_p()
+            s2x.call("s2x_vision_create", ctypes.byref(w), ctypes.byref(h))
+        finally:
+            s2x.lib.s2x_gguf_close(g)
+        try:
+            pd = dev(px)
+            out = empty((2, SMALL_V.hidden), torch.float32)
+            s2x.call("s2x_vision_encode_batch_dev", h, ptr(pd), 2, 27, 27, s2x.POOL_PROBE, ptr(out))
+            assert np.array_equal(host(out), b)
+        finally:
+            s2x.lib.s2x_vision_destroy(h)
+    finally:
+        v.close()
+
+    hm = synth.text_model(SMALL_T, seed=26, down_f16=True)
+    t = Text(hm)
+    try:
+        om = orc.text_model(hm)
+        ids, _ = synth.text_tokens(3, 64, vocab=SMALL_T.vocab, seed=27)
+        b = t.batch(ids)
+        for i in range(3):
+            c = cos(b[i], orc.text_encode(om, ids[i]))
+            say(f"small text F16 ffn_down prompt {i}: cosine {c:.7f}")
+            assert c >= 0.9999
+            assert np.array_equal(t.encode(ids[i]), b[i])
+        path = tmp_path / "t16.gguf"
+        write_gguf(path, *text_tensors(hm))
+        g = ctypes.c_void_p()
+        s2x.call("s2x_gguf_open", str(path).encode(), ctypes.byref(g))
+        try:
+            w = s2x.TextWeights()
+            s2x.call("s2x_gguf_text_weights", g, ctypes.byref(w))
+            assert w.down_f16 == 1
+            h = ctypes.c_void_p()
+            s2x.call("s2x_text_create", ctypes.byref(w), ctypes.byref(h))
+        finally:
+            s2x.lib.s2x_gguf_close(g)
+        try:
+            out = np.empty((3, SMALL_T.proj), np.float32)
+            s2x.call("s2x_text_encode_batch", h, ids.ctypes.data, 64, 3, out.ctypes.data)
+            assert np.array_equal(out, b)
+        finally:
+            s2x.lib.s2x_text_destroy(h)
+    finally:
+        t.close()
+
+
 def test_small_towers_from_gguf_same_bits(tmp_path, small_vision):
     """Encoders created from a GGUF file (s2x_gguf_*) equal the ones created
     from the host structs, bit for bit."""

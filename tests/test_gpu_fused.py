@@ -288,3 +288,62 @@ def test_residual_epilogues_h1152(orc, weights, kind, M):
     rows = np.arange(M) if M <= 729 else _rows(M, 32, 39)
     rq, rd = orc.quantize_q8_1(x[rows], K_pad)
     assert_same(mm[rows], orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd), f"GEMM rows M={M}")
+
+
+# --------------------------------------------- F16 weights (ffn_down) -------
+def _f16_terms_abs(w16, x):
+    xh = np.abs(x.astype(np.float16).astype(np.float64))
+    return xh @ np.abs(w16.astype(np.float64)).T
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("M", [1, 333, 729, 32 * 729])
+def test_mul_mat_f16_matches_oracle(orc, M):
+    # the converter's F16 ffn_down: K = 4304 (not a multiple of 32), N = 1152
+    from gpu_util import h5_rel
+    K, N = INTER, H
+    rng = np.random.default_rng(50)
+    w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    say(f"F16 mul_mat M={M}")
+    wd, xd = dev(w16.view(np.uint16)), dev(x)
+    wsb = s2x.lib.s2x_mul_mat_f16_workspace_size(K, N, M)
+    ws = empty((wsb,), torch.uint8)
+    y = empty((M, N), torch.float32)
+    s2x.call("s2x_mul_mat_f16_f32", ptr(wd), K, N, ptr(xd), K, M, ptr(y), ptr(ws),
+             ctypes.c_size_t(wsb), stream())
+    yg = host(y)
+    rows = np.arange(M) if M <= 729 else _rows(M, 48, 51)
+    ref = orc.mul_mat_f16_f32(w16, x[rows])
+    rel = h5_rel(yg[rows], ref.astype(np.float64), _f16_terms_abs(w16, x[rows]))
+    say(f"  max rel err (tau = 1e-3 rms) {rel:.2e}")
+    assert rel <= 1e-4
+    assert s2x.lib.s2x_mul_mat_f16_f32(ptr(wd), K, N, ptr(xd), K, M, ptr(y), ptr(ws),
+                                       ctypes.c_size_t(wsb - 1), stream()) == 4
+
+
+@pytest.mark.parametrize("M", [729, 32 * 729])
+def test_gelu_f16_epilogue(orc, weights, M):
+    # fc1 with its output rounded to f16 for an F16 ffn_down: bit for bit
+    # f16(gelu(mm + b)) of the oracle, columns 4304..4319 zero
+    raw, N, K, K_pad, bias = weights["fc1"]
+    say(f"fc1 GELU->f16 epilogue M={M}")
+    x = np.random.default_rng(52).standard_normal((M, K)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)
+    bd = dev(bias)
+    h = torch.full((M, INTER_PAD), 7.0, dtype=torch.float16, device="cuda:0")
+    w = _weight(raw, K_pad, N)
+    try:
+        e = s2x.Epilogue()
+        e.kind, e.bias = s2x.EPI_GELU_F16, bd.data_ptr()
+        e.q_out, e.q_kpad = h.data_ptr(), INTER_PAD
+        s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, None, 0, ctypes.byref(e),
+                 stream())
+        hg = host(h)
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+    assert not hg[:, N:].view(np.uint16).any()
+    rows = np.arange(M) if M <= 729 else _rows(M, 48, 53)
+    rq, rd = orc.quantize_q8_1(x[rows], K_pad)
+    ref = orc.gelu(orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd) + bias).astype(np.float16)
+    assert_same(hg[rows, :N].view(np.uint16), ref.view(np.uint16), "GELU_F16 vs oracle")

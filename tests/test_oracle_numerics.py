@@ -203,6 +203,36 @@ def test_mul_mat_f32_pads_k(orc):
 
 
 # ------------------------------------------------------------ LN / GELU --
+def test_mul_mat_f16_integers_exact(orc):
+    # small integers: every f16 value, product and partial sum is exact, so
+    # the result is the integer dot product itself (a transposed operand or a
+    # dropped term cannot pass)
+    rng = np.random.default_rng(40)
+    M, N, K = 7, 9, 4304
+    x = rng.integers(-8, 9, (M, K)).astype(np.float32)
+    w = rng.integers(-8, 9, (N, K)).astype(np.float16)
+    y = orc.mul_mat_f16_f32(w, x)
+    assert np.array_equal(y, (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32))
+
+
+def test_mul_mat_f16_rounds_x_to_f16_and_sums_in_double(orc):
+    rng = np.random.default_rng(41)
+    M, N, K = 33, 20, 1000
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0, :4] = [1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11), 65520.0]  # ties; overflow
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    y = orc.mul_mat_f16_f32(w, x)
+    xh = x.astype(np.float16).astype(np.float64)  # numpy: round to nearest even
+    assert xh[0, 0] == 1.0 and xh[0, 1] == 1 + 2.0 ** -9 and np.isinf(xh[0, 3])
+    ref = xh @ w.astype(np.float64).T
+    fin = np.isfinite(ref)
+    assert not fin[0].any() and fin[1:].all()
+    # double sums in another order round to the same f32 but for rare ties
+    d = np.abs(y[fin].astype(np.float64) - ref[fin].astype(np.float32).astype(np.float64))
+    assert (d <= np.spacing(np.abs(ref[fin]).astype(np.float32))).all()
+    assert (y[fin] == ref[fin].astype(np.float32)).mean() > 0.999
+
+
 def test_layernorm_float64(orc):
     rng = np.random.default_rng(12)
     x = (rng.standard_normal((50, 1152)) * 3 + 0.5).astype(np.float32)
