@@ -32,6 +32,7 @@ os.environ.setdefault("OMP_PLACES", "cores")
 sys.path.insert(0, os.path.join(ROOT, "hbd-siglip2.cpp_amd"))
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
 KERNEL = ("k_gemm (Q8_0 x Q8_1 GEMM, 128x128 tiles of 8 waves, two workgroups per CU: int8 "
           "quants and scales by LDS DMA in 4-block stages, v_mfma_i32_32x32x32_i8 block dots, "
@@ -245,7 +246,8 @@ def bench_gemm_shapes(np, torch, s2x, synth, warm=20, iters=200):
     """Config 2: the four vision-layer GEMMs on their own, Q8_0 W (prepared
     once) x F32 X ~ N(0, 1): each iteration quantizes X to Q8_1 and runs the
     GEMM (one GGML_OP_MUL_MAT), timed per iteration with HIP events on the
-    stream both run on; at M = 729 and at the batch-32 row count."""
+    stream both run on; at M = 729 and at the batch-32 row count.  Plus the
+    F16 ffn_down of the reference's converter (s2x_mul_mat_f16_f32)."""
     st = torch.cuda.current_stream()
     sp = ctypes.c_void_p(st.cuda_stream)
     res = {}
@@ -294,6 +296,41 @@ def bench_gemm_shapes(np, torch, s2x, synth, warm=20, iters=200):
                                   "frac": round(tops / INT8_PEAK_TOPS, 4), "iters": n_it}
             log(f"bench: GEMM {lab} M={M}: {g50:.1f} us ({tops:.1f} TOPS, frac "
                 f"{tops / INT8_PEAK_TOPS:.3f}) + quantize {q50:.1f} us")
+        # ffn_down as the reference's converter stores it (F16, K = 4304): the
+        # whole drop-in op (weight rows padded, X rounded to f16, f16 MFMA
+        # GEMM), priced against the f16 dense peak
+        N, K = 1152, 4304
+        rng = np.random.default_rng(9)
+        w16 = torch.from_numpy((rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+                               .astype(np.float16).view(np.uint16)).to("cuda:0")
+        x = torch.randn(M, K, device="cuda:0")
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+        wsb = s2x.lib.s2x_mul_mat_f16_workspace_size(K, N, M)
+        ws = torch.empty((wsb,), dtype=torch.uint8, device="cuda:0")
+        a = [ctypes.c_void_p(t.data_ptr()) for t in (w16, x, y, ws)]
+
+        def mm16():
+            s2x.call("s2x_mul_mat_f16_f32", a[0], K, N, a[1], K, M, a[2], a[3],
+                     ctypes.c_size_t(wsb), sp)
+
+        n_it = iters if M <= 729 else iters // 4
+        for _ in range(warm):
+            mm16()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n_it)]
+        torch.cuda.synchronize()
+        for e0, e1 in ev:
+            e0.record(st)
+            mm16()
+            e1.record(st)
+        torch.cuda.synchronize()
+        us = pct([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev], 0.5)
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        res[f"fc2_f16_m{M}"] = {"M": M, "N": N, "K": K, "mul_mat_us_p50": round(us, 2),
+                                "tflops": round(tf, 1), "frac_f16": round(tf / F16_PEAK_TFLOPS, 4),
+                                "iters": n_it}
+        log(f"bench: F16 mul_mat fc2 M={M}: {us:.1f} us ({tf:.1f} TFLOP/s, frac of f16 peak "
+            f"{tf / F16_PEAK_TFLOPS:.3f})")
     return res
 
 

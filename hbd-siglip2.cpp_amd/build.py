@@ -87,9 +87,25 @@ def build(jobs=None, asm=False, verbose=True):
     return LIB
 
 
+DRIVER_SRC = os.path.join(ROOT, "tests", "cpp", "drop_in_driver.cpp")
+DRIVER = os.path.join(ROOT, "tests", "cpp", "drop_in_driver")
+
+
+def build_driver():
+    """The tests' C++ program over the drop-in classes (include/siglip2_*.h),
+    linked against libs2x.so like a user's program would be."""
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"), DRIVER_SRC,
+           "-L", HERE, "-ls2x", "-Wl,-rpath,$ORIGIN/../../hbd-siglip2.cpp_amd", "-o", DRIVER]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError("driver build failed:\n" + r.stdout + r.stderr)
+    return DRIVER
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--asm", action="store_true", help="keep the gfx950 assembly")
     a = ap.parse_args()
     print(build(a.jobs, a.asm))
+    print(build_driver())
