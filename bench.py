@@ -3,6 +3,7 @@ patches (27x27 grid, GEMM M = 23328), probe pooling, one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32]
                     [--cpu-images 3] [--cpu-threads T] [--no-cpu] [--no-extra]
+                    [--text | --preproc]
 
 A step = one encode of the whole batch with the pixels already resident in
 HBM.  Prints ONE JSON line.  `roofline` reports the dominant kernel (the
@@ -90,6 +91,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (a plain copy kernel "
                          "for calibrating HBM byte counters) and exit")
+    ap.add_argument("--text", action="store_true",
+                    help="instead of the vision tower: time the so400m text tower on 5 prompts "
+                         "x 64 tokens and print its own JSON line")
     ap.add_argument("--preproc", action="store_true",
                     help="instead of the tower: time the NaFlex front end (GPU resize + "
                          "patchify of a batch of RGB images) and print its own JSON line")
@@ -118,6 +122,17 @@ def main():
 
     if args.preproc:
         bench_preproc(args, np, torch, s2x)
+        return
+    if args.text:
+        t = bench_text(np, s2x, synth, warm=args.warmup, iters=args.steps)
+        print(json.dumps({
+            "metric": "ms per batch, SigLIP2 text tower Q8_0, 5 prompts x 64 tokens",
+            "value": t["ms_p50"], "unit": "ms", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": t["ms_p50"], "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seeded N(0,0.02) Q8_0 weights, uniform token ids)",
+            "config": {"workload": t["workload"], "global_batch": 5, "seq_len": 64,
+                       "parallelism": "single GPU"}, "text_5x64": t}), flush=True)
         return
 
     cfg = synth.SO400M_VISION
