@@ -166,6 +166,7 @@ constexpr int FA_VP = FA_KT + 8;       // V^T tile pitch (halves): 16-byte rows,
 constexpr int FA_ONES = 88;            // V^T padding row held at 1.0: O^T row 88 = sum of P
 constexpr int FA_STAGE = FA_KT * FA_KP + FA_DV * FA_VP;  // halves per buffer
 constexpr int FA_WAVES = 12;  // waves (32 queries each) per workgroup
+constexpr int FA_WAVES_SMALL = 4;  // the same for launches of few workgroups
 constexpr float P_SHIFT = 15.0f;  // log2 of the largest P of a row (<= 65504 as f16)
 
 template <bool P_SPLIT, int NW>
@@ -436,11 +437,16 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     if (L.d_pad != FA_DP || L.dv_pad != FA_DV || (L.d_head % 4) != 0) return hipErrorInvalidValue;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
     const float log2e = 1.4426950408889634f;
-    constexpr int NW = FA_WAVES;
+    // 12-wave workgroups fill the chip from 256 of them up (batch 32: 1,024);
+    // below that, 4-wave ones spread the same waves over 3x the CUs (batch
+    // 1: 96 workgroups instead of 32).  Each query's arithmetic is the same.
+    int NW = FA_WAVES;
+    if (((L.max_len + 32 * NW - 1) / (32 * NW)) * L.n_head * L.n_seg < 256) NW = FA_WAVES_SMALL;
     const int64_t n_qt = (L.max_len + 32 * NW - 1) / (32 * NW);
     const int64_t n_wg = n_qt * L.n_head * L.n_seg;
     if (n_wg > 0x7fffffff) return hipErrorInvalidValue;
-    auto kern = L.p_split ? k_attn<true, NW> : k_attn<false, NW>;
+    auto kern = NW == FA_WAVES ? (L.p_split ? k_attn<true, FA_WAVES> : k_attn<false, FA_WAVES>)
+                               : (L.p_split ? k_attn<true, FA_WAVES_SMALL> : k_attn<false, FA_WAVES_SMALL>);
     hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(64 * NW), 0, stream,
                        reinterpret_cast<const _Float16 *>(base + L.q_off),
                        reinterpret_cast<const _Float16 *>(base + L.k_off),

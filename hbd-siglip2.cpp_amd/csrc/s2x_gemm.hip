@@ -21,7 +21,9 @@
 //
 // Work decomposition.  128 x 128 output tiles, one per workgroup of 8 waves
 // (each 32 x 64: 2 subtiles), two workgroups per CU so that one's epilogue
-// and pipeline fill overlap the other's K loop.  The K loop runs over
+// and pipeline fill overlap the other's K loop.  GEMMs of too few such tiles
+// to give every CU two (batch 1, M = 729) run 64 x 128 tiles of 4 waves
+// whose K stages are scheduled for a lone wave's latency instead.  The K loop runs over
 // stages of KS blocks whose operands (X and W quants and scales) arrive by
 // LDS DMA (buffer_load ... lds) into a ring of NS stage buffers, NS - 1
 // stages ahead; one workgroup barrier per stage.
@@ -52,14 +54,20 @@ constexpr int GM = 8;    // tile-row group of the tile order
 constexpr int WSB = BN * 2 + 80;  // W scales of a block: BN fp16 values, then 80 zero bytes
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-// 128 x 128 tiles, 8 waves of 32 x 64 outputs; stages of KS K blocks in a
-// ring of NS stage buffers (NS - 1 stages in flight).  Two workgroups per
-// CU when two rings fit in the LDS (then 4 waves per SIMD, <= 128 VGPRs),
-// else one (2 waves per SIMD).
-template <int KS_, int NS_>
+// BM x 128 tiles (BM 128 or 64), BM / 16 waves of 32 x 64 outputs (BM / 32
+// along M, 2 along N); stages of KS K blocks in a ring of NS stage buffers
+// (NS - 1 stages in flight).  Throughput form (LAT false): as many
+// workgroups per CU as two rings allow, each K block its own scheduling
+// region, <= 128 VGPRs (4 waves per SIMD cover each other's latency).
+// Latency form (LAT true, for GEMMs of too few tiles to give a SIMD more
+// than one or two waves): a stage's KS blocks are one scheduling region --
+// all their fragments read up front, their MFMAs interleaved -- with up to
+// 256 VGPRs, so that a lone wave keeps its matrix pipe busy.
+template <int KS_, int NS_, int BM_ = 128, bool LAT_ = false>
 struct Cfg {
-    static constexpr int TM = 1, BM = 128, KS = KS_, NS = NS_;
-    static constexpr int NWAVE = 8, NT = NWAVE * WAVE;
+    static constexpr int TM = 1, BM = BM_, KS = KS_, NS = NS_;
+    static constexpr bool LAT = LAT_;
+    static constexpr int NWAVE = BM / 16, NT = NWAVE * WAVE;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
     static constexpr int XS = WQ + KS * BN * 32;  // [KS][BM] u32 X ds words
@@ -67,18 +75,22 @@ struct Cfg {
     static constexpr int STAGE = WS + KS * WSB;
     static constexpr int LDS_BYTES = NS * STAGE;
     static constexpr int WG_PER_CU = 2 * LDS_BYTES <= 163840 ? 2 : 1;
-    static constexpr int WPE = WG_PER_CU * NWAVE / 4;  // waves per SIMD
-    // DMA instructions per stage and wave: QPW X-quant and QPW W-quant (each
-    // 32 rows of one block: 4 KS per stage over 8 waves), SPW X-scale (64
-    // rows of one block: 2 KS per stage) and 1 W-scale (one block: KS per
-    // stage); where a stage has fewer than 8 of a kind, waves w and w + 8 / n
-    // fetch the same bytes to the same place, so every wave issues the same
-    // count
-    static constexpr int QPW = KS / 2, SPW = KS >= 4 ? KS / 4 : 1;
-    static constexpr int DMA_N = 2 * QPW + SPW + 1;
+    static constexpr int WPE = LAT ? 2 : WG_PER_CU * NWAVE / 4;  // waves per SIMD
+    // DMA instructions per stage and wave: QPX X-quant and QPW W-quant (each
+    // 32 rows of one block: KS BM / 32 and 4 KS per stage), SPW X-scale (64
+    // rows of one block: KS BM / 64 per stage) and 1 W-scale (one block: KS
+    // per stage); where a stage has fewer than NWAVE of a kind, waves w and
+    // w + NWAVE / n fetch the same bytes to the same place, so every wave
+    // issues the same count
+    static constexpr int NH = BM / 64;  // 64-row halves of a block's X rows
+    static constexpr int QPX = KS * (BM / 32) / NWAVE, QPW = KS * (BN / 32) / NWAVE;
+    static constexpr int SPW = KS * NH >= NWAVE ? KS * NH / NWAVE : 1;
+    static constexpr int DMA_N = QPX + QPW + SPW + 1;
     static_assert(KS == 2 || KS == 4, "stage of 2 or 4 blocks");
+    static_assert(BM == 128 || BM == 64, "tile rows");
+    static_assert(QPX >= 1 && QPW >= 1 && QPX <= KS && QPW <= KS, "DMA split");
     static_assert(NS >= 2 && (NS - 2) * DMA_N <= 63, "vmcnt range");
-    static_assert(LDS_BYTES <= 163840, "LDS");
+    static_assert(LDS_BYTES * WG_PER_CU <= 163840, "LDS");
     static_assert(NWAVE * 5120 <= LDS_BYTES, "epilogue scratch");
 };
 
@@ -421,19 +433,22 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 
     // Per-lane DMA source offsets (relative to the tile's first row / column;
     // the K position goes into the scalar offset).
-    //   X and W quants, instructions t < QPW: i = QPW wave + t, block i % KS,
-    //             rows 32 (i / KS) .. + 31 (= 32 (wave / 2) for every t)
-    //   X scales, instructions t < SPW: i = (SPW wave + t) % (2 KS), block
-    //             i / 2, rows 64 (i % 2) .. + 63 (one ds word per lane)
+    //   X quants, instructions t < QPX: i = QPX wave + t, block i % KS, rows
+    //             32 (i / KS) .. + 31 (= 32 (QPX wave / KS) for every t)
+    //   W quants, instructions t < QPW: likewise with QPW
+    //   X scales, instructions t < SPW: i = (SPW wave + t) % (NH KS), block
+    //             i / NH, rows 64 (i % NH) .. + 63 (one ds word per lane)
     //   W scales: block wave % KS, columns 2 lane, 2 lane + 1
-    uint32_t vq, vxs[C::SPW];
+    uint32_t vqx, vqw, vxs[C::SPW];
     {
-        const int r = 32 * (wave >> 1) + (lane >> 1);
-        vq = (uint32_t)(r * row_bytes) + (uint32_t)(((lane & 1) ^ swz(r)) * 16);
+        const int rx = 32 * (C::QPX * wave / KS) + (lane >> 1);
+        vqx = (uint32_t)(rx * row_bytes) + (uint32_t)(((lane & 1) ^ swz(rx)) * 16);
+        const int rw = 32 * (C::QPW * wave / KS) + (lane >> 1);
+        vqw = (uint32_t)(rw * row_bytes) + (uint32_t)(((lane & 1) ^ swz(rw)) * 16);
 #pragma unroll
         for (int t = 0; t < C::SPW; ++t) {
-            const int i = (C::SPW * wave + t) % (2 * KS);
-            vxs[t] = (uint32_t)(((i & 1) * 64 + lane) * ld_ds * 4);
+            const int i = (C::SPW * wave + t) % (C::NH * KS);
+            vxs[t] = (uint32_t)(((i % C::NH) * 64 + lane) * ld_ds * 4);
         }
     }
     const __amdgpu_buffer_rsrc_t xr_live = __builtin_amdgcn_make_buffer_rsrc(
@@ -458,19 +473,19 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         uint8_t *sb = lds + (g % NS) * STAGE;
         const uint32_t k0 = (uint32_t)(g * KS);
 #pragma unroll
-        for (int t = 0; t < C::QPW; ++t) {
-            const int i = C::QPW * wave + t, j = i % KS;
-            dma16(xr, vq, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
+        for (int t = 0; t < C::QPX; ++t) {
+            const int i = C::QPX * wave + t, j = i % KS;
+            dma16(xr, vqx, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
         }
 #pragma unroll
         for (int t = 0; t < C::QPW; ++t) {
             const int i = C::QPW * wave + t, j = i % KS;
-            dma16(wr, vq, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
+            dma16(wr, vqw, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
         }
 #pragma unroll
         for (int t = 0; t < C::SPW; ++t) {
-            const int i = (C::SPW * wave + t) % (2 * KS), j = i >> 1;
-            dma4(xsr, vxs[t], (k0 + j) * 4, sb + XS + j * BM * 4 + (i & 1) * 256);
+            const int i = (C::SPW * wave + t) % (C::NH * KS), j = i / C::NH;
+            dma4(xsr, vxs[t], (k0 + j) * 4, sb + XS + j * BM * 4 + (i % C::NH) * 256);
         }
         dma4(wsr, (uint32_t)lane * 4, (uint32_t)((k0 + wave % KS) * ldT * 2),
              sb + WS + (wave % KS) * WSB);
@@ -565,8 +580,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], S[r], acc[a][b][r]);
             }
         }
-        // one scheduling region per block: nothing moves across blocks
-        __builtin_amdgcn_sched_barrier(0);
+        // throughput form: one scheduling region per block, nothing moves
+        // across blocks
+        if constexpr (!C::LAT) __builtin_amdgcn_sched_barrier(0);
     };
 
     // the zero pads after each block's W scales (never written by the DMA)
@@ -599,10 +615,24 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     for (int g = 0; g < n_st - 1; ++g) {
         const uint8_t *sb = lds + (g % NS) * STAGE;
         const int kb0 = g * KS;
-        static_for<KS>([&](auto jc) {
-            load_frag(sb, jc, F);
-            compute(F, kb0 + decltype(jc)::value);
-        });
+        if constexpr (C::LAT) {
+            // every fragment of the stage first, then its blocks in order
+            Frag<TM> Fs[KS];
+            static_for<KS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+#pragma unroll
+                for (int a = 0; a < TM; ++a) Fs[j].sx[a] = v2i{0, 0};
+#pragma unroll
+                for (int b = 0; b < 2; ++b) Fs[j].sw[b] = v2i{0, 0};
+                load_frag(sb, jc, Fs[j]);
+            });
+            static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value); });
+        } else {
+            static_for<KS>([&](auto jc) {
+                load_frag(sb, jc, F);
+                compute(F, kb0 + decltype(jc)::value);
+            });
+        }
         arrive(g + 1);
     }
     {
@@ -803,11 +833,20 @@ hipError_t run_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16
 
 }  // namespace gemm
 
-// Stage configuration: 4-block stages, a ring of 2, two workgroups per CU.
-// (A ring of 8 two-block stages at one workgroup per CU, for GEMMs of too
-// few tiles to fill the chip, measured 5-13 % slower at M = 729: their time
-// is the waves' own operand-to-result latency, not the fetch latency.)
+// Stage configurations: 4-block stages in a ring of 2.  Wide: 128 x 128
+// tiles, two workgroups per CU, for GEMMs of enough tiles to fill the chip.
+// Small: 64 x 128 tiles in the latency form, for GEMMs of fewer 128 x 128
+// tiles than two per CU (M = 729: batch 1).  Each output's K order is the
+// same in both, so the choice does not change a bit.  At M = 729 the small
+// form takes out from 19.8 to 14.6 us and fc2 from 58.7 to 42.5 us; rings
+// of 3 or 4 stages, 2-block stages and an imposed MFMA / VALU alternation
+// measured slower.
 using Wide = gemm::Cfg<4, 2>;
+using Small = gemm::Cfg<4, 2, 64, true>;
+
+static bool use_small(int64_t M, int64_t N) {
+    return ((M + 127) / 128) * ((N + 127) / 128) < 2 * 256;
+}
 
 hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
                        int64_t M, float *y, int64_t ldy, const EpiParams &epi,
@@ -821,7 +860,9 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
         (int64_t)C::BM * KB * QK > 0x7fffffff || w.ldT * KB * 2 > 0x7fffffff ||
         C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff)
         return hipErrorInvalidValue;
-#define S2X_RUN(E) gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream)
+#define S2X_RUN(E)                                                                    \
+    (use_small(M, w.N) ? gemm::run<Small, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
+                       : gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream))
     switch (epi.kind) {
     case EPI_NONE: return S2X_RUN(EPI_NONE);
     case EPI_BIAS: return S2X_RUN(EPI_BIAS);

@@ -207,16 +207,17 @@ __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
     float *__restrict__ y, int64_t ldy, int vec4) {
     __shared__ __align__(16) float sw[NIT * 256], sb[NIT * 256];
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * 4;
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // the first row's loads in flight before w and b are staged
+    float v[NIT][4];
+    ln_load_row<NIT>(v, x + row * ldx, H, lane, row < M, vec4);
     for (int i = threadIdx.x; i < H; i += 256) {
         sw[i] = w ? w[i] : 1.0f;
         sb[i] = b ? b[i] : 0.0f;
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int64_t stride = (int64_t)gridDim.x * 4;
-    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    float v[NIT][4];
-    ln_load_row<NIT>(v, x + row * ldx, H, lane, row < M, vec4);
     for (; row < M; row += stride) {  // wave-uniform
         float vn[NIT][4];
         const int64_t next = row + stride;
