@@ -23,10 +23,10 @@
 // (each 32 x 64: 2 subtiles), two workgroups per CU so that one's epilogue
 // and pipeline fill overlap the other's K loop.  GEMMs of too few such tiles
 // to give every CU two (batch 1, M = 729) run 64 x 128 tiles of 4 waves
-// whose K stages are scheduled for a lone wave's latency instead.  The K loop runs over
-// stages of KS blocks whose operands (X and W quants and scales) arrive by
-// LDS DMA (buffer_load ... lds) into a ring of NS stage buffers, NS - 1
-// stages ahead; one workgroup barrier per stage.
+// whose K stages are scheduled for a lone wave's latency instead.  The K
+// loop runs over stages of KS blocks whose operands (X and W quants and
+// scales) arrive by LDS DMA (buffer_load ... lds) into a ring of NS stage
+// buffers, NS - 1 stages ahead; one workgroup barrier per stage.
 //
 // Scale layouts: X scales are the Q8_1 ds words of the activation
 // (ds[m * ld_ds + kb] = fp16 d | fp16 s << 16, the block_q8_1 scale pair);
