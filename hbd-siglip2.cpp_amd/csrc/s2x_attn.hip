@@ -551,49 +551,89 @@ __global__ __launch_bounds__(64) void k_attn_f64(
 }
 
 // The same arithmetic for segments of at most 64 tokens (the text prompts),
-// spread over a workgroup of 256 lanes per (head, segment) instead of one
+// spread over a workgroup of 1,024 lanes per (head, segment) instead of one
 // lane per query: each score, each query's maximum, sum and each output
 // element keeps its own sequential order (the keys ascending, d ascending),
 // so the results are the bits of k_attn_f64; only independent sums run side
-// by side.  Q, K, V are staged as f16 (rows of 74 halves: consecutive rows
-// start 37 dwords apart, so a wave reading one d of 64 rows spreads over
-// the banks), the scores and then the probabilities as doubles.
-constexpr int A64S_P = 74;
+// by side.  Q, K, V are staged as the doubles of their f16 values (rows of
+// 73 doubles: consecutive rows start 146 dwords apart, so a wave reading one
+// d of 64 rows touches distinct banks), the scores and then the
+// probabilities as doubles, all in dynamic LDS; no conversion in the inner
+// loops, and a thread tests each probability against zero once for all of
+// its output columns.
+constexpr int A64S_P = 73;
+constexpr int A64S_LDS = (3 * A64_T * A64S_P + A64_T * (A64_T + 1) + 2 * A64_T) * 8;
+constexpr int A64S_NT = 1024;                // threads per workgroup
+constexpr int A64S_C = (A64S_P - 1 + 15) / 16;  // PV columns per thread (d_head <= 72)
 
-__global__ __launch_bounds__(256) void k_attn_f64_short(
+__global__ __launch_bounds__(A64S_NT) void k_attn_f64_short(
     const float *__restrict__ qkv, int64_t ld, const float *__restrict__ bias,
     const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len,
     const uint8_t *__restrict__ key_valid, int n_head, int d_head, double scale,
     float *__restrict__ out, int64_t ld_out) {
-    __shared__ _Float16 qs[A64_T][A64S_P], ks[A64_T][A64S_P], vs[A64_T][A64S_P];
-    __shared__ double S[A64_T][A64_T + 1];
-    __shared__ double mx_s[A64_T], den_s[A64_T];
+    extern __shared__ __align__(16) double a64s[];
+    double(*qs)[A64S_P] = reinterpret_cast<double(*)[A64S_P]>(a64s);
+    double(*ks)[A64S_P] = qs + A64_T;
+    double(*vs)[A64S_P] = ks + A64_T;
+    double(*S)[A64_T + 1] = reinterpret_cast<double(*)[A64_T + 1]>(vs + A64_T);
+    double *mx_s = &S[A64_T][0], *den_s = mx_s + A64_T;
     const int h = blockIdx.x, sg = blockIdx.y;
     const int len = seg_len[sg];
+    if (len <= 0) return;  // whole workgroup: nothing to write
     const int64_t row0 = seg_start[sg];
     const int H = n_head * d_head;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < A64_T * d_head; i += 256) {
-        const int p = i / d_head, d = i % d_head;
-        float q = 0.0f, k = 0.0f, v = 0.0f;
-        if (p < len) {
-            const float *r = qkv + (row0 + p) * ld + h * d_head + d;
-            q = r[0] + bias[h * d_head + d];
-            k = r[H] + bias[H + h * d_head + d];
-            v = r[2 * H] + bias[2 * H + h * d_head + d];
+    // staging: thread t takes column t % d_head of rows t / d_head + s k
+    // (s = A64S_NT / d_head row groups); every load is issued up front and
+    // unconditionally (rows past the segment read its last row, then store
+    // zeros)
+    {
+        const int s_rows = A64S_NT / d_head;
+        if (tid < s_rows * d_head) {
+            const int d = tid % d_head, p0 = tid / d_head;
+            const float bq = bias[h * d_head + d], bk = bias[H + h * d_head + d];
+            const float bv = bias[2 * H + h * d_head + d];
+            const float *col = qkv + row0 * ld + h * d_head + d;
+            constexpr int NR = (A64_T + A64S_NT / 72 - 1) / (A64S_NT / 72);  // rows per thread
+            float q[NR], k[NR], v[NR];
+#pragma unroll
+            for (int u = 0; u < NR; ++u) {
+                const float *r = col + (int64_t)min(p0 + u * s_rows, len - 1) * ld;
+                q[u] = r[0];
+                k[u] = r[H];
+                v[u] = r[2 * H];
+            }
+#pragma unroll
+            for (int u = 0; u < NR; ++u) {
+                const int p = p0 + u * s_rows;
+                if (p < A64_T) {
+                    const bool in = p < len;
+                    qs[p][d] = in ? (double)(float)f32_to_f16(q[u] + bq) : 0.0;
+                    ks[p][d] = in ? (double)(float)f32_to_f16(k[u] + bk) : 0.0;
+                    vs[p][d] = in ? (double)(float)f32_to_f16(v[u] + bv) : 0.0;
+                }
+            }
         }
-        qs[p][d] = f32_to_f16(q);
-        ks[p][d] = f32_to_f16(k);
-        vs[p][d] = f32_to_f16(v);
     }
     __syncthreads();
-    // scores: wave w takes queries w, w + 4, ..., lane j the key j
+    // scores: wave w takes queries w + 16 u (u < 4), lane j the key j: four
+    // independent sums (each in d order) share one read of the key's row
     const bool key_ok = lane < len && (key_valid == nullptr || key_valid[row0 + lane] != 0);
-    for (int q = wave; q < len; q += 4) {
-        double acc = 0.0;
-        for (int d = 0; d < d_head; ++d)
-            acc = acc + (double)(float)qs[q][d] * (double)(float)ks[lane][d];
-        S[q][lane] = key_ok ? acc * scale : -INFINITY;
+    static_assert(A64S_NT / 64 * 4 == A64_T, "one query group per wave");
+    if (wave < len) {
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+        int qi[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) qi[u] = wave + 16 * u;
+#pragma unroll 8
+        for (int d = 0; d < d_head; ++d) {
+            const double k = ks[lane][d];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] = acc[u] + qs[qi[u]][d] * k;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (qi[u] < len) S[qi[u]][lane] = key_ok ? acc[u] * scale : -INFINITY;
     }
     __syncthreads();
     if (tid < len) {
@@ -602,7 +642,7 @@ __global__ __launch_bounds__(256) void k_attn_f64_short(
         mx_s[tid] = m;
     }
     __syncthreads();
-    for (int i = tid; i < len * A64_T; i += 256) {
+    for (int i = tid; i < len * A64_T; i += A64S_NT) {
         const int q = i >> 6, j = i & 63;
         if (j < len) {
             const double sc = S[q][j];
@@ -616,14 +656,34 @@ __global__ __launch_bounds__(256) void k_attn_f64_short(
         den_s[tid] = den;
     }
     __syncthreads();
-    for (int i = tid; i < len * d_head; i += 256) {
-        const int q = i / d_head, d = i % d_head;
-        double acc = 0.0;
-        for (int j = 0; j < len; ++j) {
-            const double p = S[q][j];
-            if (p != 0.0) acc = acc + p * (double)(float)vs[j][d];
+    // PV: thread t takes query t / 16 and the columns d = t % 16 + 16 c, so
+    // a probability read once serves A64S_C outputs
+    {
+        const int q = tid >> 4, d0 = tid & 15;
+        double acc[A64S_C];
+#pragma unroll
+        for (int c = 0; c < A64S_C; ++c) acc[c] = 0.0;
+        if (q < len) {
+#pragma unroll 2
+            for (int j = 0; j < len; ++j) {
+                const double p = S[q][j];
+                // the row's values first (one wait for all of them); columns
+                // d_head .. are padding or the next row: computed, not stored
+                double vv[A64S_C];
+#pragma unroll
+                for (int c = 0; c < A64S_C; ++c) vv[c] = vs[j][d0 + 16 * c];
+                if (p != 0.0) {
+#pragma unroll
+                    for (int c = 0; c < A64S_C; ++c) acc[c] = acc[c] + p * vv[c];
+                }
+            }
+            float *orow = out + (row0 + q) * ld_out + h * d_head;
+#pragma unroll
+            for (int c = 0; c < A64S_C; ++c) {
+                const int d = d0 + 16 * c;
+                if (d < d_head) orow[d] = (float)(acc[c] / den_s[q]);
+            }
         }
-        out[(row0 + q) * ld_out + h * d_head + d] = (float)(acc / den_s[q]);
     }
 }
 
@@ -634,9 +694,17 @@ hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bi
                            int64_t ld_out, hipStream_t stream) {
     if (n_seg == 0) return hipSuccess;
     if (d_head > A64_DMAX) return hipErrorInvalidValue;
-    if (max_len <= A64_T && d_head <= A64S_P - 2) {
-        hipLaunchKernelGGL(k_attn_f64_short, dim3((unsigned)n_head, (unsigned)n_seg), dim3(256), 0,
-                           stream, qkv, ld_qkv, qkv_bias, seg_start, seg_len, key_valid, (int)n_head,
+    if (max_len <= A64_T && d_head < A64S_P) {
+        static bool attr_set = false;  // idempotent; a racing second call repeats it
+        if (!attr_set) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_f64_short),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     A64S_LDS);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(k_attn_f64_short, dim3((unsigned)n_head, (unsigned)n_seg),
+                           dim3(A64S_NT), A64S_LDS, stream, qkv, ld_qkv, qkv_bias, seg_start, seg_len, key_valid, (int)n_head,
                            (int)d_head, (double)scale, out, ld_out);
         return hipGetLastError();
     }
