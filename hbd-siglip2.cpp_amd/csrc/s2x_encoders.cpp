@@ -85,6 +85,11 @@ struct DevBuf {
     template <class T> T *as() const { return reinterpret_cast<T *>(p); }
 };
 
+// Encodes of at most this many packed rows run as HIP graph replays, of up
+// to GRAPH_CACHE distinct shapes per encoder.
+constexpr int64_t GRAPH_MAX_ROWS = 8192;
+constexpr size_t GRAPH_CACHE = 4;
+
 // Grow a device buffer; waits for `stream` before releasing the old one.
 int ensure(DevBuf &b, size_t bytes, hipStream_t stream) {
     if (b.n >= bytes && b.p) return S2X_OK;
@@ -223,10 +228,71 @@ struct Tower {
     // attention in fp64 (k_attn_f64, from an f32 QKV GEMM output) instead of
     // the f16-MFMA flash kernel fed by the QKV GEMM's attention-layout epilogue
     bool attn_f64 = false;
+    // HIP graphs of recent encodes' launch sequences (see launch_seq)
+    bool graphs = true;
+    struct GraphEntry {
+        std::vector<int64_t> key;
+        hipGraphExec_t exec = nullptr;  // null: seen once, not captured yet
+    };
+    std::vector<GraphEntry> gcache;  // most recently used last
 
     ~Tower() {
+        for (auto &g : gcache)
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
         for (auto &L : layers) L.release();
         if (own) (void)hipStreamDestroy(own);
+    }
+
+    // Launch-bound encodes (M <= GRAPH_MAX_ROWS: batch 1, text prompts) run
+    // ~250 short kernels whose launch gaps are a large share of the time.
+    // body() issues an encode's kernels on `stream` and nothing else (no
+    // allocation, copy from host memory or synchronisation: every buffer it
+    // uses is already sized).  The first call with a given key runs body()
+    // as it is; the second call with that key captures body() into a HIP
+    // graph and launches it; later calls replay the graph.  Up to
+    // GRAPH_CACHE keys are kept (least recently used dropped), as the
+    // reference's encoders cache one graph per shape.  The key holds every
+    // size and device address the kernels take (the caller's and the
+    // tower's buffers), so a replay launches exactly the kernels, arguments
+    // and order that body() would.
+    template <class Body>
+    int launch_seq(std::vector<int64_t> key, int64_t M, Body &&body) {
+        if (!graphs || timing.on || M > GRAPH_MAX_ROWS || stream == nullptr) return body();
+        for (const DevBuf *b : {&x, &qs, &ds, &qs2, &ds2, &h16, &qkv, &att, &attn_ws, &seg, &rowmap})
+            key.push_back((int64_t)(uintptr_t)b->p);
+        key.push_back((int64_t)(uintptr_t)stream);
+        key.push_back(attn_f64);
+        size_t i = 0;
+        while (i < gcache.size() && gcache[i].key != key) ++i;
+        if (i == gcache.size()) {  // first call with this key
+            if (gcache.size() >= GRAPH_CACHE) {
+                if (gcache.front().exec) {
+                    S2X_HIP_TRY(hipStreamSynchronize(stream));
+                    (void)hipGraphExecDestroy(gcache.front().exec);
+                }
+                gcache.erase(gcache.begin());
+            }
+            gcache.push_back({key, nullptr});
+            return body();
+        }
+        GraphEntry g = gcache[i];
+        gcache.erase(gcache.begin() + (long)i);
+        if (!g.exec) {
+            S2X_HIP_TRY(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+            const int st = body();
+            hipGraph_t gr = nullptr;
+            const hipError_t e = hipStreamEndCapture(stream, &gr);
+            if (st != S2X_OK || e != hipSuccess) {
+                if (gr) (void)hipGraphDestroy(gr);
+                return st != S2X_OK ? st : hip_fail(e, "graph capture");
+            }
+            const hipError_t ei = hipGraphInstantiate(&g.exec, gr, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(gr);
+            if (ei != hipSuccess) return hip_fail(ei, "graph instantiate");
+        }
+        gcache.push_back(g);
+        S2X_HIP_TRY(hipGraphLaunch(g.exec, stream));
+        return S2X_OK;
     }
 
     int init_stream() {
@@ -498,6 +564,18 @@ struct s2x_vision {
         return S2X_OK;
     }
 
+    // launch_seq key of an encode: its path, sizes, the device addresses it
+    // reads and writes, and the vision tower's own buffers
+    std::vector<int64_t> seq_key(int64_t path, int64_t M, int64_t n_img, int64_t max_len,
+                                 int32_t pooling, const void *in, const void *out_dev,
+                                 const void *pos) const {
+        std::vector<int64_t> k{path, M, n_img, max_len, pooling, (int64_t)(uintptr_t)in,
+                               (int64_t)(uintptr_t)out_dev, (int64_t)(uintptr_t)pos};
+        for (const DevBuf *b : {&pix, &pos_packed, &kv, &hq, &ha, &hid})
+            k.push_back((int64_t)(uintptr_t)b->p);
+        return k;
+    }
+
     // After the packed, position-embedded patch rows are in t.x: the blocks,
     // post-LN and pooling into out_dev [n_img][H].
     int tail(int64_t M, int64_t n_img, int64_t max_len, int32_t pooling, float *out_dev) {
@@ -638,6 +716,12 @@ int s2x_vision_set_attention_fp64(s2x_vision *v, int enable) {
     return S2X_OK;
 }
 
+int s2x_vision_set_graphs(s2x_vision *v, int enable) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    v->t.graphs = enable != 0;
+    return S2X_OK;
+}
+
 int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t n_img, int32_t n_h,
                                 int32_t n_w, int32_t pooling, float *out_dev) {
     if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
@@ -654,10 +738,12 @@ int s2x_vision_encode_batch_dev(s2x_vision *v, const float *pixels_dev, int32_t 
     S2X_TRY(t.set_segments(st, ln, M));
     const float *pos = nullptr;
     S2X_TRY(v->pos_for(n_h, n_w, &pos));
-    S2X_TRY(t.quantize(pixels_dev, v->patch_dim, M, v->patch_dim, v->patch_dim));
-    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
-                   EpiParams{EPI_BIAS_RESID, v->patch_b, pos, t.H, n_pos, 0}, v->patch_dim));
-    return v->tail(M, n_img, n_pos, pooling, out_dev);
+    return t.launch_seq(v->seq_key(1, M, n_img, n_pos, pooling, pixels_dev, out_dev, pos), M, [&] {
+        S2X_TRY(t.quantize(pixels_dev, v->patch_dim, M, v->patch_dim, v->patch_dim));
+        S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                       EpiParams{EPI_BIAS_RESID, v->patch_b, pos, t.H, n_pos, 0}, v->patch_dim));
+        return v->tail(M, n_img, n_pos, pooling, out_dev);
+    });
 }
 
 int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h, int32_t n_w,
@@ -711,11 +797,13 @@ int s2x_vision_encode_ragged_dev(s2x_vision *v, const float *pixels_dev,
                                    sizeof(float) * (size_t)(ln[(size_t)i] * t.H),
                                    hipMemcpyDeviceToDevice, t.stream));
     }
-    S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
-    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
-                   EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
-                   v->patch_dim));
-    return v->tail(M, n_img, max_len, pooling, out_dev);
+    return t.launch_seq(v->seq_key(2, M, n_img, max_len, pooling, nullptr, out_dev, nullptr), M, [&] {
+        S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
+        S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                       EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
+                       v->patch_dim));
+        return v->tail(M, n_img, max_len, pooling, out_dev);
+    });
 }
 
 int s2x_vision_encode_rgb_batch_dev(s2x_vision *v, const uint8_t *const *rgb_dev,
@@ -771,11 +859,13 @@ int s2x_vision_encode_rgb_batch_dev(s2x_vision *v, const uint8_t *const *rgb_dev
                                    sizeof(float) * (size_t)(ln[(size_t)i] * t.H),
                                    hipMemcpyDeviceToDevice, t.stream));
     }
-    S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
-    S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
-                   EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
-                   v->patch_dim));
-    return v->tail(M, n_img, max_len, pooling, out_dev);
+    return t.launch_seq(v->seq_key(2, M, n_img, max_len, pooling, nullptr, out_dev, nullptr), M, [&] {
+        S2X_TRY(t.quantize(v->pix.as<float>(), v->patch_dim, M, v->patch_dim, v->patch_dim));
+        S2X_TRY(t.gemm(v->patch, M, t.x.as<float>(), t.H,
+                       EpiParams{EPI_BIAS_RESID, v->patch_b, v->pos_packed.as<float>(), t.H, 0, 0},
+                       v->patch_dim));
+        return v->tail(M, n_img, max_len, pooling, out_dev);
+    });
 }
 
 int s2x_vision_gemm_timing(s2x_vision *v, int enable) {
@@ -826,21 +916,26 @@ struct s2x_text {
             last[(size_t)b] = b * n_tok + n_tok - 1;
         }
         S2X_TRY(t.set_segments(st, ln, M));
-        hipError_t e = launch_get_rows_q8_0(tok, H, vocab, ids.as<int32_t>(), M, pos_embd, n_tok,
-                                            t.x.as<float>(), t.stream);
-        if (e != hipSuccess) return hip_fail(e, "get_rows launch");
-        S2X_TRY(t.run_layers(M, n_batch, n_tok, key_valid_dev));
-        e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr,
-                             t.x.as<float>(), H, t.stream);
-        if (e != hipSuccess) return hip_fail(e, "final LN launch");
         S2X_TRY(ensure(rows, sizeof(int32_t) * (size_t)n_batch, t.stream));
         S2X_TRY(ensure(pooled, sizeof(float) * (size_t)(n_batch * H), t.stream));
         S2X_TRY(ensure(out, sizeof(float) * (size_t)(n_batch * proj), t.stream));
         S2X_HIP_TRY(hipMemcpyAsync(rows.p, last.data(), 4 * (size_t)n_batch, hipMemcpyHostToDevice, t.stream));
-        e = launch_gather_rows(t.x.as<float>(), H, rows.as<int32_t>(), n_batch, pooled.as<float>(), t.stream);
-        if (e != hipSuccess) return hip_fail(e, "gather launch");
-        S2X_TRY(t.quantize(pooled.as<float>(), H, n_batch, H, H));
-        S2X_TRY(t.gemm(head, n_batch, out.as<float>(), proj, EpiParams{EPI_BIAS, head_b, nullptr, 0, 0, 0}, H));
+        const std::vector<int64_t> key{3, n_tok, n_batch, (int64_t)(uintptr_t)key_valid_dev,
+                                       (int64_t)(uintptr_t)ids.p, (int64_t)(uintptr_t)rows.p,
+                                       (int64_t)(uintptr_t)pooled.p, (int64_t)(uintptr_t)out.p};
+        S2X_TRY(t.launch_seq(key, M, [&] {
+            hipError_t e = launch_get_rows_q8_0(tok, H, vocab, ids.as<int32_t>(), M, pos_embd, n_tok,
+                                                t.x.as<float>(), t.stream);
+            if (e != hipSuccess) return hip_fail(e, "get_rows launch");
+            S2X_TRY(t.run_layers(M, n_batch, n_tok, key_valid_dev));
+            e = launch_layernorm(t.x.as<float>(), H, M, H, fln_w, fln_b, t.eps, nullptr,
+                                 t.x.as<float>(), H, t.stream);
+            if (e != hipSuccess) return hip_fail(e, "final LN launch");
+            e = launch_gather_rows(t.x.as<float>(), H, rows.as<int32_t>(), n_batch, pooled.as<float>(), t.stream);
+            if (e != hipSuccess) return hip_fail(e, "gather launch");
+            S2X_TRY(t.quantize(pooled.as<float>(), H, n_batch, H, H));
+            return t.gemm(head, n_batch, out.as<float>(), proj, EpiParams{EPI_BIAS, head_b, nullptr, 0, 0, 0}, H);
+        }));
         S2X_HIP_TRY(hipMemcpyAsync(out_host, out.p, sizeof(float) * (size_t)(n_batch * proj),
                                    hipMemcpyDeviceToHost, t.stream));
         S2X_HIP_TRY(hipStreamSynchronize(t.stream));
@@ -924,6 +1019,12 @@ int s2x_text_set_stream(s2x_text *x, void *stream) {
 int s2x_text_set_attention_fp64(s2x_text *x, int enable) {
     if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
     x->t.attn_f64 = enable != 0;
+    return S2X_OK;
+}
+
+int s2x_text_set_graphs(s2x_text *x, int enable) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    x->t.graphs = enable != 0;
     return S2X_OK;
 }
 

@@ -379,6 +379,13 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream);
 /* Attention precision: 0 (default) = f16-MFMA flash attention with f32
  * softmax and an exact f16 hi/lo split of P; 1 = s2x_attn_fp64. */
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
+/* HIP graph replay of encodes of at most 8,192 packed rows (1 = default,
+ * 0 = plain launches).  The reference turns on ggml's CUDA graphs with one
+ * graph per shape in its encoders (CMakeLists.txt:59-64); here the second
+ * encode with the same sizes and buffers is captured into a HIP graph and
+ * later ones replay it (up to 4 shapes per encoder).  Results are the same
+ * bits either way. */
+int s2x_vision_set_graphs(s2x_vision *v, int enable);
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */
 int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h,
@@ -431,6 +438,8 @@ int s2x_text_set_stream(s2x_text *t, void *stream);
 /* Attention precision for the text tower: 1 (default) = s2x_attn_fp64 (the
  * oracle's arithmetic to within 1 ulp), 0 = the f16-MFMA flash kernel. */
 int s2x_text_set_attention_fp64(s2x_text *t, int enable);
+/* As s2x_vision_set_graphs, for the text tower. */
+int s2x_text_set_graphs(s2x_text *t, int enable);
 /* TextEncoder::encode: one prompt of n_tok ids (host), optional host mask
  * (1 = valid), out_host proj floats.  Synchronous. */
 int s2x_text_encode(s2x_text *t, const int32_t *ids_host, int32_t n_tok,

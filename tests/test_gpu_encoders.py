@@ -161,6 +161,59 @@ class Text:
         s2x.lib.s2x_text_destroy(self.h)
 
 
+def test_vision_graph_replays_match_eager(small_vision):
+    """Batch-size-1 encodes run as HIP graph replays from the second call
+    with the same shape and buffers on.  Every call -- the first (plain
+    launches), the capturing one and the replays, with another shape's
+    encodes (cached as a second graph), op-level work on torch's stream and
+    synchronisations between them -- gives the plain launches' bits."""
+    v, _ = small_vision
+    H = v.host.cfg.hidden
+    a = dev(synth.pixels(1, 27 * 27, seed=6000))
+    b = dev(synth.pixels(2, 16 * 16, seed=6001))
+    oa, ob = empty((1, H), torch.float32), empty((2, H), torch.float32)
+
+    def run_a():
+        s2x.call("s2x_vision_encode_batch_dev", v.h, ptr(a), 1, 27, 27, s2x.POOL_PROBE, ptr(oa))
+        return host(oa).copy()
+
+    def run_b():
+        s2x.call("s2x_vision_encode_batch_dev", v.h, ptr(b), 2, 16, 16, s2x.POOL_MEAN, ptr(ob))
+        return host(ob).copy()
+
+    s2x.call("s2x_vision_set_graphs", v.h, 0)
+    try:
+        ref_a, ref_b = run_a(), run_b()
+    finally:
+        s2x.call("s2x_vision_set_graphs", v.h, 1)
+    scratch = empty((1 << 20,), torch.float32)
+    for i in range(6):
+        oa.fill_(float("nan"))
+        ob.fill_(float("nan"))
+        assert np.array_equal(run_a(), ref_a), f"27x27 call {i}"
+        scratch.normal_()  # eager work on torch's stream between replays
+        assert np.array_equal(run_b(), ref_b), f"2 x 16x16 call {i}"
+        torch.cuda.synchronize()
+    say("vision: 6 rounds of two shapes, graph replays equal plain launches")
+
+
+def test_text_graph_replays_match_eager():
+    hm = synth.text_model(SMALL_T, seed=23)
+    t = Text(hm)
+    try:
+        rng = np.random.default_rng(24)
+        ids = rng.integers(0, SMALL_T.vocab, (3, 20)).astype(np.int32)
+        s2x.call("s2x_text_set_graphs", t.h, 0)
+        ref = t.batch(ids)
+        ref1 = t.encode(ids[0])
+        s2x.call("s2x_text_set_graphs", t.h, 1)
+        for i in range(5):
+            assert np.array_equal(t.batch(ids), ref), f"batch call {i}"
+            assert np.array_equal(t.encode(ids[0]), ref1), f"single call {i}"
+    finally:
+        t.close()
+
+
 @pytest.mark.parametrize("fp64", [0, 1])
 def test_small_text_vs_oracle(orc, fp64):
     # the flash (f16 MFMA) attention, the default, and the fp64 option
