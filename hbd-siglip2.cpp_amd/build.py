@@ -102,6 +102,27 @@ def build_driver():
     return DRIVER
 
 
+CLI_DIR = os.path.join(HERE, "cli")
+BIN = os.path.join(HERE, "bin")
+CLIS = {"siglip2-cli": "siglip2_cli.cpp", "siglip2-text-cli": "siglip2_text_cli.cpp"}
+
+
+def build_cli():
+    """The command-line encoders over the drop-in classes, into bin/."""
+    os.makedirs(BIN, exist_ok=True)
+    out = []
+    for name, src in CLIS.items():
+        exe = os.path.join(BIN, name)
+        cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"),
+               os.path.join(CLI_DIR, src), "-L", HERE, "-ls2x", "-Wl,-rpath,$ORIGIN/..",
+               "-o", exe]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(f"{name} build failed:\n" + r.stdout + r.stderr)
+        out.append(exe)
+    return out
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
@@ -109,3 +130,4 @@ if __name__ == "__main__":
     a = ap.parse_args()
     print(build(a.jobs, a.asm))
     print(build_driver())
+    print(build_cli())
