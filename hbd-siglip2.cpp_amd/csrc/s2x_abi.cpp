@@ -448,6 +448,34 @@ int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
     return e == hipSuccess ? S2X_OK : hip_fail(e, "attn launch");
 }
 
+int s2x_attn_run_q8_1(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
+                      const int32_t *seg_len_dev, const uint8_t *key_valid, int64_t n_seg,
+                      int64_t max_len, int64_t n_head, int64_t d_head, float scale,
+                      int64_t n_rows, void *qs, void *ds, int64_t ld_ds, float *out,
+                      int64_t ld_out, void *stream) {
+    int st = check_attn_shape(n_seg, max_len, n_head, d_head, "attn_run_q8_1");
+    if (st != S2X_OK) return st;
+    if (!attn_q81_fusable(n_head, d_head))
+        return fail(S2X_ERR_UNSUPPORTED, "attn_run_q8_1: needs d_head 72 and n_head %% 4 == 0");
+    if (n_seg == 0 || n_rows == 0) return S2X_OK;
+    const AttnLayout L = attn_layout(n_seg, max_len, n_head, d_head);
+    const int64_t H = n_head * d_head;
+    if (!ws || !seg_start_dev || !seg_len_dev || !out || !qs || !ds || n_rows < 0)
+        return fail(S2X_ERR_INVALID_ARG, "attn_run_q8_1: null pointer or negative rows");
+    if (ws_bytes < L.bytes) return fail(S2X_ERR_WORKSPACE, "attn_run_q8_1: workspace too small");
+    if (ld_out < H || ld_out % 4 != 0 || !aligned(out, 16) || ld_ds < H / 32 || !aligned(qs, 4) ||
+        !aligned(ds, 4))
+        return fail(S2X_ERR_INVALID_ARG,
+                    "attn_run_q8_1: out 16-byte aligned with ld_out %% 4 == 0, ld_ds >= H / 32");
+    Q81Out o;
+    o.qs = reinterpret_cast<int8_t *>(qs);
+    o.ds = reinterpret_cast<uint32_t *>(ds);
+    o.ld_ds = ld_ds;
+    hipError_t e = launch_attn(ws, seg_start_dev, seg_len_dev, key_valid, L, scale, out, ld_out,
+                               (hipStream_t)stream, &o, n_rows);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "attn launch");
+}
+
 int s2x_attn_fp64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                   const int32_t *seg_start_dev, const int32_t *seg_len_dev,
                   const uint8_t *key_valid, int64_t n_seg, int64_t max_len, int64_t n_head,

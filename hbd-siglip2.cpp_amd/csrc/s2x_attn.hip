@@ -151,6 +151,106 @@ hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_b
 }
 
 // ---------------------------------------------------------------------------
+// Q8_1 of the attention output, folded into the flash kernel for 72-wide
+// heads in groups of four (288 columns = 9 blocks of 32): head r = h % 4
+// owns whole blocks {0, 1}, {3}, {5}, {7, 8} of its group (r = 0 .. 3) and
+// quantizes them in its epilogue; blocks 2, 4, 6 straddle heads (r, r + 1),
+// so their columns are written as f32 and a second pass (k_quant_straddle)
+// quantizes them.  Both apply k_quantize_q8_1's arithmetic to the same f32
+// values: the same bits as quantizing the whole f32 output.
+// ---------------------------------------------------------------------------
+template <int M0>  // first 8-column group of the block within the head
+__device__ __forceinline__ void attn_q81_block(const v16f (&o)[3], float inv, int lh,
+                                               int8_t *qrow, uint32_t *dsrow, int kb) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * k + i] = o[(M0 + k) / 4][4 * ((M0 + k) % 4) + i] * inv;
+    // lane lh holds columns 8 m + 4 lh + 0..3 of each group m: the block is
+    // this lane's 16 values and lane l ^ 32's
+    float a = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
+    a = fmaxf(a, __shfl_xor(a, 32));
+    const float d = a / 127.0f;
+    const float qinv = a != 0.0f ? 127.0f / a : 0.0f;
+    int sq = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q0 = q8_round(v[4 * k], qinv), q1 = q8_round(v[4 * k + 1], qinv);
+        const int q2 = q8_round(v[4 * k + 2], qinv), q3 = q8_round(v[4 * k + 3], qinv);
+        *reinterpret_cast<uint32_t *>(qrow + 8 * (M0 + k) + 4 * lh) = pack4_i8(q0, q1, q2, q3);
+        sq += q0 + q1 + q2 + q3;
+    }
+    sq += __shfl_xor(sq, 32);
+    if (lh == 0)
+        dsrow[kb] = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)sq * d) << 16);
+}
+
+template <int M>  // an 8-column group written as f32 (part of a straddling block)
+__device__ __forceinline__ void attn_f32_group(const v16f (&o)[3], float inv, int lh, float *orow) {
+    const float4 v = make_float4(o[M / 4][4 * (M % 4)] * inv, o[M / 4][4 * (M % 4) + 1] * inv,
+                                 o[M / 4][4 * (M % 4) + 2] * inv, o[M / 4][4 * (M % 4) + 3] * inv);
+    *reinterpret_cast<float4 *>(orow + 8 * M + 4 * lh) = v;
+}
+
+// Epilogue of one query row for head position R = h % 4 within its group.
+template <int R>
+__device__ __forceinline__ void attn_q81_row(const v16f (&o)[3], float inv, int lh, float *orow,
+                                             int8_t *qrow, uint32_t *dsrow, int kb0) {
+    if constexpr (R == 0) {
+        attn_q81_block<0>(o, inv, lh, qrow, dsrow, kb0);
+        attn_q81_block<4>(o, inv, lh, qrow, dsrow, kb0 + 1);
+        attn_f32_group<8>(o, inv, lh, orow);
+    } else if constexpr (R == 1) {
+        attn_f32_group<0>(o, inv, lh, orow);
+        attn_f32_group<1>(o, inv, lh, orow);
+        attn_f32_group<2>(o, inv, lh, orow);
+        attn_q81_block<3>(o, inv, lh, qrow, dsrow, kb0 + 3);
+        attn_f32_group<7>(o, inv, lh, orow);
+        attn_f32_group<8>(o, inv, lh, orow);
+    } else if constexpr (R == 2) {
+        attn_f32_group<0>(o, inv, lh, orow);
+        attn_f32_group<1>(o, inv, lh, orow);
+        attn_q81_block<2>(o, inv, lh, qrow, dsrow, kb0 + 5);
+        attn_f32_group<6>(o, inv, lh, orow);
+        attn_f32_group<7>(o, inv, lh, orow);
+        attn_f32_group<8>(o, inv, lh, orow);
+    } else {
+        attn_f32_group<0>(o, inv, lh, orow);
+        attn_q81_block<1>(o, inv, lh, qrow, dsrow, kb0 + 7);
+        attn_q81_block<5>(o, inv, lh, qrow, dsrow, kb0 + 8);
+    }
+}
+
+// The straddling blocks 9 g + 2, + 4, + 6 of every 288-column group, from the
+// f32 rows: one 8-lane group per (row, block), as k_quantize_q8_1.
+__global__ __launch_bounds__(256) void k_quant_straddle(const float *__restrict__ x, int64_t ldx,
+                                                         int64_t M, int64_t n_grp, Q81Out o,
+                                                         int64_t ld_q) {
+    const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+    const int sub = threadIdx.x & 7;
+    const int64_t per_row = 3 * n_grp;
+    if (g >= M * per_row) return;  // whole 8-lane groups leave together
+    const int64_t m = g / per_row, i = g - m * per_row;
+    const int64_t kb = 9 * (i / 3) + 2 + 2 * (i % 3);
+    const int64_t c = kb * QK + sub * 4;
+    const float4 t = *reinterpret_cast<const float4 *>(x + m * ldx + c);
+    float a = fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w)));
+    a = group8_max(a);
+    const float d = a / 127.0f;
+    const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+    const int q0 = q8_round(t.x, inv), q1 = q8_round(t.y, inv);
+    const int q2 = q8_round(t.z, inv), q3 = q8_round(t.w, inv);
+    *reinterpret_cast<uint32_t *>(o.qs + m * ld_q + c) = pack4_i8(q0, q1, q2, q3);
+    const int s = group8_isum(q0 + q1 + q2 + q3);
+    if (sub == 0)
+        o.ds[m * o.ld_ds + kb] =
+            (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
+}
+
+// ---------------------------------------------------------------------------
 // flash attention: one workgroup = FA_WAVES waves x 32 queries of one
 // (segment, head); 64-key tiles of K and V^T staged through LDS (double
 // buffered).  12 waves: each thread stages one K and one V^T chunk per
@@ -169,13 +269,13 @@ constexpr int FA_WAVES = 12;  // waves (32 queries each) per workgroup
 constexpr int FA_WAVES_SMALL = 4;  // the same for launches of few workgroups
 constexpr float P_SHIFT = 15.0f;  // log2 of the largest P of a row (<= 65504 as f16)
 
-template <bool P_SPLIT, int NW>
+template <bool P_SPLIT, int NW, bool QUANT>
 __global__ __launch_bounds__(64 * NW) void k_attn(
     const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
     const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
     const int32_t *__restrict__ seg_len, const uint8_t *__restrict__ key_valid,
     int n_head, int d_head, int len_pad, int n_qt, float scale_log2, float *__restrict__ out,
-    int64_t ld_out) {
+    int64_t ld_out, Q81Out qo, int64_t ld_q) {
     __shared__ __align__(16) _Float16 lds[2 * FA_STAGE];
     // (query tile, head, segment), query tile fastest, in XCD-contiguous
     // order: the query tiles of one head share their XCD's L2 for K and V^T
@@ -414,7 +514,22 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
     static_assert(FA_ONES == 2 * 32 + 8 * 3 && FA_ONES >= FA_DP && FA_ONES < FA_DV, "ones row");
     const float l_tot = __shfl(o[2][12], lr);
     const float inv = 1.0f / l_tot;
-    if (q < len) {
+    if (QUANT) {
+        // (d_head 72, heads in groups of four: checked by the launcher)
+        if (q < len) {
+            const int64_t row = row0 + q;
+            float *orow = out + row * ld_out + h * d_head;
+            int8_t *qrow = qo.qs + row * ld_q + h * d_head;
+            uint32_t *dsrow = qo.ds + row * qo.ld_ds;
+            const int kb0 = 9 * (h >> 2);
+            switch (h & 3) {
+            case 0: attn_q81_row<0>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+            case 1: attn_q81_row<1>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+            case 2: attn_q81_row<2>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+            default: attn_q81_row<3>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+            }
+        }
+    } else if (q < len) {
         float *orow = out + (row0 + q) * ld_out + h * d_head;
 #pragma unroll
         for (int j = 0; j < 3; ++j)
@@ -432,9 +547,14 @@ __global__ __launch_bounds__(64 * NW) void k_attn(
 
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
                        const uint8_t *key_valid, const AttnLayout &L, float scale,
-                       float *out, int64_t ld_out, hipStream_t stream) {
+                       float *out, int64_t ld_out, hipStream_t stream, const Q81Out *qo,
+                       int64_t n_rows) {
     if (L.n_seg == 0) return hipSuccess;
     if (L.d_pad != FA_DP || L.dv_pad != FA_DV || (L.d_head % 4) != 0) return hipErrorInvalidValue;
+    const int64_t H = L.n_head * L.d_head;
+    if (qo && (!attn_q81_fusable(L.n_head, L.d_head) || !qo->qs || !qo->ds || n_rows <= 0 ||
+               qo->ld_ds < H / QK || ld_out < H || ld_out % 4 != 0))
+        return hipErrorInvalidValue;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(ws);
     const float log2e = 1.4426950408889634f;
     // 12-wave workgroups fill the chip from 256 of them up (batch 32: 1,024);
@@ -445,14 +565,31 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     const int64_t n_qt = (L.max_len + 32 * NW - 1) / (32 * NW);
     const int64_t n_wg = n_qt * L.n_head * L.n_seg;
     if (n_wg > 0x7fffffff) return hipErrorInvalidValue;
-    auto kern = NW == FA_WAVES ? (L.p_split ? k_attn<true, FA_WAVES> : k_attn<false, FA_WAVES>)
-                               : (L.p_split ? k_attn<true, FA_WAVES_SMALL> : k_attn<false, FA_WAVES_SMALL>);
+    using KFn = void (*)(const _Float16 *, const _Float16 *, const _Float16 *, const int32_t *,
+                         const int32_t *, const uint8_t *, int, int, int, int, float, float *,
+                         int64_t, Q81Out, int64_t);
+    KFn kern;
+    const bool qz = qo != nullptr;
+    if (NW == FA_WAVES)
+        kern = L.p_split ? (qz ? k_attn<true, FA_WAVES, true> : k_attn<true, FA_WAVES, false>)
+                         : (qz ? k_attn<false, FA_WAVES, true> : k_attn<false, FA_WAVES, false>);
+    else
+        kern = L.p_split ? (qz ? k_attn<true, FA_WAVES_SMALL, true> : k_attn<true, FA_WAVES_SMALL, false>)
+                         : (qz ? k_attn<false, FA_WAVES_SMALL, true> : k_attn<false, FA_WAVES_SMALL, false>);
+    const Q81Out q_none{};
     hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(64 * NW), 0, stream,
                        reinterpret_cast<const _Float16 *>(base + L.q_off),
                        reinterpret_cast<const _Float16 *>(base + L.k_off),
                        reinterpret_cast<const _Float16 *>(base + L.vt_off), seg_start, seg_len,
                        key_valid, (int)L.n_head, (int)L.d_head, (int)L.len_pad, (int)n_qt,
-                       scale * log2e, out, ld_out);
+                       scale * log2e, out, ld_out, qz ? *qo : q_none, H);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !qz) return e;
+    // the blocks that straddle two heads, from the f32 columns just written
+    // (rows of the packed segments: 0 .. n_rows - 1, every row a segment's)
+    const int64_t groups = n_rows * 3 * (L.n_head / 4);
+    hipLaunchKernelGGL(k_quant_straddle, dim3((unsigned)((groups * 8 + 255) / 256)), dim3(256), 0,
+                       stream, out, ld_out, n_rows, L.n_head / 4, *qo, H);
     return hipGetLastError();
 }
 

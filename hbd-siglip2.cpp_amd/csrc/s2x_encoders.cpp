@@ -456,7 +456,8 @@ struct Tower {
     const int32_t *seg_len(int64_t n_seg) const { return seg.as<int32_t>() + n_seg; }
 
     // The encoder blocks in place on x (M packed rows, n_seg segments):
-    //   LN1+Q8_1 -> QKV GEMM -> attention -> Q8_1 -> O GEMM (+bias +residual,
+    //   LN1+Q8_1 -> QKV GEMM -> attention -> Q8_1 (folded into the flash
+    //   attention for 72-wide heads in groups of four) -> O GEMM (+bias +residual,
     //   in place) -> LN2+Q8_1 -> FC1 GEMM (+bias, GELU, Q8_1 of the result
     //   with K padded to F_pad) -> FC2 GEMM (+bias +residual, in place)
     // The QKV GEMM writes the flash kernel's operands itself (EPI_QKV); with
@@ -478,6 +479,17 @@ struct Tower {
                 if (e != hipSuccess) return hip_fail(e, "attn_f64 launch");
             } else {
                 S2X_TRY(gemm(L.qkv, M, nullptr, 0, epi_qkv(AL, attn_ws.p, L.qkv_b, rowmap.as<int32_t>()), H));
+                if (attn_q81_fusable(n_head, d_head)) {
+                    // the out-projection's Q8_1 input straight from attention
+                    const Q81Out o = qout(H);
+                    e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
+                                    att.as<float>(), H, stream, &o, M);
+                    if (e != hipSuccess) return hip_fail(e, "attn launch");
+                    S2X_TRY(gemm(L.o, M, xp, H, EpiParams{EPI_BIAS_RESID, L.o_b, xp, H, 0, 0}, H));
+                    S2X_TRY(layernorm_q(xp, M, L.ln2_w, L.ln2_b, nullptr));
+                    S2X_TRY(ffn(L.up, L.up_b, L.down, L.down_b, M, xp, xp));
+                    continue;
+                }
                 e = launch_attn(attn_ws.p, seg_start(), seg_len(n_seg), key_valid, AL, kq_scale,
                                 att.as<float>(), H, stream);
                 if (e != hipSuccess) return hip_fail(e, "attn launch");

@@ -126,9 +126,18 @@ hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64
                          int64_t max_len, int32_t *rowmap, int64_t n_rows, hipStream_t stream);
 // EPI_QKV destination planes of layout L in workspace ws.
 EpiParams epi_qkv(const AttnLayout &L, void *ws, const float *qkv_bias, const int32_t *rowmap);
+// With qo: the output's Q8_1 (K = n_head * d_head) instead of the whole f32
+// output -- only the columns of Q8_1 blocks that straddle two heads are
+// written to `out` -- over the packed rows 0 .. n_rows - 1 (every row a
+// segment's); needs attn_q81_fusable.
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,
                        const uint8_t *key_valid, const AttnLayout &L, float scale,
-                       float *out, int64_t ld_out, hipStream_t stream);
+                       float *out, int64_t ld_out, hipStream_t stream,
+                       const Q81Out *qo = nullptr, int64_t n_rows = 0);
+// 72-wide heads in groups of four: whole Q8_1 blocks per group of heads
+inline bool attn_q81_fusable(int64_t n_head, int64_t d_head) {
+    return d_head == 72 && n_head % 4 == 0;
+}
 // fp64 attention straight from the QKV GEMM rows (+bias), fixed summation
 // order; for short sequences (the text tower).
 hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,

@@ -138,6 +138,8 @@ _sig("s2x_nf_preprocess_rgb_batch_dev", [_p, _i32, _i32, _i32, _i32, _i32, _f32,
 _sig("s2x_attn_workspace_size", [_i64, _i64, _i64, _i64], _sz)
 _sig("s2x_attn_prep", [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p])
 _sig("s2x_attn_run", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])
+_sig("s2x_attn_run_q8_1", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i64, _p, _p, _i64,
+                          _p, _i64, _p])
 _sig("s2x_attn_fp64", [_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])
 _sig("s2x_resize_pos_embed", [_p, _i64, _i64, _i64, _i64, _p, _p])
 _sig("s2x_get_rows_q8_0", [_p, _i64, _i64, _p, _i64, _p, _i64, _p, _p])

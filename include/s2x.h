@@ -239,6 +239,22 @@ int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
                  int64_t d_head, float scale, float *out, int64_t ld_out,
                  void *stream);
 
+/* s2x_attn_run followed by s2x_quantize_q8_1 of its output (K = H), in
+ * one pass for 72-wide heads in groups of four (n_head % 4 == 0): the
+ * post-attention contiguous copy and the activation quantizer of the
+ * out-projection (siglip2_vision.cpp:148 launch_fused_post_fa_cont,
+ * siglip2_custom_mmq.cuh:63 launch_quantize_activation).  qs [n_rows][H]
+ * int8, ds [n_rows][ld_ds] words as s2x_quantize_q8_1 writes them, the same
+ * bits.  `out` (f32 [n_rows][ld_out], 16-byte aligned) is scratch: only the
+ * columns of Q8_1 blocks that straddle two heads are written.  The segments
+ * must cover rows 0 .. n_rows - 1. */
+int s2x_attn_run_q8_1(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
+                      const int32_t *seg_len_dev, const uint8_t *key_valid,
+                      int64_t n_seg, int64_t max_len, int64_t n_head,
+                      int64_t d_head, float scale, int64_t n_rows, void *qs,
+                      void *ds, int64_t ld_ds, float *out, int64_t ld_out,
+                      void *stream);
+
 /* fp64 attention straight from the QKV rows (bias added in f32, Q/K/V
  * rounded to f16 as the reference casts them, then scores, softmax and PV in
  * double in a fixed key order).  Needs no staging workspace; meant for short

@@ -359,6 +359,52 @@ def test_attention_key_mask(orc):
     assert _attn_case(orc, lens, key_valid=kv, seed=11) < 1e-5
 
 
+@pytest.mark.parametrize("case", ["ragged", "masked", "batch32", "one"])
+def test_attention_q8_1_equals_attention_then_quantize(case):
+    """s2x_attn_run_q8_1 (Q8_1 of whole blocks in the attention epilogue,
+    the blocks that straddle two heads in a second pass) gives exactly the
+    bytes of s2x_attn_run followed by s2x_quantize_q8_1."""
+    n_head, dh = 16, 72
+    H = n_head * dh
+    lens = {"ragged": [729, 1, 64, 130, 255, 128, 33], "masked": [64, 200],
+            "batch32": [729] * 32, "one": [729]}[case]
+    rng = np.random.default_rng(17)
+    M = int(sum(lens))
+    qkv = (rng.standard_normal((M, 3 * H)) * 1.5).astype(np.float32)
+    bias = rng.normal(0, 0.5, 3 * H).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    lens = np.asarray(lens, np.int32)
+    max_len = int(lens.max())
+    kv = None
+    if case == "masked":
+        kv = np.ones(M, np.uint8)
+        kv[40:64] = 0
+        kv[64 + 150:] = 0
+    say(f"attention + Q8_1: {case}, M={M}")
+    wsb = s2x.lib.s2x_attn_workspace_size(len(lens), max_len, n_head, dh)
+    ws = zeros((wsb,), torch.uint8)
+    qd, bd, sd, ld = dev(qkv), dev(bias), dev(starts), dev(lens)
+    kd = dev(kv) if kv is not None else None
+    scale = ctypes.c_float(np.float32(1.0 / np.sqrt(np.float32(dh))))
+    s2x.call("s2x_attn_prep", ptr(qd), 3 * H, ptr(bd), ptr(sd), ptr(ld), len(lens), max_len,
+             n_head, dh, ptr(ws), ctypes.c_size_t(wsb), stream())
+    out = empty((M, H), torch.float32)
+    s2x.call("s2x_attn_run", ptr(ws), ctypes.c_size_t(wsb), ptr(sd), ptr(ld), ptr(kd), len(lens),
+             max_len, n_head, dh, scale, ptr(out), H, stream())
+    qs_r = zeros((M, H), torch.int8)
+    ds_r = zeros((M, H // 32), torch.int32)
+    s2x.call("s2x_quantize_q8_1", ptr(out), H, M, H, H, ptr(qs_r), ptr(ds_r), stream())
+    # the fused path, into garbage-filled buffers (every byte must be written)
+    qs_f = torch.full((M, H), 0x5A, dtype=torch.int8, device="cuda:0")
+    ds_f = torch.full((M, H // 32), 0x5A5A5A5A, dtype=torch.int32, device="cuda:0")
+    scratch = torch.full((M, H), float("nan"), dtype=torch.float32, device="cuda:0")
+    s2x.call("s2x_attn_run_q8_1", ptr(ws), ctypes.c_size_t(wsb), ptr(sd), ptr(ld), ptr(kd),
+             len(lens), max_len, n_head, dh, scale, M, ptr(qs_f), ptr(ds_f), H // 32, ptr(scratch),
+             H, stream())
+    assert_same(host(qs_f), host(qs_r), f"{case} quants")
+    assert_same(host(ds_f), host(ds_r), f"{case} scale words")
+
+
 @pytest.mark.parametrize("masked", [False, True])
 def test_attention_fp64_matches_oracle(orc, masked):
     n_head, dh = 16, 72
