@@ -175,6 +175,7 @@ hipError_t launch_repack_f16(const void *raw, int64_t K, int64_t N, int64_t K_pa
 // ---------------------------------------------------------------------------
 constexpr int LN_MAXIT = 8;        // H <= 8 * 256
 constexpr int LN_MAX_BLOCKS = 3072;  // resident-size grid; blocks stride over the rows
+constexpr int64_t LN_WREG_ROWS = 4096;
 
 // 4 columns per lane per 256-column pass; a missing row (ok false) or a
 // column past H reads as zeros
@@ -198,26 +199,44 @@ __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr,
     }
 }
 
-// NIT = ceil(H / 256) column passes.  w and b are staged once per block in
-// LDS; each wave walks rows row, row + 4 * gridDim.x, ... and loads its next
-// row before reducing the current one, so HBM reads overlap the reductions.
-template <bool QUANT, bool WRITE_Y, int NIT>
+// NIT = ceil(H / 256) column passes.  w and b: in LDS, staged once per
+// workgroup (WREG false: many rows per wave), or in the registers of the
+// lanes' own columns (WREG true: launches of few rows, where the staging
+// barrier in front of the first row is most of a wave's time).  Each wave
+// walks rows row, row + 4 * gridDim.x, ... and loads its next row before
+// reducing the current one, so HBM reads overlap the reductions.
+template <bool QUANT, bool WRITE_Y, int NIT, bool WREG>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
     const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
     float *__restrict__ y, int64_t ldy, int vec4) {
-    __shared__ __align__(16) float sw[NIT * 256], sb[NIT * 256];
+    __shared__ __align__(16) float sw[WREG ? 4 : NIT * 256], sb[WREG ? 4 : NIT * 256];
     const int lane = threadIdx.x & 63;
     const int64_t stride = (int64_t)gridDim.x * 4;
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    // the first row's loads in flight before w and b are staged
-    float v[NIT][4];
+    // the first row's loads in flight before w and b are fetched
+    float v[NIT][4], wr[NIT][4], br[NIT][4];
     ln_load_row<NIT>(v, x + row * ldx, H, lane, row < M, vec4);
-    for (int i = threadIdx.x; i < H; i += 256) {
-        sw[i] = w ? w[i] : 1.0f;
-        sb[i] = b ? b[i] : 0.0f;
+    if constexpr (WREG) {
+        // few rows per wave: w and b of the lane's own columns in registers,
+        // no staging barrier in front of the first row
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int64_t c = (int64_t)it * 256 + lane * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                wr[it][j] = w && c + j < H ? w[c + j] : 1.0f;
+                br[it][j] = b && c + j < H ? b[c + j] : 0.0f;
+            }
+        }
+    } else {
+        // many rows per wave: w and b staged once per workgroup in LDS
+        for (int i = threadIdx.x; i < H; i += 256) {
+            sw[i] = w ? w[i] : 1.0f;
+            sb[i] = b ? b[i] : 0.0f;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     for (; row < M; row += stride) {  // wave-uniform
         float vn[NIT][4];
         const int64_t next = row + stride;
@@ -252,9 +271,19 @@ __global__ __launch_bounds__(256) void k_layernorm(
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
             if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
-            const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
-            const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
-            const float wa[4] = {wv.x, wv.y, wv.z, wv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
+            float wa[4], ba[4];
+            if constexpr (WREG) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    wa[j] = wr[it][j];
+                    ba[j] = br[it][j];
+                }
+            } else {
+                const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
+                const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
+                wa[0] = wv.x; wa[1] = wv.y; wa[2] = wv.z; wa[3] = wv.w;
+                ba[0] = bv.x; ba[1] = bv.y; ba[2] = bv.z; ba[3] = bv.w;
+            }
             float o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -291,19 +320,30 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
 }
 
+template <int NIT, bool WREG>
+void launch_ln_cfg(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
+                   const float *b, float eps, bool quant, const Q81Out &qo, float *y,
+                   int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
+    if (quant && y)
+        hipLaunchKernelGGL((k_layernorm<true, true, NIT, WREG>), grid, dim3(256), 0, stream, x, H,
+                           M, ldx, w, b, eps, qo, y, ldy, vec4);
+    else if (quant)
+        hipLaunchKernelGGL((k_layernorm<true, false, NIT, WREG>), grid, dim3(256), 0, stream, x,
+                           H, M, ldx, w, b, eps, qo, y, ldy, vec4);
+    else
+        hipLaunchKernelGGL((k_layernorm<false, true, NIT, WREG>), grid, dim3(256), 0, stream, x,
+                           H, M, ldx, w, b, eps, qo, y, ldy, vec4);
+}
+
 template <int NIT>
 void launch_ln_nit(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
                    const float *b, float eps, bool quant, const Q81Out &qo, float *y,
                    int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
-    if (quant && y)
-        hipLaunchKernelGGL((k_layernorm<true, true, NIT>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qo, y, ldy, vec4);
-    else if (quant)
-        hipLaunchKernelGGL((k_layernorm<true, false, NIT>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qo, y, ldy, vec4);
+    // registers for w and b below LN_WREG_ROWS rows (at most ~1.5 rows per wave)
+    if (M <= LN_WREG_ROWS)
+        launch_ln_cfg<NIT, true>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
     else
-        hipLaunchKernelGGL((k_layernorm<false, true, NIT>), grid, dim3(256), 0, stream, x, H, M,
-                           ldx, w, b, eps, qo, y, ldy, vec4);
+        launch_ln_cfg<NIT, false>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
 }
 
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
