@@ -36,8 +36,9 @@
 //   XQ  [KS][128 rows][32]  X quants, the two 16-byte chunks of row r at
 //                            chunk position c ^ swz(r)
 //   WQ  [KS][128 rows][32]  W quants, same swizzle
-//   XS  [KS][128] u32        X ds words
-//   WS  [KS][128 + 40] u16   W scales, each block's followed by zeros
+//   XS  [128][KS] u32        X ds words, a row's KS blocks together (as in
+//                            the ds plane: one 16-byte DMA lane per row)
+//   WS  [KS][128] u16        W scales, then 1 KB of zeros
 // A fragment read (lane l: row l & 31, chunk l >> 5, 16 bytes) then touches
 // 16 distinct 16-byte bank groups per 16 lanes: no bank conflicts.
 #include "s2x_device.h"
@@ -51,7 +52,6 @@ namespace gemm {
 
 constexpr int BN = 128;  // output tile columns
 constexpr int GM = 8;    // tile-row group of the tile order
-constexpr int WSB = BN * 2 + 80;  // W scales of a block: BN fp16 values, then 80 zero bytes
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
 // BM x 128 tiles (BM 128 or 64), BM / 16 waves of 32 x 64 outputs (BM / 32
@@ -70,26 +70,26 @@ struct Cfg {
     static constexpr int NWAVE = BM / 16, NT = NWAVE * WAVE;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
-    static constexpr int XS = WQ + KS * BN * 32;  // [KS][BM] u32 X ds words
-    static constexpr int WS = XS + KS * BM * 4;   // [KS] x (BN fp16 + zeros) W scales
-    static constexpr int STAGE = WS + KS * WSB;
+    static constexpr int XS = WQ + KS * BN * 32;  // [BM][KS] u32 X ds words
+    static constexpr int WS = XS + KS * BM * 4;   // [KS][BN] fp16 W scales, then 1 KB of zeros
+    static constexpr int STAGE = WS + KS * BN * 2 + 1024;
     static constexpr int LDS_BYTES = NS * STAGE;
     static constexpr int WG_PER_CU = 2 * LDS_BYTES <= 163840 ? 2 : 1;
     static constexpr int WPE = LAT ? 2 : WG_PER_CU * NWAVE / 4;  // waves per SIMD
-    // DMA instructions per stage and wave: QPX X-quant and QPW W-quant (each
-    // 32 rows of one block: KS BM / 32 and 4 KS per stage), SPW X-scale (64
-    // rows of one block: KS BM / 64 per stage) and 1 W-scale (one block: KS
-    // per stage); where a stage has fewer than NWAVE of a kind, waves w and
-    // w + NWAVE / n fetch the same bytes to the same place, so every wave
-    // issues the same count
-    static constexpr int NH = BM / 64;  // 64-row halves of a block's X rows
+    // DMA instructions per stage: QPX X-quant and QPW W-quant per wave (each
+    // 32 rows of one block: KS BM / 32 and 4 KS per stage); the scales, 16
+    // bytes per lane (a row's 4 consecutive ds words, or 8 W scales of one
+    // block), by the first NSX + 1 waves: waves 0 .. NSX - 1 the X scales
+    // of 64 rows each, wave NSX the W scales.  The issue cost of these
+    // instructions, not their bytes, is what the K loop feels, hence the
+    // scales in as few of them as their 16-byte rows allow.
+    static constexpr int NSX = BM / 64;
     static constexpr int QPX = KS * (BM / 32) / NWAVE, QPW = KS * (BN / 32) / NWAVE;
-    static constexpr int SPW = KS * NH >= NWAVE ? KS * NH / NWAVE : 1;
-    static constexpr int DMA_N = QPX + QPW + SPW + 1;
-    static_assert(KS == 2 || KS == 4, "stage of 2 or 4 blocks");
+    static_assert(KS == 4, "stage of 4 blocks: one 16-byte ds row per X row");
     static_assert(BM == 128 || BM == 64, "tile rows");
     static_assert(QPX >= 1 && QPW >= 1 && QPX <= KS && QPW <= KS, "DMA split");
-    static_assert(NS >= 2 && (NS - 2) * DMA_N <= 63, "vmcnt range");
+    static_assert(NS == 2, "a ring of two stages: each stage's DMA is waited for in full");
+    static_assert(NSX + 1 <= NWAVE, "scale DMA waves");
     static_assert(LDS_BYTES * WG_PER_CU <= 163840, "LDS");
     static_assert(NWAVE * 5120 <= LDS_BYTES, "epilogue scratch");
 };
@@ -112,10 +112,6 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                       uint8_t *lds_wave_base) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
-                                     uint8_t *lds_wave_base) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 4, voff, soff, 0, 0);
 }
 
 template <int N>
@@ -436,20 +432,17 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     //   X quants, instructions t < QPX: i = QPX wave + t, block i % KS, rows
     //             32 (i / KS) .. + 31 (= 32 (QPX wave / KS) for every t)
     //   W quants, instructions t < QPW: likewise with QPW
-    //   X scales, instructions t < SPW: i = (SPW wave + t) % (NH KS), block
-    //             i / NH, rows 64 (i % NH) .. + 63 (one ds word per lane)
-    //   W scales: block wave % KS, columns 2 lane, 2 lane + 1
-    uint32_t vqx, vqw, vxs[C::SPW];
+    //   X scales: waves w < NSX, rows 64 w + lane, the ds words of blocks
+    //             k0 .. k0 + 3 (16 bytes)
+    //   W scales: wave NSX, block lane / 16, columns 8 (lane % 16) .. + 7
+    uint32_t vqx, vqw, vxs, vws;
     {
         const int rx = 32 * (C::QPX * wave / KS) + (lane >> 1);
         vqx = (uint32_t)(rx * row_bytes) + (uint32_t)(((lane & 1) ^ swz(rx)) * 16);
         const int rw = 32 * (C::QPW * wave / KS) + (lane >> 1);
         vqw = (uint32_t)(rw * row_bytes) + (uint32_t)(((lane & 1) ^ swz(rw)) * 16);
-#pragma unroll
-        for (int t = 0; t < C::SPW; ++t) {
-            const int i = (C::SPW * wave + t) % (C::NH * KS);
-            vxs[t] = (uint32_t)(((i % C::NH) * 64 + lane) * ld_ds * 4);
-        }
+        vxs = (uint32_t)((min(wave, C::NSX - 1) * 64 + lane) * ld_ds * 4);
+        vws = (uint32_t)((lane >> 4) * ldT * 2 + (lane & 15) * 16);
     }
     const __amdgpu_buffer_rsrc_t xr_live = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(xq + (int64_t)m0 * row_bytes), (short)0, clip32((int64_t)(M - m0) * row_bytes), BUF_DW3);
@@ -466,7 +459,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     // blocks past KB in the last stage are fetched and never used.  Stages
     // past the last are issued too, through zero-size buffers (no memory is
     // read), so that no branch splits the K loop.
-    auto issue = [&](int g) {
+    // ROLE (a constant per wave: 1 X scales, 2 W scales, 0 neither) is a
+    // template value so that no branch splits the K loop
+    auto issue = [&](int g, auto role) {
+        constexpr int ROLE = decltype(role)::value;
         const bool live = g < n_st;
         const __amdgpu_buffer_rsrc_t xr = live ? xr_live : none, wr = live ? wr_live : none;
         const __amdgpu_buffer_rsrc_t xsr = live ? xsr_live : none, wsr = live ? wsr_live : none;
@@ -482,31 +478,29 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             const int i = C::QPW * wave + t, j = i % KS;
             dma16(wr, vqw, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
         }
-#pragma unroll
-        for (int t = 0; t < C::SPW; ++t) {
-            const int i = (C::SPW * wave + t) % (C::NH * KS), j = i / C::NH;
-            dma4(xsr, vxs[t], (k0 + j) * 4, sb + XS + j * BM * 4 + (i % C::NH) * 256);
-        }
-        dma4(wsr, (uint32_t)lane * 4, (uint32_t)((k0 + wave % KS) * ldT * 2),
-             sb + WS + (wave % KS) * WSB);
+        if constexpr (ROLE == 1)
+            dma16(xsr, vxs, k0 * 4, sb + XS + wave * 64 * 16);
+        else if constexpr (ROLE == 2)
+            dma16(wsr, vws, (uint32_t)(k0 * ldT * 2), sb + WS);
     };
 
     // Stage g visible to every wave: this wave's DMA of it has landed (the
     // NS - 2 later stages may still be in flight), then the barrier.  After
     // the barrier no wave reads the buffer of stage g - 1 any more (its last
     // fragments were read before this point), so stage g + NS - 1 refills it.
-    auto arrive = [&](int g) {
-        wait_vm<(NS - 2) * C::DMA_N>();
+    auto arrive = [&](int g, auto role) {
+        wait_vm<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        issue(g + NS - 1);
+        issue(g + NS - 1, role);
     };
 
     // fragment addresses (bytes within a stage buffer) of this lane
     const int xrow = wm * 32 * TM + lr, wcol = wn * 64 + lr;
     const int a_off = XQ + xrow * 32 + ((lh ^ swz(lr)) * 16);
     const int b_off = WQ + wcol * 32 + ((lh ^ swz(lr)) * 16);
-    const int sx_off = XS + xrow * 4;
-    const int sw_off = lh ? WS + BN * 2 : WS + wcol * 2;  // lanes 32..63: the zero pad
+    const int sx_off = XS + xrow * 16;
+    // lanes 32..63 read the zeros after the W scales (at offsets < 1 KB)
+    const int sw_off = lh ? WS + KS * BN * 2 : WS + wcol * 2;
     auto load_frag = [&](const uint8_t *sb, auto jc, Frag<TM> &f) {
         constexpr int j = decltype(jc)::value;
 #pragma unroll
@@ -517,10 +511,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             f.b[b] = *reinterpret_cast<const v4i *>(sb + b_off + j * BN * 32 + b * 32 * 32);
 #pragma unroll
         for (int a = 0; a < TM; ++a)
-            f.sx[a][0] = *reinterpret_cast<const uint16_t *>(sb + sx_off + j * BM * 4 + a * 32 * 4);
+            f.sx[a][0] = *reinterpret_cast<const uint16_t *>(sb + sx_off + j * 4 + a * 32 * 16);
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-            f.sw[b][0] = *reinterpret_cast<const uint16_t *>(sb + sw_off + j * WSB + b * 32 * 2);
+            f.sw[b][0] = *reinterpret_cast<const uint16_t *>(sb + sw_off + j * BN * 2 + b * 32 * 2);
     };
 
     float acc[TM][2][16];
@@ -585,12 +579,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         if constexpr (!C::LAT) __builtin_amdgcn_sched_barrier(0);
     };
 
-    // the zero pads after each block's W scales (never written by the DMA)
-    if (tid < NS * KS * 5) {
-        const int i = tid / 5, c = tid % 5;
-        *reinterpret_cast<v4i *>(lds + (i / KS) * STAGE + WS + (i % KS) * WSB + BN * 2 + c * 16) =
+    // the zeros after each stage's W scales (never written by the DMA)
+    if (tid < NS * 64)
+        *reinterpret_cast<v4i *>(lds + (tid >> 6) * STAGE + WS + KS * BN * 2 + (tid & 63) * 16) =
             v4i{0, 0, 0, 0};
-    }
     float bias_v[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -604,12 +596,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
+    auto k_loop = [&](auto role) {
 #pragma unroll
-    for (int g = 0; g < NS - 1; ++g) issue(g);
+    for (int g = 0; g < NS - 1; ++g) issue(g, role);
     // the first stage visible, stage NS - 1 issued
-    wait_vm<(NS - 2) * C::DMA_N>();
+    wait_vm<0>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(NS - 1);
+    issue(NS - 1, role);
     // each block's fragments are read right before its MFMAs (the other
     // waves of the SIMD cover the LDS latency)
     for (int g = 0; g < n_st - 1; ++g) {
@@ -633,7 +626,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
                 compute(F, kb0 + decltype(jc)::value);
             });
         }
-        arrive(g + 1);
+        arrive(g + 1, role);
     }
     {
         // the last stage: nb = 1 .. KS blocks
@@ -647,6 +640,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             }
         });
     }
+    };
+    if (wave < C::NSX)
+        k_loop(std::integral_constant<int, 1>{});
+    else if (wave == C::NSX)
+        k_loop(std::integral_constant<int, 2>{});
+    else
+        k_loop(std::integral_constant<int, 0>{});
 
     // ----------------------------------------------------------------------
     // Epilogue.  The LDS is free scratch once the last (empty) stage's DMA
