@@ -456,42 +456,47 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 
     // Issue the DMA of stage g into buffer g % NS.  Reads past M, N or the
     // planes return zeros (the scalar offset is part of the range check);
-    // blocks past KB in the last stage are fetched and never used.  Stages
-    // past the last are issued too, through zero-size buffers (no memory is
-    // read), so that no branch splits the K loop.
-    // ROLE (a constant per wave: 1 X scales, 2 W scales, 0 neither) is a
-    // template value so that no branch splits the K loop
-    auto issue = [&](int g, auto role) {
-        constexpr int ROLE = decltype(role)::value;
+    // blocks past KB in the last stage are fetched and never used.  A stage
+    // past the last is issued through zero-size buffers (no memory is read)
+    // and ROLE (a constant per wave: 1 X scales, 2 W scales, 0 neither) is
+    // a template value, so that no branch splits the K loop.
+    // PART: 0 the X quants, 1 the W quants, 2 the scales, -1 all three
+    auto issue = [&](int g, auto role, auto part) {
+        constexpr int ROLE = decltype(role)::value, PART = decltype(part)::value;
         const bool live = g < n_st;
         const __amdgpu_buffer_rsrc_t xr = live ? xr_live : none, wr = live ? wr_live : none;
         const __amdgpu_buffer_rsrc_t xsr = live ? xsr_live : none, wsr = live ? wsr_live : none;
         uint8_t *sb = lds + (g % NS) * STAGE;
         const uint32_t k0 = (uint32_t)(g * KS);
+        if constexpr (PART == 0 || PART < 0) {
 #pragma unroll
-        for (int t = 0; t < C::QPX; ++t) {
-            const int i = C::QPX * wave + t, j = i % KS;
-            dma16(xr, vqx, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
+            for (int t = 0; t < C::QPX; ++t) {
+                const int i = C::QPX * wave + t, j = i % KS;
+                dma16(xr, vqx, (k0 + j) * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
+            }
         }
+        if constexpr (PART == 1 || PART < 0) {
 #pragma unroll
-        for (int t = 0; t < C::QPW; ++t) {
-            const int i = C::QPW * wave + t, j = i % KS;
-            dma16(wr, vqw, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
+            for (int t = 0; t < C::QPW; ++t) {
+                const int i = C::QPW * wave + t, j = i % KS;
+                dma16(wr, vqw, (k0 + j) * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
+            }
         }
-        if constexpr (ROLE == 1)
-            dma16(xsr, vxs, k0 * 4, sb + XS + wave * 64 * 16);
-        else if constexpr (ROLE == 2)
-            dma16(wsr, vws, (uint32_t)(k0 * ldT * 2), sb + WS);
+        if constexpr (PART == 2 || PART < 0) {
+            if constexpr (ROLE == 1)
+                dma16(xsr, vxs, k0 * 4, sb + XS + wave * 64 * 16);
+            else if constexpr (ROLE == 2)
+                dma16(wsr, vws, (uint32_t)(k0 * ldT * 2), sb + WS);
+        }
     };
+    using All = std::integral_constant<int, -1>;
 
-    // Stage g visible to every wave: this wave's DMA of it has landed (the
-    // NS - 2 later stages may still be in flight), then the barrier.  After
-    // the barrier no wave reads the buffer of stage g - 1 any more (its last
-    // fragments were read before this point), so stage g + NS - 1 refills it.
-    auto arrive = [&](int g, auto role) {
+    // Stage g + 1 visible to every wave: this wave's DMA of it has landed,
+    // then the barrier.  After it no wave reads stage g's buffer any more, so
+    // the DMA of stage g + 2 may refill it.
+    auto arrive = [&]() {
         wait_vm<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        issue(g + NS - 1, role);
     };
 
     // fragment addresses (bytes within a stage buffer) of this lane
@@ -597,14 +602,12 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
     auto k_loop = [&](auto role) {
-#pragma unroll
-    for (int g = 0; g < NS - 1; ++g) issue(g, role);
-    // the first stage visible, stage NS - 1 issued
-    wait_vm<0>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(NS - 1, role);
-    // each block's fragments are read right before its MFMAs (the other
-    // waves of the SIMD cover the LDS latency)
+    issue(0, role, All{});
+    arrive();  // the first stage visible
+    if constexpr (C::LAT) issue(1, role, All{});
+    // stage g computed while stage g + 1 loads; each block's fragments are
+    // read right before its MFMAs (the other waves of the SIMD cover the
+    // LDS latency)
     for (int g = 0; g < n_st - 1; ++g) {
         const uint8_t *sb = lds + (g % NS) * STAGE;
         const int kb0 = g * KS;
@@ -621,12 +624,21 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             });
             static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value); });
         } else {
+            // the next stage's DMA in three parts after blocks 0, 1 and 2:
+            // spread over the stage rather than in one burst after the
+            // barrier, when every wave of the CU starts reading fragments
             static_for<KS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
                 load_frag(sb, jc, F);
-                compute(F, kb0 + decltype(jc)::value);
+                compute(F, kb0 + j);
+                if constexpr (j < 3) issue(g + 1, role, std::integral_constant<int, j>{});
             });
         }
-        arrive(g + 1, role);
+        arrive();
+        // the latency form's MFMAs may sink below the barrier (its stage is
+        // one scheduling region): its next DMA goes out after the barrier,
+        // a whole stage before the wait for it
+        if constexpr (C::LAT) issue(g + 2, role, All{});
     }
     {
         // the last stage: nb = 1 .. KS blocks
