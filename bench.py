@@ -380,21 +380,29 @@ def bench_text(np, s2x, synth, warm=3, iters=20):
     def enc():
         s2x.call("s2x_text_encode_batch", t, ids.ctypes.data, 64, 5, out.ctypes.data)
 
-    for _ in range(warm):
-        enc()
-    lat = []
-    for _ in range(iters):
-        t0 = time.perf_counter()
-        enc()
-        lat.append((time.perf_counter() - t0) * 1000.0)
+    def timed():
+        for _ in range(warm):
+            enc()
+        lat = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            enc()
+            lat.append((time.perf_counter() - t0) * 1000.0)
+        assert np.isfinite(out).all()
+        return lat
+
+    lat = timed()
+    # the K-split GEMM option (off by default), for comparison
+    s2x.call("s2x_text_set_split_k", t, 1)
+    lat_split = timed()
     s2x.lib.s2x_text_destroy(t)
-    assert np.isfinite(out).all()
     p50 = pct(lat, 0.5)
-    log(f"bench: text 5 x 64: p50 {p50:.3f} ms")
+    log(f"bench: text 5 x 64: p50 {p50:.3f} ms (K-split GEMMs: {pct(lat_split, 0.5):.3f} ms)")
     return {"workload": "SigLIP2-so400m text tower, 5 prompts x 64 tokens, last-token pooling "
                         "+ head, host ids in / host embeddings out",
             "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
-            "ms_min": round(min(lat), 3), "iters": iters}
+            "ms_min": round(min(lat), 3), "iters": iters,
+            "ms_p50_split_k": round(pct(lat_split, 0.5), 3)}
 
 
 def cpu_baseline(args, hm, px, n_pos, gh, gw):

@@ -205,6 +205,34 @@ int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds, i
     return e == hipSuccess ? S2X_OK : hip_fail(e, "gemm launch");
 }
 
+int s2x_mul_mat_q8_0_q8_1_split_k(const s2x_weight *w, const void *qs, const void *ds, int64_t M,
+                                  float *y, int64_t ldy, const s2x_epilogue *epi, int32_t n_split,
+                                  void *workspace, size_t ws_bytes, void *stream) {
+    int st = check_q81_input(w, qs, ds, M, "mul_mat_q8_0_q8_1_split_k");
+    if (st != S2X_OK) return st;
+    EpiParams p;
+    st = check_epi(epi, w->view.N, p);
+    if (st != S2X_OK) return st;
+    if ((p.kind != EPI_NONE && p.kind != EPI_BIAS_RESID) || p.resid_rows != 0)
+        return fail(S2X_ERR_UNSUPPORTED,
+                    "mul_mat_q8_0_q8_1_split_k: epilogue NONE or BIAS_RESID (resid_rows 0) only");
+    if (n_split < 1 || n_split > 64)
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1_split_k: n_split=%d not in 1..64",
+                    (int)n_split);
+    if (!y || ldy < w->view.N || !aligned(y, 4))
+        return fail(S2X_ERR_INVALID_ARG, "mul_mat_q8_0_q8_1_split_k: y null/misaligned or ldy < N");
+    const size_t need = sizeof(float) * (size_t)n_split * (size_t)M * (size_t)w->view.N;
+    if (!workspace || !aligned(workspace, 16) || ws_bytes < need)
+        return fail(S2X_ERR_INVALID_ARG,
+                    "mul_mat_q8_0_q8_1_split_k: workspace of n_split * M * N floats needed (%zu bytes, "
+                    "16-byte aligned)", need);
+    if (M == 0) return S2X_OK;
+    hipError_t e = launch_gemm_split_k(w->view, (const int8_t *)qs, (const uint32_t *)ds,
+                                       w->view.K_pad / QK_, M, y, ldy, p, n_split,
+                                       (float *)workspace, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "split-k gemm launch");
+}
+
 size_t s2x_mul_mat_workspace_size(int64_t K_pad, int64_t N, int64_t M) {
     if (K_pad <= 0 || N <= 0 || M < 0 || K_pad % QK_ != 0) return 0;
     return mul_mat_ws_layout(K_pad, N, M).total;

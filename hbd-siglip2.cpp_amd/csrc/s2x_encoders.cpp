@@ -222,12 +222,23 @@ struct Tower {
     // ([M][kmax] int8, [M][kmax/32] ds words); qs2 / ds2: the fc1 epilogue's
     // Q8_1 output (fc2 input, K = F_pad); h16: its f16 output instead, for
     // an F16 ffn_down ([M][F_pad] halves)
-    DevBuf x, qs, ds, qs2, ds2, h16, qkv, att, attn_ws, seg, rowmap;
+    DevBuf x, qs, ds, qs2, ds2, h16, qkv, att, attn_ws, seg, rowmap, part;
     bool down_f16 = false;
     GemmTiming timing;
     // attention in fp64 (k_attn_f64, from an f32 QKV GEMM output) instead of
     // the f16-MFMA flash kernel fed by the QKV GEMM's attention-layout epilogue
     bool attn_f64 = false;
+    // K-split GEMMs (launch_gemm_split_k) for the plain and residual
+    // epilogues, an option of the text tower, whose few rows give the long-K
+    // GEMMs (fc2: 135 blocks) only tens of workgroups.  The split is a
+    // function of K, so a prompt's bits do not depend on the batch it is in;
+    // off by default, since the sums' new order moves a 27-layer random-weight
+    // text embedding to cosine ~0.99988 against the block-order oracle.
+    bool split_k = false;
+    int splits(int64_t KB, int kind) const {
+        if (!split_k || (kind != EPI_NONE && kind != EPI_BIAS_RESID)) return 1;
+        return KB >= 96 ? 4 : KB >= 32 ? 2 : 1;
+    }
     // HIP graphs of recent encodes' launch sequences (see launch_seq)
     bool graphs = true;
     struct GraphEntry {
@@ -258,7 +269,7 @@ struct Tower {
     template <class Body>
     int launch_seq(std::vector<int64_t> key, int64_t M, Body &&body) {
         if (!graphs || timing.on || M > GRAPH_MAX_ROWS || stream == nullptr) return body();
-        for (const DevBuf *b : {&x, &qs, &ds, &qs2, &ds2, &h16, &qkv, &att, &attn_ws, &seg, &rowmap})
+        for (const DevBuf *b : {&x, &qs, &ds, &qs2, &ds2, &h16, &qkv, &att, &attn_ws, &seg, &rowmap, &part})
             key.push_back((int64_t)(uintptr_t)b->p);
         key.push_back((int64_t)(uintptr_t)stream);
         key.push_back(attn_f64);
@@ -334,8 +345,12 @@ struct Tower {
             b = timing.get();
             S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        const hipError_t err = launch_gemm(w->view, xq.as<int8_t>(), xd.as<uint32_t>(),
-                                           w->view.K_pad / QK_, M, y, ldy, e, stream);
+        const int ns = splits(w->view.K_pad / QK_, e.kind);
+        const hipError_t err =
+            ns > 1 ? launch_gemm_split_k(w->view, xq.as<int8_t>(), xd.as<uint32_t>(),
+                                         w->view.K_pad / QK_, M, y, ldy, e, ns, part.as<float>(), stream)
+                   : launch_gemm(w->view, xq.as<int8_t>(), xd.as<uint32_t>(), w->view.K_pad / QK_,
+                                 M, y, ldy, e, stream);
         if (err != hipSuccess) return hip_fail(err, "gemm launch");
         if (timing.on) {
             S2X_HIP_TRY(hipEventRecord(b, stream));
@@ -408,6 +423,8 @@ struct Tower {
             S2X_TRY(ensure(attn_ws, attn_layout(n_seg, max_len, n_head, d_head).bytes, stream));
         S2X_TRY(ensure(seg, sizeof(int32_t) * (size_t)(2 * n_seg), stream));
         S2X_TRY(ensure(rowmap, sizeof(int32_t) * (size_t)M, stream));
+        // partial sums of a split GEMM: at most 4 x H (fc2) or 2 x 3 H (QKV)
+        if (split_k) S2X_TRY(ensure(part, sizeof(float) * (size_t)(M * 6 * H), stream));
         return S2X_OK;
     }
 
@@ -1031,6 +1048,12 @@ int s2x_text_set_stream(s2x_text *x, void *stream) {
 int s2x_text_set_attention_fp64(s2x_text *x, int enable) {
     if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
     x->t.attn_f64 = enable != 0;
+    return S2X_OK;
+}
+
+int s2x_text_set_split_k(s2x_text *x, int enable) {
+    if (!x) return fail(S2X_ERR_NOT_LOADED, "text: not created");
+    x->t.split_k = enable != 0;
     return S2X_OK;
 }
 

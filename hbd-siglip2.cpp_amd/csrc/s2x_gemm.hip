@@ -424,8 +424,16 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     int tm, tn;
     tile_of(xcd_linear(blockIdx.x, gridDim.x), m_tiles, n_tiles, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    const int KB_all = KB;
+    const int64_t row_bytes = (int64_t)KB_all * QK;  // X and W rows: all KB blocks
+    // a K split: this workgroup's blocks kbs .. kbs + KB - 1 (EPI_NONE)
+    int kbs = 0;
+    if (EPI == EPI_NONE && epi.kb_split > 0) {
+        kbs = (int)blockIdx.y * epi.kb_split;
+        KB = min(epi.kb_split, KB - kbs);
+        y += (int64_t)blockIdx.y * epi.y_split;
+    }
     const int n_st = (KB + KS - 1) / KS;
-    const int64_t row_bytes = (int64_t)KB * QK;
 
     // Per-lane DMA source offsets (relative to the tile's first row / column;
     // the K position goes into the scalar offset).
@@ -444,14 +452,19 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         vxs = (uint32_t)((min(wave, C::NSX - 1) * 64 + lane) * ld_ds * 4);
         vws = (uint32_t)((lane >> 4) * ldT * 2 + (lane & 15) * 16);
     }
+    // (the bases start at block kbs; the ranges end where the planes end)
     const __amdgpu_buffer_rsrc_t xr_live = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(xq + (int64_t)m0 * row_bytes), (short)0, clip32((int64_t)(M - m0) * row_bytes), BUF_DW3);
+        (void *)(xq + (int64_t)m0 * row_bytes + kbs * QK), (short)0,
+        clip32((int64_t)(M - m0) * row_bytes - kbs * QK), BUF_DW3);
     const __amdgpu_buffer_rsrc_t wr_live = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(wq + (int64_t)n0 * row_bytes), (short)0, clip32((int64_t)(N - n0) * row_bytes), BUF_DW3);
+        (void *)(wq + (int64_t)n0 * row_bytes + kbs * QK), (short)0,
+        clip32((int64_t)(N - n0) * row_bytes - kbs * QK), BUF_DW3);
     const __amdgpu_buffer_rsrc_t xsr_live = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(xds + (int64_t)m0 * ld_ds), (short)0, clip32((int64_t)(M - m0) * ld_ds * 4), BUF_DW3);
+        (void *)(xds + (int64_t)m0 * ld_ds + kbs), (short)0,
+        clip32((int64_t)(M - m0) * ld_ds * 4 - kbs * 4), BUF_DW3);
     const __amdgpu_buffer_rsrc_t wsr_live = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(wdT + n0), (short)0, clip32(((int64_t)KB * ldT - n0) * 2), BUF_DW3);
+        (void *)(wdT + (int64_t)kbs * ldT + n0), (short)0,
+        clip32(((int64_t)(KB_all - kbs) * ldT - n0) * 2), BUF_DW3);
     const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, 0, BUF_DW3);
 
     // Issue the DMA of stage g into buffer g % NS.  Reads past M, N or the
@@ -687,9 +700,11 @@ hipError_t run(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64
         attr_set = true;
     }
     const int64_t tiles = ((M + C::BM - 1) / C::BM) * ((w.N + BN - 1) / BN);
+    const int64_t KB = w.K_pad / QK;
+    const unsigned splits = epi.kb_split > 0 ? (unsigned)((KB + epi.kb_split - 1) / epi.kb_split) : 1u;
     // without scales (the block-dot dump) the scale DMA reads a zero-size
     // buffer at a valid address
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::NT), C::LDS_BYTES, stream,
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, splits), dim3(C::NT), C::LDS_BYTES, stream,
                        reinterpret_cast<const uint8_t *>(xq),
                        xds ? xds : reinterpret_cast<const uint32_t *>(xq), xds ? ld_ds : 0,
                        reinterpret_cast<const uint8_t *>(w.qs), w.dT, w.ldT, (int)M, (int)w.N,
@@ -844,6 +859,68 @@ hipError_t run_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16
 }
 
 }  // namespace gemm
+
+// y = ((p_0 + p_1) + ...) [+ bias] [+ resid], 4 columns per thread (N % 4
+// == 0) or 1; y may be resid itself (each element read, then written, by
+// one thread)
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int n_split,
+                                                   int64_t plane, int64_t M, int64_t N,
+                                                   const float *__restrict__ bias,
+                                                   const float *resid, int64_t ld_resid,
+                                                   float *y, int64_t ldy) {
+    constexpr int W = VEC ? 4 : 1;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t nq = N / W;
+    if (i >= M * nq) return;
+    const int64_t m = i / nq, n = (i - m * nq) * W;
+    float v[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) v[j] = part[m * N + n + j];
+    for (int s = 1; s < n_split; ++s)
+#pragma unroll
+        for (int j = 0; j < W; ++j) v[j] = v[j] + part[s * plane + m * N + n + j];
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+        if (bias) v[j] = v[j] + bias[n + j];
+        if (resid) v[j] = v[j] + resid[m * ld_resid + n + j];
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) y[m * ldy + n + j] = v[j];
+}
+
+hipError_t launch_gemm_split_k(const WeightView &w, const int8_t *xq, const uint32_t *xds,
+                               int64_t ld_ds, int64_t M, float *y, int64_t ldy,
+                               const EpiParams &epi, int n_split, float *part,
+                               hipStream_t stream) {
+    if (M == 0 || w.N == 0) return hipSuccess;
+    const int64_t KB = w.K_pad / QK;
+    const bool resid = epi.kind == EPI_BIAS_RESID;
+    if ((epi.kind != EPI_NONE && !resid) || n_split < 1 || !part || ldy < w.N ||
+        (resid && (!epi.resid || epi.ld_resid < w.N || epi.resid_rows != 0)))
+        return hipErrorInvalidValue;
+    // whole 4-block stages per range
+    const int64_t per = ((KB + n_split - 1) / n_split + 3) / 4 * 4;
+    const int64_t splits = (KB + per - 1) / per;
+    EpiParams e{};
+    e.kind = EPI_NONE;
+    e.kb_split = (int)per;
+    e.y_split = M * w.N;
+    hipError_t err = launch_gemm(w, xq, xds, ld_ds, M, part, w.N, e, stream);
+    if (err != hipSuccess) return err;
+    const bool vec = w.N % 4 == 0 && ldy % 4 == 0 && (!resid || epi.ld_resid % 4 == 0);
+    const int64_t n = M * (vec ? w.N / 4 : w.N);
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (vec)
+        hipLaunchKernelGGL(k_split_sum<true>, dim3(grid), dim3(256), 0, stream, part,
+                           (int)splits, M * w.N, M, w.N, resid ? epi.bias : nullptr, resid ? epi.resid : nullptr,
+                           epi.ld_resid, y, ldy);
+    else
+        hipLaunchKernelGGL(k_split_sum<false>, dim3(grid), dim3(256), 0, stream, part,
+                           (int)splits, M * w.N, M, w.N, resid ? epi.bias : nullptr, resid ? epi.resid : nullptr,
+                           epi.ld_resid, y, ldy);
+    return hipGetLastError();
+}
 
 // Stage configurations: 4-block stages in a ring of 2.  Wide: 128 x 128
 // tiles, two workgroups per CU, for GEMMs of enough tiles to fill the chip.

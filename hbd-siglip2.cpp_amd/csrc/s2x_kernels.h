@@ -61,6 +61,11 @@ struct EpiParams {
     // EPI_GELU_F16: f16 rows [M][h_ld], columns N..h_kpad-1 written as zero
     _Float16 *h_out;
     int64_t   h_ld, h_kpad;
+    // K split (EPI_NONE only; set by launch_gemm_split_k): workgroup row
+    // blockIdx.y sums blocks [kb_split * y, min(KB, kb_split * (y + 1)))
+    // into the outputs at y + blockIdx.y * y_split
+    int       kb_split;
+    int64_t   y_split;
 };
 
 // a1: F32 -> Q8_1 into the planes of `out`.
@@ -82,6 +87,18 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
 // of 32, e.g. ffn_down): Y = W16 x f16(X) with f32 accumulation on f16 MFMA.
 // w16: N rows of K_pad halves, x16: M rows of K_pad halves (both zero past
 // K, 16-byte aligned rows); epilogues NONE, BIAS, BIAS_RESID.
+// The same product as launch_gemm with EPI_NONE / EPI_BIAS_RESID, its K
+// blocks in n_split contiguous ranges of whole 4-block stages (a function of
+// K alone): each range's sum, in block order from zero, goes to a partial
+// plane of `part` (n_split x M x N floats) in one launch of
+// n_split x the tiles, then y = ((p_0 + p_1) + ...) [+ bias] [+ resid] in
+// that order.  For GEMMs of too few tiles to fill the chip (a text batch);
+// the bits depend on K and n_split, not on M.
+hipError_t launch_gemm_split_k(const WeightView &w, const int8_t *xq, const uint32_t *xds,
+                               int64_t ld_ds, int64_t M, float *y, int64_t ldy,
+                               const EpiParams &epi, int n_split, float *part,
+                               hipStream_t stream);
+
 hipError_t launch_gemm_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16 *x16,
                            int64_t M, float *y, int64_t ldy, const EpiParams &epi,
                            hipStream_t stream);

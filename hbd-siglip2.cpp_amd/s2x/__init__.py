@@ -117,6 +117,8 @@ _sig("s2x_weight_destroy", [_p], None)
 _sig("s2x_weight_k", [_p], _i64)
 _sig("s2x_weight_n", [_p], _i64)
 _sig("s2x_mul_mat_q8_0_q8_1", [_p, _p, _p, _i64, _p, _i64, ctypes.POINTER(Epilogue), _p])
+_sig("s2x_mul_mat_q8_0_q8_1_split_k",
+     [_p, _p, _p, _i64, _p, _i64, ctypes.POINTER(Epilogue), ctypes.c_int32, _p, _sz, _p])
 _sig("s2x_mul_mat_workspace_size", [_i64, _i64, _i64], _sz)
 _sig("s2x_mul_mat_q8_0_f32", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _sz, _p])
 _sig("s2x_mul_mat_q8_0_f32_static", [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p])
@@ -151,6 +153,7 @@ _sig("s2x_vision_set_graphs", [_p, ctypes.c_int])
 _sig("s2x_vision_encode_rgb_batch_dev", [_p, _p, _p, _i32, _i32, _f32, _p, _p, _i32, _p])
 _sig("s2x_text_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_text_set_graphs", [_p, ctypes.c_int])
+_sig("s2x_text_set_split_k", [_p, ctypes.c_int])
 _sig("s2x_vision_encode", [_p, _p, _i32, _i32, _i32, _p])
 _sig("s2x_vision_encode_batch_dev", [_p, _p, _i32, _i32, _i32, _i32, _p])
 _sig("s2x_vision_encode_ragged_dev", [_p, _p, _p, _i32, _i32, _i32, _p])

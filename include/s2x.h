@@ -123,6 +123,19 @@ int s2x_mul_mat_q8_0_q8_1(const s2x_weight *w, const void *qs, const void *ds,
                           int64_t M, float *y, int64_t ldy,
                           const s2x_epilogue *epi, void *stream);
 
+/* s2x_mul_mat_q8_0_q8_1 with the K blocks in n_split contiguous ranges of
+ * whole 4-block stages, summed separately (each in block order from zero)
+ * and then added in range order: y = ((p_0 + p_1) + ...) [+ bias]
+ * [+ resid].  Epilogue NONE or BIAS_RESID (resid_rows 0); workspace: n_split
+ * * M * N floats, 16-byte aligned.  No counterpart in the reference: the
+ * form the text encoder runs for its long-K GEMMs, whose few rows give one
+ * launch per K range too few workgroups; its bits depend on K and n_split,
+ * not on M. */
+int s2x_mul_mat_q8_0_q8_1_split_k(const s2x_weight *w, const void *qs, const void *ds,
+                                  int64_t M, float *y, int64_t ldy,
+                                  const s2x_epilogue *epi, int32_t n_split,
+                                  void *workspace, size_t ws_bytes, void *stream);
+
 /* Drop-in GGML_OP_MUL_MAT(W: Q8_0 raw device blocks (K_pad, N), X: F32
  * (K, M)) -> Y: F32 (N, M).  X is quantized to Q8_1 (K zero-padded to K_pad)
  * and W repacked inside `workspace`, whose size s2x_mul_mat_workspace_size()
@@ -456,6 +469,12 @@ int s2x_text_set_stream(s2x_text *t, void *stream);
 int s2x_text_set_attention_fp64(s2x_text *t, int enable);
 /* As s2x_vision_set_graphs, for the text tower. */
 int s2x_text_set_graphs(s2x_text *t, int enable);
+/* 1 = the text tower's plain and residual GEMMs of 32+ K blocks run as
+ * s2x_mul_mat_q8_0_q8_1_split_k (2 ranges, 4 from 96 blocks); 0 (default) =
+ * one block-order sum per output, the oracle's.  No counterpart in the
+ * reference (whose GPU GEMMs split K by stream-K); a prompt's bits do not
+ * depend on its batch either way. */
+int s2x_text_set_split_k(s2x_text *t, int enable);
 /* TextEncoder::encode: one prompt of n_tok ids (host), optional host mask
  * (1 = valid), out_host proj floats.  Synchronous. */
 int s2x_text_encode(s2x_text *t, const int32_t *ids_host, int32_t n_tok,

@@ -353,6 +353,28 @@ def test_so400m_vision_naflex16_workload(orc, so400m_vision):
 
 
 @pytest.mark.timeout(600)
+def test_so400m_text_split_k(orc):
+    # the K-split GEMM option: a prompt's bits do not depend on its batch;
+    # against the block-order oracle the 27 random-weight layers amplify the
+    # new summation order to cosine ~0.99988 (the tower's sensitivity, not an
+    # error of the split: each split GEMM is bit-exact against its oracle
+    # restatement in test_gemm_split_k_bit_exact)
+    hm = synth.text_model(synth.SO400M_TEXT, seed=0)
+    t = Text(hm)
+    try:
+        s2x.call("s2x_text_set_split_k", t.h, 1)
+        om = orc.text_model(hm)
+        ids, _ = synth.text_tokens(5, 64)
+        b = t.batch(ids)
+        assert np.array_equal(t.encode(ids[3]), b[3])
+        c = cos(b[0], orc.text_encode(om, ids[0]))
+        say(f"so400m text, K-split GEMMs: cosine {c:.7f}")
+        assert c >= 0.9998
+    finally:
+        t.close()
+
+
+@pytest.mark.timeout(600)
 def test_so400m_text_5x64_vs_oracle(orc):
     say("generating so400m text weights")
     hm = synth.text_model(synth.SO400M_TEXT, seed=0)

@@ -299,6 +299,67 @@ def test_gemm_epilogues(orc, gemm_data, kind):
     assert_same(yg, ref.astype(np.float32), f"epilogue {kind}")
 
 
+def _split_ref(orc, raw, N, K_pad, rq, rd, n_split):
+    """The split form restated on the oracle: each K range's product from
+    the oracle's own block-order GEMM on that slice, then added in range
+    order in f32."""
+    KB = K_pad // 32
+    per = ((KB + n_split - 1) // n_split + 3) // 4 * 4
+    blocks = raw.reshape(N, KB, 34)
+    acc = None
+    for a in range(0, KB, per):
+        b = min(KB, a + per)
+        p = orc.mul_mat_q8_0_q8_1(np.ascontiguousarray(blocks[:, a:b]).reshape(-1), (b - a) * 32, N,
+                                  np.ascontiguousarray(rq[:, a * 32:b * 32]),
+                                  np.ascontiguousarray(rd[:, a:b]))
+        acc = p if acc is None else (acc + p).astype(np.float32)
+    return acc, (KB + per - 1) // per
+
+
+# fc2 (135 blocks) in 4 ranges, out (36) in 2, a 13-block K in 3 requested
+# (2 ranges of whole stages); M = 320 (a 5 x 64 text batch) and its first 64
+# rows alone, which must give the same bits
+@pytest.mark.parametrize("case", [("fc2", 4, "resid"), ("out", 2, "resid"), ("out", 2, "none"),
+                                  ("k13", 3, "resid")])
+def test_gemm_split_k_bit_exact(orc, gemm_data, case):
+    label, n_split, kind = case
+    if label == "k13":
+        N, K_pad = 200, 13 * 32
+        K = K_pad - 5
+        raw = synth.quantize_q8_0(np.random.default_rng(41).normal(0, 0.02, (N, K)).astype(np.float32), K_pad)
+    else:
+        raw, N, K, K_pad = gemm_data[label]
+    rng = np.random.default_rng(9)
+    bias = rng.normal(0, 0.02, N).astype(np.float32)
+    say(f"split-K gemm {label} n_split={n_split} {kind}")
+    outs = {}
+    for M in (320, 64):
+        x = np.random.default_rng(12).standard_normal((320, K)).astype(np.float32)[:M]
+        res = np.random.default_rng(13).standard_normal((320, N)).astype(np.float32)[:M]
+        qs, ds = _quant_gpu(x, K_pad)
+        rq, rd = orc.quantize_q8_1(x, K_pad)
+        ref, splits = _split_ref(orc, raw, N, K_pad, rq, rd, n_split)
+        e = s2x.Epilogue()
+        bd, rdv = dev(bias), dev(res)
+        if kind == "resid":
+            e.kind, e.bias, e.resid, e.ld_resid = s2x.EPI_BIAS_RESID, bd.data_ptr(), rdv.data_ptr(), N
+            ref = (ref + bias) + res
+        else:
+            e.kind = s2x.EPI_NONE
+        y = rdv if kind == "resid" else empty((M, N), torch.float32)  # in place on the residual
+        ws = empty((n_split * M * N,), torch.float32)
+        w = _weight(raw, K_pad, N)
+        try:
+            s2x.call("s2x_mul_mat_q8_0_q8_1_split_k", w, ptr(qs), ptr(ds), M, ptr(y), N, ctypes.byref(e),
+                     n_split, ptr(ws), ws.numel() * 4, stream())
+            outs[M] = host(y)
+        finally:
+            s2x.lib.s2x_weight_destroy(w)
+        assert splits > 1
+        assert_same(outs[M], ref.astype(np.float32), f"split-K {label} M={M}")
+    assert np.array_equal(outs[64], outs[320][:64])
+
+
 def test_standalone_epilogues(orc):
     rng = np.random.default_rng(9)
     H, n = 4304, 37
