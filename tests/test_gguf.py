@@ -11,7 +11,8 @@ import pytest
 
 import s2x
 from s2x import synth
-from gguf_util import T_F16, text_tensors, vision_tensors, write_gguf
+from gguf_util import GT_F32 as GT_F32_, GT_STRING as GT_STR_, GT_U32 as GT_U32_
+from gguf_util import T_F16, T_F32 as T_F32_, text_tensors, vision_tensors, write_gguf
 
 SMALL_V = synth.VisionConfig(hidden=288, inter=1076, n_head=4, n_layer=2)
 SMALL_T = synth.TextConfig(hidden=288, inter=1076, n_head=4, n_layer=2, vocab=1000, max_pos=64,
@@ -206,3 +207,50 @@ def test_gguf_rejects_bad_files(tmp_path):
         s2x.lib.s2x_gguf_close(g)
 
     assert _open(tmp_path / "does-not-exist.gguf")[0] != 0
+
+
+def _converter_names():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "converter_names.json")) as f:
+        return json.load(f)
+
+
+def _keep_f32(name, rule):
+    return (any(name.endswith(s) for s in rule["suffixes"]) or
+            any(s in name for s in rule["substrings"]) or name in rule["names"])
+
+
+def test_names_match_reference_converter():
+    """The writer above and the reader are pinned to the names the
+    reference's converter emits (tests/golden/converter_names.json, read from
+    its source by tests/golden/make_converter_names.py): the same tensor set
+    for a 2-layer tower, F32 exactly where the converter keeps F32, and the
+    metadata keys with the converter's types."""
+    import os
+    import re
+    ref = _converter_names()
+    n_layer = 2
+    gt = {GT_U32_: "uint32", GT_F32_: "float32", GT_STR_: "string"}
+    for tower, hm, fn, own in (("v", synth.vision_model(SMALL_V, seed=3), vision_tensors, ref["vision_tensors"]),
+                               ("t", synth.text_model(SMALL_T, seed=4), text_tensors, ref["text_tensors"])):
+        kv, ts = fn(hm)
+        want = set(own) | {f"{tower}.blk.{i}.{b}" for i in range(n_layer) for b in ref["block_tensors"]}
+        names = [n for n, _, _, _ in ts]
+        assert len(names) == len(set(names))
+        assert set(names) == want, (set(names) ^ want)
+        for n, t, _, _ in ts:
+            # converter F32 tensors: F32 here; its matrices: Q8_0 (or F16 ffn_down)
+            assert (t == T_F32_) == _keep_f32(n, ref["keep_f32"]), n
+        for key, t, _ in kv:
+            if key.startswith(ref["arch"] + "."):
+                assert ref["metadata"].get(key) == gt[t], key
+    # every name the reader binds is one the converter writes
+    src = open(os.path.join(os.path.dirname(__file__), "..", "hbd-siglip2.cpp_amd", "csrc",
+                            "s2x_gguf.cpp")).read()
+    lit = set(re.findall(r'"((?:v|t)\.[\w.]+|siglip2\.[\w.]+)"', src))
+    blk = set(re.findall(r'blk\(tower, i, "([\w.]+)"\)', src))
+    assert lit and blk
+    every = set(ref["vision_tensors"]) | set(ref["text_tensors"]) | set(ref["metadata"])
+    assert lit <= every, lit - every
+    assert blk == set(ref["block_tensors"])
