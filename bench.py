@@ -37,7 +37,8 @@ F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA, published
 METRIC = "images/sec SigLIP2 vision Q8_0 @729 patches; MMQ int8 TOPS % of peak"
 KERNEL = ("k_gemm (Q8_0 x Q8_1 GEMM, 128x128 tiles of 8 waves, two workgroups per CU: int8 "
           "quants and scales by LDS DMA in 4-block stages, v_mfma_i32_32x32x32_i8 block dots, "
-          "dx*dw scale tile on v_mfma_f32_32x32x8_f16, one convert + fma per element and block; "
+          "the int-to-float conversion and the dx*dw scale tile on v_mfma_f32_32x32x8_f16, one "
+          "fma per element and block; "
           "priced against the int8 peak)")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_vision_b32_traffic.json")
 
