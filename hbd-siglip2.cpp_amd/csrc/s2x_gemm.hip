@@ -947,7 +947,8 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
         M > (1 << 30) || w.N > (1 << 30) || ((uintptr_t)xq & 15) || ((uintptr_t)w.qs & 15) ||
         ((uintptr_t)xds & 3) || (epi.kind != EPI_DUMP_I && (!xds || ld_ds < KB)) ||
         (int64_t)C::BM * KB * QK > 0x7fffffff || w.ldT * KB * 2 > 0x7fffffff ||
-        C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff)
+        C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff ||
+        (epi.kb_split != 0 && (epi.kind != EPI_NONE || epi.kb_split < 0 || epi.y_split < M * ldy)))
         return hipErrorInvalidValue;
 #define S2X_RUN(E)                                                                    \
     (use_small(M, w.N) ? gemm::run<Small, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
