@@ -251,27 +251,42 @@ def bench_batch1(step, sync, gemm_stats, v, s2x, np, iters=60):
     s2x.call("s2x_vision_set_graphs", v, 0)
     lat_plain = latencies()
     s2x.call("s2x_vision_set_graphs", v, 1)
-    # the GEMM rate at M = 729 from event-timed launches (plain launches)
-    gemm_stats()
-    s2x.call("s2x_vision_gemm_timing", v, 1)
-    n_rate = 20
-    for _ in range(n_rate):
-        step(1)
-    sync()
-    g_ms, g_ops, g_launches = gemm_stats()
-    s2x.call("s2x_vision_gemm_timing", v, 0)
-    tops = g_ops / (g_ms / 1000.0) / 1e12
+    # the GEMM rate at M = 729 from event-timed launches (plain launches;
+    # a K-split GEMM's time spans its partial-sum launch and the sum pass)
+    def rate(n_rate=20):
+        gemm_stats()
+        s2x.call("s2x_vision_gemm_timing", v, 1)
+        for _ in range(n_rate):
+            step(1)
+        sync()
+        g_ms, g_ops, _ = gemm_stats()
+        s2x.call("s2x_vision_gemm_timing", v, 0)
+        return g_ops / (g_ms / 1000.0) / 1e12, g_ms / n_rate
+
+    tops, g_img = rate()
+    # the K-split GEMM option (s2x_vision_set_split_k): other bits, same
+    # arithmetic per K range
+    s2x.call("s2x_vision_set_split_k", v, 1)
+    lat_split = latencies()
+    tops_split, g_img_split = rate()
+    s2x.call("s2x_vision_set_split_k", v, 0)
     p50 = pct(lat, 0.5)
-    log(f"bench: batch 1: p50 {p50:.3f} ms (plain launches {pct(lat_plain, 0.5):.3f}), p99 "
-        f"{pct(lat, 0.99):.3f} ms, GEMM {tops:.1f} TOPS at M = 729 ({g_ms / n_rate:.3f} ms of "
-        f"GEMM per image)")
+    log(f"bench: batch 1: p50 {p50:.3f} ms (plain launches {pct(lat_plain, 0.5):.3f}, K-split "
+        f"GEMMs {pct(lat_split, 0.5):.3f}), p99 {pct(lat, 0.99):.3f} ms, GEMM {tops:.1f} TOPS at "
+        f"M = 729 ({g_img:.3f} ms of GEMM per image; K-split {tops_split:.1f} TOPS, "
+        f"{g_img_split:.3f} ms)")
     return {"workload": "SigLIP2-so400m vision tower, 1 image x 729 patches, probe pooling",
             "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
             "ms_min": round(min(lat), 3), "images_per_s": round(1000.0 / p50, 1),
             "ms_p50_plain_launches": round(pct(lat_plain, 0.5), 3),
             "iters": iters, "gemm_tops": round(tops, 1),
             "gemm_frac": round(tops / INT8_PEAK_TOPS, 4),
-            "gemm_ms_per_image": round(g_ms / n_rate, 3)}
+            "gemm_ms_per_image": round(g_img, 3),
+            "split_k": {"ms_p50": round(pct(lat_split, 0.5), 3),
+                        "images_per_s": round(1000.0 / pct(lat_split, 0.5), 1),
+                        "gemm_tops": round(tops_split, 1),
+                        "gemm_frac": round(tops_split / INT8_PEAK_TOPS, 4),
+                        "gemm_ms_per_image": round(g_img_split, 3)}}
 
 
 def bench_gemm_shapes(np, torch, s2x, synth, warm=20, iters=200):

@@ -229,14 +229,17 @@ struct Tower {
     // the f16-MFMA flash kernel fed by the QKV GEMM's attention-layout epilogue
     bool attn_f64 = false;
     // K-split GEMMs (launch_gemm_split_k) for the plain and residual
-    // epilogues, an option of the text tower, whose few rows give the long-K
-    // GEMMs (fc2: 135 blocks) only tens of workgroups.  The split is a
-    // function of K, so a prompt's bits do not depend on the batch it is in;
-    // off by default, since the sums' new order moves a 27-layer random-weight
-    // text embedding to cosine ~0.99988 against the block-order oracle.
+    // epilogues, an option of both towers for encodes of few rows (text
+    // prompts, one image), whose long-K GEMMs (fc2: 135 blocks) otherwise
+    // get only tens of workgroups.  The split is a function of K, so an
+    // input's bits do not depend on the batch it is in (with the option set
+    // the same way); off by default, since the sums' new order moves a
+    // 27-layer random-weight embedding to cosine ~0.9999 against the
+    // block-order oracle.
     bool split_k = false;
-    int splits(int64_t KB, int kind) const {
-        if (!split_k || (kind != EPI_NONE && kind != EPI_BIAS_RESID)) return 1;
+    int splits(int64_t KB, const EpiParams &e) const {
+        if (!split_k || (e.kind != EPI_NONE && e.kind != EPI_BIAS_RESID) || e.resid_rows != 0)
+            return 1;
         return KB >= 96 ? 4 : KB >= 32 ? 2 : 1;
     }
     // HIP graphs of recent encodes' launch sequences (see launch_seq)
@@ -273,6 +276,7 @@ struct Tower {
             key.push_back((int64_t)(uintptr_t)b->p);
         key.push_back((int64_t)(uintptr_t)stream);
         key.push_back(attn_f64);
+        key.push_back(split_k);
         size_t i = 0;
         while (i < gcache.size() && gcache[i].key != key) ++i;
         if (i == gcache.size()) {  // first call with this key
@@ -345,7 +349,7 @@ struct Tower {
             b = timing.get();
             S2X_HIP_TRY(hipEventRecord(a, stream));
         }
-        const int ns = splits(w->view.K_pad / QK_, e.kind);
+        const int ns = splits(w->view.K_pad / QK_, e);
         const hipError_t err =
             ns > 1 ? launch_gemm_split_k(w->view, xq.as<int8_t>(), xd.as<uint32_t>(),
                                          w->view.K_pad / QK_, M, y, ldy, e, ns, part.as<float>(), stream)
@@ -742,6 +746,12 @@ int s2x_vision_set_stream(s2x_vision *v, void *stream) {
 int s2x_vision_set_attention_fp64(s2x_vision *v, int enable) {
     if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
     v->t.attn_f64 = enable != 0;
+    return S2X_OK;
+}
+
+int s2x_vision_set_split_k(s2x_vision *v, int enable) {
+    if (!v) return fail(S2X_ERR_NOT_LOADED, "vision: not created");
+    v->t.split_k = enable != 0;
     return S2X_OK;
 }
 

@@ -150,6 +150,7 @@ _sig("s2x_vision_destroy", [_p], None)
 _sig("s2x_vision_set_stream", [_p, _p])
 _sig("s2x_vision_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_vision_set_graphs", [_p, ctypes.c_int])
+_sig("s2x_vision_set_split_k", [_p, ctypes.c_int])
 _sig("s2x_vision_encode_rgb_batch_dev", [_p, _p, _p, _i32, _i32, _f32, _p, _p, _i32, _p])
 _sig("s2x_text_set_attention_fp64", [_p, ctypes.c_int])
 _sig("s2x_text_set_graphs", [_p, ctypes.c_int])

@@ -415,6 +415,13 @@ int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
  * later ones replay it (up to 4 shapes per encoder).  Results are the same
  * bits either way. */
 int s2x_vision_set_graphs(s2x_vision *v, int enable);
+/* 1 = the vision tower's plain and residual GEMMs of 32+ K blocks (out,
+ * fc2, the head's) run as s2x_mul_mat_q8_0_q8_1_split_k (2 ranges, 4 from
+ * 96 blocks), for latency at batch 1; 0 (default) = one block-order sum per
+ * output, the oracle's.  No counterpart in the reference (whose GPU GEMMs
+ * split K by stream-K); an image's bits do not depend on its batch either
+ * way.  Batch 32 runs slower with it (partial sums of 4 x 107 MB per fc2). */
+int s2x_vision_set_split_k(s2x_vision *v, int enable);
 /* Reference signature (VisionEncoder::encode): one image, host pixels
  * [n_h*n_w, patch_dim], host output `hidden` floats. Synchronous. */
 int s2x_vision_encode(s2x_vision *v, const float *pixels_host, int32_t n_h,

@@ -286,6 +286,35 @@ def test_so400m_vision_batch_and_ragged_invariance(so400m_vision):
 
 
 @pytest.mark.timeout(600)
+def test_so400m_vision_split_k(orc, so400m_vision):
+    # the K-split GEMM option for batch-1 latency: an image's bits do not
+    # depend on its batch with the option on, graph replays follow the
+    # option as it is set, and the embedding stays within the tower's
+    # sensitivity of the block-order oracle (each split GEMM is bit-exact
+    # against its oracle restatement in test_gemm_split_k_bit_exact)
+    v, om = so400m_vision
+    px = synth.pixels(3, 729, seed=4321)
+    plain = v.encode(px[:729], 27, 27, s2x.POOL_PROBE)
+    s2x.call("s2x_vision_set_split_k", v.h, 1)
+    try:
+        # eager, captured, replayed
+        split = [v.encode(px[:729], 27, 27, s2x.POOL_PROBE) for _ in range(3)]
+        assert all(np.array_equal(split[0], g) for g in split[1:])
+        assert not np.array_equal(split[0], plain)
+        b = v.batch(px, 3, 27, 27, s2x.POOL_PROBE)
+        assert np.array_equal(b[0], split[0])
+        assert np.array_equal(b[2], v.batch(px[2 * 729:], 1, 27, 27, s2x.POOL_PROBE)[0])
+        r = orc.vision_encode(om, px[:729], 27, 27, pooling=1)
+        c = cos(split[0], r)
+        say(f"so400m vision 27x27, K-split GEMMs: cosine {c:.7f} (block order: {cos(plain, r):.7f})")
+        assert c >= 0.9998
+    finally:
+        s2x.call("s2x_vision_set_split_k", v.h, 0)
+    for _ in range(2):
+        assert np.array_equal(v.encode(px[:729], 27, 27, s2x.POOL_PROBE), plain)
+
+
+@pytest.mark.timeout(600)
 def test_so400m_vision_naflex_vs_oracle(orc, so400m_vision):
     v, om = so400m_vision
     h, w = 16, 64
