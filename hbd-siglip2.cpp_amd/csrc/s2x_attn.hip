@@ -156,19 +156,17 @@ hipError_t launch_attn_prep(const float *qkv, int64_t ld_qkv, const float *qkv_b
 // owns whole blocks {0, 1}, {3}, {5}, {7, 8} of its group (r = 0 .. 3) and
 // quantizes them in its epilogue; blocks 2, 4, 6 straddle heads (r, r + 1),
 // so their columns are written as f32 and a second pass (k_quant_straddle)
-// quantizes them.  Both apply k_quantize_q8_1's arithmetic to the same f32
-// values: the same bits as quantizing the whole f32 output.
+// quantizes them -- or, where a workgroup runs all four heads of a group in
+// turn (launches of enough workgroups, batch 32), each lane keeps its
+// columns of the block the next head completes in LDS, and that head's
+// epilogue quantizes it.  All apply k_quantize_q8_1's arithmetic to the same
+// f32 values: the same bits as quantizing the whole f32 output.
 // ---------------------------------------------------------------------------
-template <int M0>  // first 8-column group of the block within the head
-__device__ __forceinline__ void attn_q81_block(const v16f (&o)[3], float inv, int lh,
-                                               int8_t *qrow, uint32_t *dsrow, int kb) {
-    float v[16];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[4 * k + i] = o[(M0 + k) / 4][4 * ((M0 + k) % 4) + i] * inv;
-    // lane lh holds columns 8 m + 4 lh + 0..3 of each group m: the block is
-    // this lane's 16 values and lane l ^ 32's
+// One Q8_1 block of a row from this lane's 16 values v[4 k + i] (columns
+// 8 k + 4 lh + i of the block, k, i = 0..3) and lane l ^ 32's (the other
+// 4 columns of each 8): quants at qblk + 8 k + 4 lh, its scale word at *ds.
+__device__ __forceinline__ void q81_block16(const float (&v)[16], int lh, int8_t *qblk,
+                                            uint32_t *ds) {
     float a = 0.0f;
 #pragma unroll
     for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
@@ -180,12 +178,24 @@ __device__ __forceinline__ void attn_q81_block(const v16f (&o)[3], float inv, in
     for (int k = 0; k < 4; ++k) {
         const int q0 = q8_round(v[4 * k], qinv), q1 = q8_round(v[4 * k + 1], qinv);
         const int q2 = q8_round(v[4 * k + 2], qinv), q3 = q8_round(v[4 * k + 3], qinv);
-        *reinterpret_cast<uint32_t *>(qrow + 8 * (M0 + k) + 4 * lh) = pack4_i8(q0, q1, q2, q3);
+        *reinterpret_cast<uint32_t *>(qblk + 8 * k + 4 * lh) = pack4_i8(q0, q1, q2, q3);
         sq += q0 + q1 + q2 + q3;
     }
     sq += __shfl_xor(sq, 32);
-    if (lh == 0)
-        dsrow[kb] = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)sq * d) << 16);
+    if (lh == 0) *ds = (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)sq * d) << 16);
+}
+
+template <int M0>  // first 8-column group of the block within the head
+__device__ __forceinline__ void attn_q81_block(const v16f (&o)[3], float inv, int lh,
+                                               int8_t *qrow, uint32_t *dsrow, int kb) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * k + i] = o[(M0 + k) / 4][4 * ((M0 + k) % 4) + i] * inv;
+    // lane lh holds columns 8 m + 4 lh + 0..3 of each group m: the block is
+    // this lane's 16 values and lane l ^ 32's
+    q81_block16(v, lh, qrow + 8 * M0, dsrow + kb);
 }
 
 template <int M>  // an 8-column group written as f32 (part of a straddling block)
@@ -221,6 +231,50 @@ __device__ __forceinline__ void attn_q81_row(const v16f (&o)[3], float inv, int 
         attn_f32_group<0>(o, inv, lh, orow);
         attn_q81_block<1>(o, inv, lh, qrow, dsrow, kb0 + 7);
         attn_q81_block<5>(o, inv, lh, qrow, dsrow, kb0 + 8);
+    }
+}
+
+// Epilogue of one query row for head R of a group of four run by one
+// workgroup: qg / dsg are the row's quants and scale words of the group
+// (288 columns, blocks 0..8); st[64 i], i < 12, is this lane's LDS slot i,
+// which carries the 8-column groups of head R - 1 that open block 2 R.
+template <int R>
+__device__ __forceinline__ void attn_q81_group_row(const v16f (&o)[3], float inv, int lh,
+                                                   int8_t *qg, uint32_t *dsg, float *st) {
+    constexpr int NK = R;        // 8-column groups of block 2 R held from head R - 1
+    constexpr int NH = 4 - NK;   // its groups from this head: 0 .. NH - 1
+    int8_t *qh = qg + 72 * R;    // this head's first column
+    if constexpr (R > 0) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[4 * k + i] = st[64 * (4 * k + i)];
+#pragma unroll
+        for (int k = 0; k < NH; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[4 * (NK + k) + i] = o[k / 4][4 * (k % 4) + i] * inv;
+        q81_block16(v, lh, qg + 64 * R, dsg + 2 * R);
+    }
+    // whole blocks of this head, then the groups that open block 2 R + 2
+    if constexpr (R == 0) {
+        attn_q81_block<0>(o, inv, lh, qh, dsg, 0);
+        attn_q81_block<4>(o, inv, lh, qh, dsg, 1);
+    } else if constexpr (R == 1) {
+        attn_q81_block<3>(o, inv, lh, qh, dsg, 3);
+    } else if constexpr (R == 2) {
+        attn_q81_block<2>(o, inv, lh, qh, dsg, 5);
+    } else {
+        attn_q81_block<1>(o, inv, lh, qh, dsg, 7);
+        attn_q81_block<5>(o, inv, lh, qh, dsg, 8);
+    }
+    if constexpr (R < 3) {
+        constexpr int NS = R + 1;  // groups 9 - NS .. 8 of this head
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                st[64 * (4 * k + i)] = o[(9 - NS + k) / 4][4 * ((9 - NS + k) % 4) + i] * inv;
     }
 }
 
@@ -269,279 +323,305 @@ constexpr int FA_WAVES = 12;  // waves (32 queries each) per workgroup
 constexpr int FA_WAVES_SMALL = 4;  // the same for launches of few workgroups
 constexpr float P_SHIFT = 15.0f;  // log2 of the largest P of a row (<= 65504 as f16)
 
-template <bool P_SPLIT, int NW, bool QUANT>
+// G4 (with QUANT): one workgroup runs the four heads of a group in turn and
+// quantizes every Q8_1 block of its rows itself (no f32 output, no second
+// pass); each lane's columns of the block that the next head completes wait
+// in an LDS slot of its own.
+template <bool P_SPLIT, int NW, bool QUANT, bool G4 = false>
 __global__ __launch_bounds__(64 * NW) void k_attn(
     const _Float16 *__restrict__ Q, const _Float16 *__restrict__ K,
     const _Float16 *__restrict__ Vt, const int32_t *__restrict__ seg_start,
     const int32_t *__restrict__ seg_len, const uint8_t *__restrict__ key_valid,
     int n_head, int d_head, int len_pad, int n_qt, float scale_log2, float *__restrict__ out,
     int64_t ld_out, Q81Out qo, int64_t ld_q) {
+    static_assert(!G4 || QUANT, "the grouped form writes Q8_1 only");
     __shared__ __align__(16) _Float16 lds[2 * FA_STAGE];
-    // (query tile, head, segment), query tile fastest, in XCD-contiguous
-    // order: the query tiles of one head share their XCD's L2 for K and V^T
+    __shared__ float stash[G4 ? 12 * 64 * NW : 1];
+    // (query tile, head or group of four heads, segment), query tile
+    // fastest, in XCD-contiguous order: the query tiles of one head share
+    // their XCD's L2 for K and V^T
+    constexpr int HPW = G4 ? 4 : 1;  // heads per workgroup
+    const int n_hg = n_head / HPW;
     const int wg = xcd_linear(blockIdx.x, gridDim.x);
-    const int qt = wg % n_qt, h = (wg / n_qt) % n_head, sg = wg / (n_qt * n_head);
+    const int qt = wg % n_qt, hg = (wg / n_qt) % n_hg, sg = wg / (n_qt * n_hg);
     const int len = seg_len[sg];
     constexpr int NT = 64 * NW, QT = 32 * NW;  // threads, queries per workgroup
     if (qt * QT >= len) return;  // whole workgroup past the segment
     const int64_t row0 = seg_start[sg];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, lh = lane >> 5;
-    const int64_t head_qk = ((int64_t)sg * n_head + h) * len_pad * FA_DP;
-    const int64_t head_vt = ((int64_t)sg * n_head + h) * FA_DV * len_pad;
-    const _Float16 *Kh = K + head_qk;
-    const _Float16 *Vh = Vt + head_vt;
-
     // Q^T fragments (B operand): lane holds query q, d = 16 t + 8 lh + s
     const int q = qt * QT + wave * 32 + lr;
     const bool active = __builtin_amdgcn_readfirstlane(qt * QT + wave * 32) < len;
     // (a workgroup's last queries may lie past len_pad, a multiple of 128:
     // they read row len_pad - 1 and are never stored)
     const int qrow = min(q, len_pad - 1);
-    v8h qf[5];
-#pragma unroll
-    for (int t = 0; t < 5; ++t)
-        qf[t] = *reinterpret_cast<const v8h *>(Q + head_qk + (int64_t)qrow * FA_DP + 16 * t + 8 * lh);
 
-    v16f o[3];
+    // (every head ends with its last tile's barrier: the next head's first
+    // LDS store cannot overtake a read of this one's)
+    for (int hr = 0; hr < HPW; ++hr) {
+        const int h = hg * HPW + hr;
+        const int64_t head_qk = ((int64_t)sg * n_head + h) * len_pad * FA_DP;
+        const int64_t head_vt = ((int64_t)sg * n_head + h) * FA_DV * len_pad;
+        const _Float16 *Kh = K + head_qk;
+        const _Float16 *Vh = Vt + head_vt;
+        v8h qf[5];
 #pragma unroll
-    for (int j = 0; j < 3; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
-    float m_run = -INFINITY, mc_run = -INFINITY;
+        for (int t = 0; t < 5; ++t)
+            qf[t] = *reinterpret_cast<const v8h *>(Q + head_qk + (int64_t)qrow * FA_DP + 16 * t + 8 * lh);
 
-    const int n_tiles = (len + FA_KT - 1) / FA_KT;
-
-    // global -> registers for one key tile: K 64x80 halves (10240 B contiguous,
-    // 640 chunks of 16 B), V^T 96 rows x 64 halves (128 B each, 768 chunks)
-    constexpr int K_CH = FA_KT * FA_DP / 8, V_CH = FA_DV * FA_KT / 8;
-    constexpr int KC = (K_CH + NT - 1) / NT, VC = (V_CH + NT - 1) / NT;
-    struct Tile {
-        uint4 k[KC], v[VC];
-    };
-    // threads past the last K chunk re-load it (always in bounds) and later
-    // rewrite it with the value it already has
-    int kc[KC];
-#pragma unroll
-    for (int i = 0; i < KC; ++i) kc[i] = min(tid + i * NT, K_CH - 1);
-    // One code path for every tile (the edge masking happens at the LDS
-    // store): the next tile's loads stay in flight through the current
-    // tile's MFMAs, with no merge of differently loaded registers that would
-    // make the compiler wait for them right after issue.
-    auto gload = [&](int t) {
-        const int k0 = t * FA_KT;
-        const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
-        Tile g;
-#pragma unroll
-        for (int i = 0; i < KC; ++i) g.k[i] = ks[kc[i]];
-#pragma unroll
-        for (int i = 0; i < VC; ++i) {
-            const int c = tid + i * NT;  // V chunk c: row c/8, col (c%8)*8 halves
-            if (V_CH % NT == 0 || c < V_CH)
-                g.v[i] = *reinterpret_cast<const uint4 *>(Vh + (int64_t)(c >> 3) * len_pad + k0 +
-                                                          (c & 7) * 8);
-        }
-        return g;
-    };
-    auto sstore = [&](int buf, int t, const Tile &g) {
-        _Float16 *kl = lds + buf * FA_STAGE;
-        _Float16 *vl = kl + FA_KT * FA_KP;
-        const auto kput = [&](int c, uint4 v) {
-            *reinterpret_cast<uint4 *>(kl + (c / 10) * FA_KP + (c % 10) * 8) = v;
-        };
-#pragma unroll
-        for (int i = 0; i < KC; ++i) kput(kc[i], g.k[i]);
-        // V^T rows keep each 16-key group in the order [0-3, 8-11, 4-7,
-        // 12-15]: the 8 keys a lane feeds to one PV MFMA (4 lh + 0..3 and
-        // 8 + 4 lh + 0..3, the S^T result layout) are then one 16-byte read
-        const auto vput = [&](int i, uint4 v) {
-            const int c = tid + i * NT;
-            const int row = c >> 3, ch = c & 7;
-            // keys past the segment hold zeros or stale finite data; zero
-            // them so a stale NaN/Inf can never meet a zero probability
-            // (only the tile holding the segment end has such keys)
-            const int valid = len - (t * FA_KT + ch * 8);
-            if (valid < 8) {
-                const auto keep = [valid](int j) {
-                    return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
-                };
-                v = make_uint4(v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3));
-            }
-            if (row == FA_ONES) v = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
-            _Float16 *base = vl + row * FA_VP + (ch >> 1) * 16 + (ch & 1) * 4;
-            *reinterpret_cast<uint2 *>(base) = make_uint2(v.x, v.y);
-            *reinterpret_cast<uint2 *>(base + 8) = make_uint2(v.z, v.w);
-        };
-#pragma unroll
-        for (int i = 0; i < VC; ++i)
-            if (V_CH % NT == 0 || tid + i * NT < V_CH) vput(i, g.v[i]);
-    };
-
-    const int n_plain = key_valid ? 0 : len / FA_KT;  // whole tiles without a key mask
-    sstore(0, 0, gload(0));
-    __syncthreads();
-
-    // one 64-key tile; MASK: the tile holding the segment end, or a key mask
-    auto tile = [&](int t, auto maskc) {
-        constexpr bool MASK = decltype(maskc)::value;
-        const int buf = t & 1;
-        // (past the last tile: the last tile again, never stored)
-        const Tile nxt = gload(min(t + 1, n_tiles - 1));
-        const _Float16 *kl = lds + buf * FA_STAGE;
-        const _Float16 *vl = kl + FA_KT * FA_KP;
-        // a wave whose 32 queries all lie past the segment end only stages
-        // tiles for the others
-        if (active) {
-        // S^T for the tile's two 32-key halves (raw q.k, unscaled)
-        // (both halves' K fragments read up front, then the two
-        // independent MFMA chains interleaved)
-        v16f sc[2] = {};
-        v8h kf[2][5];
-#pragma unroll
-        for (int st = 0; st < 5; ++st)
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
-                kf[sub][st] = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
-#pragma unroll
-        for (int st = 0; st < 5; ++st)
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
-                sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sub][st], qf[st], sc[sub], 0, 0, 0);
-        // mask (only the tile holding the segment end, or a key mask), then
-        // the tile max; one softmax rescale per 64 keys
-        const int kbase = t * FA_KT;
-        if constexpr (MASK) {
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kbase + sub * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    bool ok = key < len;
-                    if (key_valid) ok = ok && key_valid[row0 + min(key, len - 1)] != 0;
-                    sc[sub][r] = ok ? sc[sub][r] : -INFINITY;
-                }
-        }
-        float mt = -INFINITY;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[sub][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        // P = 2^(s scale_log2 - mc) with mc = m scale_log2 - P_SHIFT: the
-        // largest P of a row is 2^P_SHIFT, not 1, so that the f16 pair below
-        // keeps ~22 significant bits for P down to 2^-13 of the row maximum
-        // (unshifted, the lo half turns f16-subnormal below 2^-4 and its
-        // truncation biases every small P downward).  O and its P sum carry
-        // the same factor, which cancels in O / sum.  alpha compares the two
-        // exponent offsets actually used, so no rounding of mc enters it.
-        const float m_new = fmaxf(m_run, mt);  // in raw score units (scale > 0)
-        const float mc = m_new == -INFINITY ? 0.0f : fmaf(m_new, scale_log2, -P_SHIFT);
-        const float alpha = __builtin_amdgcn_exp2f(mc_run - mc);  // 0 before the first key
-        m_run = m_new;
-        mc_run = m_new == -INFINITY ? -INFINITY : mc;
-        // alpha is exactly 1 where the running max did not move: skip the
-        // rescale when that holds for the whole wave (the common case once
-        // the first tiles have set the max)
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
-        }
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            // P as f16 for the PV product; with P_SPLIT as a pair p ~ hi + lo
-            // (hi = f16(p) rounded toward zero, lo = f16(p - hi) with p - hi
-            // exact in f32): ~22 significant bits instead of 11.  Pairs of
-            // values convert in one v_cvt_pkrtz_f16_f32, whose packed words
-            // are the MFMA operand registers as they stand.
-            float pv[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
-            uint32_t hw[8], lw[8];
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[r], pv[r + 1]);
-                hw[r / 2] = __builtin_bit_cast(uint32_t, h2);
-                if (P_SPLIT) {
-                    // p - hi in one v_fma_mix_f32 each (hi read as f16 from its
-                    // half of the packed word, -1.0 as f32, p as f32): exact
-                    float l0, l1;
-                    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]"
-                        : "=v"(l0) : "v"(hw[r / 2]), "v"(pv[r]));
-                    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                        : "=v"(l1) : "v"(hw[r / 2]), "v"(pv[r + 1]));
-                    lw[r / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
-                }
-            }
-            const v8h ph0 = __builtin_bit_cast(v8h, v4u{hw[0], hw[1], hw[2], hw[3]});
-            const v8h ph1 = __builtin_bit_cast(v8h, v4u{hw[4], hw[5], hw[6], hw[7]});
-            v8h pl0 = {}, pl1 = {};
-            if (P_SPLIT) {
-                pl0 = __builtin_bit_cast(v8h, v4u{lw[0], lw[1], lw[2], lw[3]});
-                pl1 = __builtin_bit_cast(v8h, v4u{lw[4], lw[5], lw[6], lw[7]});
-            }
-            // O^T += V^T P^T (row FA_ONES of V^T is 1: O^T row FA_ONES sums P).
-            // Each o[j] takes its products in the order hh 0 (hi, lo), hh 1
-            // (hi, lo); consecutive MFMAs go to different j (independent).
-            v8h vf[3][2];
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-                    vf[j][hh] = *reinterpret_cast<const v8h *>(vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 8 * lh);
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-                for (int j = 0; j < 3; ++j)
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? ph1 : ph0, o[j], 0, 0, 0);
-                if (P_SPLIT) {
-#pragma unroll
-                    for (int j = 0; j < 3; ++j)
-                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? pl1 : pl0, o[j], 0, 0, 0);
-                }
-            }
-        }
-        }
-        if (t + 1 < n_tiles) sstore(buf ^ 1, t + 1, nxt);
-        __syncthreads();
-    };
-    // whole tiles without a key mask take the unmasked instance
-    for (int t = 0; t < n_plain; ++t) tile(t, std::false_type{});
-    for (int t = n_plain; t < n_tiles; ++t) tile(t, std::true_type{});
-
-    // sum of P: O^T row FA_ONES = 64 + 24 (register 12 of lanes 0..31)
-    static_assert(FA_ONES == 2 * 32 + 8 * 3 && FA_ONES >= FA_DP && FA_ONES < FA_DV, "ones row");
-    const float l_tot = __shfl(o[2][12], lr);
-    const float inv = 1.0f / l_tot;
-    if (QUANT) {
-        // (d_head 72, heads in groups of four: checked by the launcher)
-        if (q < len) {
-            const int64_t row = row0 + q;
-            float *orow = out + row * ld_out + h * d_head;
-            int8_t *qrow = qo.qs + row * ld_q + h * d_head;
-            uint32_t *dsrow = qo.ds + row * qo.ld_ds;
-            const int kb0 = 9 * (h >> 2);
-            switch (h & 3) {
-            case 0: attn_q81_row<0>(o, inv, lh, orow, qrow, dsrow, kb0); break;
-            case 1: attn_q81_row<1>(o, inv, lh, orow, qrow, dsrow, kb0); break;
-            case 2: attn_q81_row<2>(o, inv, lh, orow, qrow, dsrow, kb0); break;
-            default: attn_q81_row<3>(o, inv, lh, orow, qrow, dsrow, kb0); break;
-            }
-        }
-    } else if (q < len) {
-        float *orow = out + (row0 + q) * ld_out + h * d_head;
+        v16f o[3];
 #pragma unroll
         for (int j = 0; j < 3; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = j * 32 + 8 * g + 4 * lh;
-                if (d < d_head) {
-                    const float4 v = make_float4(o[j][4 * g] * inv, o[j][4 * g + 1] * inv,
-                                                 o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv);
-                    *reinterpret_cast<float4 *>(orow + d) = v;
+            for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
+        float m_run = -INFINITY, mc_run = -INFINITY;
+
+        const int n_tiles = (len + FA_KT - 1) / FA_KT;
+
+        // global -> registers for one key tile: K 64x80 halves (10240 B contiguous,
+        // 640 chunks of 16 B), V^T 96 rows x 64 halves (128 B each, 768 chunks)
+        constexpr int K_CH = FA_KT * FA_DP / 8, V_CH = FA_DV * FA_KT / 8;
+        constexpr int KC = (K_CH + NT - 1) / NT, VC = (V_CH + NT - 1) / NT;
+        struct Tile {
+            uint4 k[KC], v[VC];
+        };
+        // threads past the last K chunk re-load it (always in bounds) and later
+        // rewrite it with the value it already has
+        int kc[KC];
+#pragma unroll
+        for (int i = 0; i < KC; ++i) kc[i] = min(tid + i * NT, K_CH - 1);
+        // One code path for every tile (the edge masking happens at the LDS
+        // store): the next tile's loads stay in flight through the current
+        // tile's MFMAs, with no merge of differently loaded registers that would
+        // make the compiler wait for them right after issue.
+        auto gload = [&](int t) {
+            const int k0 = t * FA_KT;
+            const uint4 *ks = reinterpret_cast<const uint4 *>(Kh + (int64_t)k0 * FA_DP);
+            Tile g;
+#pragma unroll
+            for (int i = 0; i < KC; ++i) g.k[i] = ks[kc[i]];
+#pragma unroll
+            for (int i = 0; i < VC; ++i) {
+                const int c = tid + i * NT;  // V chunk c: row c/8, col (c%8)*8 halves
+                if (V_CH % NT == 0 || c < V_CH)
+                    g.v[i] = *reinterpret_cast<const uint4 *>(Vh + (int64_t)(c >> 3) * len_pad + k0 +
+                                                              (c & 7) * 8);
+            }
+            return g;
+        };
+        auto sstore = [&](int buf, int t, const Tile &g) {
+            _Float16 *kl = lds + buf * FA_STAGE;
+            _Float16 *vl = kl + FA_KT * FA_KP;
+            const auto kput = [&](int c, uint4 v) {
+                *reinterpret_cast<uint4 *>(kl + (c / 10) * FA_KP + (c % 10) * 8) = v;
+            };
+#pragma unroll
+            for (int i = 0; i < KC; ++i) kput(kc[i], g.k[i]);
+            // V^T rows keep each 16-key group in the order [0-3, 8-11, 4-7,
+            // 12-15]: the 8 keys a lane feeds to one PV MFMA (4 lh + 0..3 and
+            // 8 + 4 lh + 0..3, the S^T result layout) are then one 16-byte read
+            const auto vput = [&](int i, uint4 v) {
+                const int c = tid + i * NT;
+                const int row = c >> 3, ch = c & 7;
+                // keys past the segment hold zeros or stale finite data; zero
+                // them so a stale NaN/Inf can never meet a zero probability
+                // (only the tile holding the segment end has such keys)
+                const int valid = len - (t * FA_KT + ch * 8);
+                if (valid < 8) {
+                    const auto keep = [valid](int j) {
+                        return (valid > 2 * j ? 0xffffu : 0u) | (valid > 2 * j + 1 ? 0xffff0000u : 0u);
+                    };
+                    v = make_uint4(v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3));
+                }
+                if (row == FA_ONES) v = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+                _Float16 *base = vl + row * FA_VP + (ch >> 1) * 16 + (ch & 1) * 4;
+                *reinterpret_cast<uint2 *>(base) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2 *>(base + 8) = make_uint2(v.z, v.w);
+            };
+#pragma unroll
+            for (int i = 0; i < VC; ++i)
+                if (V_CH % NT == 0 || tid + i * NT < V_CH) vput(i, g.v[i]);
+        };
+
+        const int n_plain = key_valid ? 0 : len / FA_KT;  // whole tiles without a key mask
+        sstore(0, 0, gload(0));
+        __syncthreads();
+
+        // one 64-key tile; MASK: the tile holding the segment end, or a key mask
+        auto tile = [&](int t, auto maskc) {
+            constexpr bool MASK = decltype(maskc)::value;
+            const int buf = t & 1;
+            // (past the last tile: the last tile again, never stored)
+            const Tile nxt = gload(min(t + 1, n_tiles - 1));
+            const _Float16 *kl = lds + buf * FA_STAGE;
+            const _Float16 *vl = kl + FA_KT * FA_KP;
+            // a wave whose 32 queries all lie past the segment end only stages
+            // tiles for the others
+            if (active) {
+            // S^T for the tile's two 32-key halves (raw q.k, unscaled)
+            // (both halves' K fragments read up front, then the two
+            // independent MFMA chains interleaved)
+            v16f sc[2] = {};
+            v8h kf[2][5];
+#pragma unroll
+            for (int st = 0; st < 5; ++st)
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub)
+                    kf[sub][st] = *reinterpret_cast<const v8h *>(kl + (sub * 32 + lr) * FA_KP + 16 * st + 8 * lh);
+#pragma unroll
+            for (int st = 0; st < 5; ++st)
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub)
+                    sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sub][st], qf[st], sc[sub], 0, 0, 0);
+            // mask (only the tile holding the segment end, or a key mask), then
+            // the tile max; one softmax rescale per 64 keys
+            const int kbase = t * FA_KT;
+            if constexpr (MASK) {
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kbase + sub * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        bool ok = key < len;
+                        if (key_valid) ok = ok && key_valid[row0 + min(key, len - 1)] != 0;
+                        sc[sub][r] = ok ? sc[sub][r] : -INFINITY;
+                    }
+            }
+            float mt = -INFINITY;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[sub][r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            // P = 2^(s scale_log2 - mc) with mc = m scale_log2 - P_SHIFT: the
+            // largest P of a row is 2^P_SHIFT, not 1, so that the f16 pair below
+            // keeps ~22 significant bits for P down to 2^-13 of the row maximum
+            // (unshifted, the lo half turns f16-subnormal below 2^-4 and its
+            // truncation biases every small P downward).  O and its P sum carry
+            // the same factor, which cancels in O / sum.  alpha compares the two
+            // exponent offsets actually used, so no rounding of mc enters it.
+            const float m_new = fmaxf(m_run, mt);  // in raw score units (scale > 0)
+            const float mc = m_new == -INFINITY ? 0.0f : fmaf(m_new, scale_log2, -P_SHIFT);
+            const float alpha = __builtin_amdgcn_exp2f(mc_run - mc);  // 0 before the first key
+            m_run = m_new;
+            mc_run = m_new == -INFINITY ? -INFINITY : mc;
+            // alpha is exactly 1 where the running max did not move: skip the
+            // rescale when that holds for the whole wave (the common case once
+            // the first tiles have set the max)
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[j][r] = o[j][r] * alpha;
+            }
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                // P as f16 for the PV product; with P_SPLIT as a pair p ~ hi + lo
+                // (hi = f16(p) rounded toward zero, lo = f16(p - hi) with p - hi
+                // exact in f32): ~22 significant bits instead of 11.  Pairs of
+                // values convert in one v_cvt_pkrtz_f16_f32, whose packed words
+                // are the MFMA operand registers as they stand.
+                float pv[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(sc[sub][r], scale_log2, -mc));
+                uint32_t hw[8], lw[8];
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[r], pv[r + 1]);
+                    hw[r / 2] = __builtin_bit_cast(uint32_t, h2);
+                    if (P_SPLIT) {
+                        // p - hi in one v_fma_mix_f32 each (hi read as f16 from its
+                        // half of the packed word, -1.0 as f32, p as f32): exact
+                        float l0, l1;
+                        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]"
+                            : "=v"(l0) : "v"(hw[r / 2]), "v"(pv[r]));
+                        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                            : "=v"(l1) : "v"(hw[r / 2]), "v"(pv[r + 1]));
+                        lw[r / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
+                    }
+                }
+                const v8h ph0 = __builtin_bit_cast(v8h, v4u{hw[0], hw[1], hw[2], hw[3]});
+                const v8h ph1 = __builtin_bit_cast(v8h, v4u{hw[4], hw[5], hw[6], hw[7]});
+                v8h pl0 = {}, pl1 = {};
+                if (P_SPLIT) {
+                    pl0 = __builtin_bit_cast(v8h, v4u{lw[0], lw[1], lw[2], lw[3]});
+                    pl1 = __builtin_bit_cast(v8h, v4u{lw[4], lw[5], lw[6], lw[7]});
+                }
+                // O^T += V^T P^T (row FA_ONES of V^T is 1: O^T row FA_ONES sums P).
+                // Each o[j] takes its products in the order hh 0 (hi, lo), hh 1
+                // (hi, lo); consecutive MFMAs go to different j (independent).
+                v8h vf[3][2];
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        vf[j][hh] = *reinterpret_cast<const v8h *>(vl + (j * 32 + lr) * FA_VP + sub * 32 + 16 * hh + 8 * lh);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? ph1 : ph0, o[j], 0, 0, 0);
+                    if (P_SPLIT) {
+#pragma unroll
+                        for (int j = 0; j < 3; ++j)
+                            o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[j][hh], hh ? pl1 : pl0, o[j], 0, 0, 0);
+                    }
                 }
             }
+            }
+            if (t + 1 < n_tiles) sstore(buf ^ 1, t + 1, nxt);
+            __syncthreads();
+        };
+        // whole tiles without a key mask take the unmasked instance
+        for (int t = 0; t < n_plain; ++t) tile(t, std::false_type{});
+        for (int t = n_plain; t < n_tiles; ++t) tile(t, std::true_type{});
+
+        // sum of P: O^T row FA_ONES = 64 + 24 (register 12 of lanes 0..31)
+        static_assert(FA_ONES == 2 * 32 + 8 * 3 && FA_ONES >= FA_DP && FA_ONES < FA_DV, "ones row");
+        const float l_tot = __shfl(o[2][12], lr);
+        const float inv = 1.0f / l_tot;
+        if (QUANT) {
+            // (d_head 72, heads in groups of four: checked by the launcher)
+            if (q < len) {
+                const int64_t row = row0 + q;
+                float *orow = out + row * ld_out + h * d_head;
+                int8_t *qrow = qo.qs + row * ld_q + h * d_head;
+                uint32_t *dsrow = qo.ds + row * qo.ld_ds;
+                const int kb0 = 9 * (h >> 2);
+                if constexpr (G4) {
+                    int8_t *qg = qrow - 72 * hr;  // the group's first column
+                    uint32_t *dsg = dsrow + kb0;
+                    float *st = stash + wave * 64 * 12 + lane;
+                    switch (hr) {
+                    case 0: attn_q81_group_row<0>(o, inv, lh, qg, dsg, st); break;
+                    case 1: attn_q81_group_row<1>(o, inv, lh, qg, dsg, st); break;
+                    case 2: attn_q81_group_row<2>(o, inv, lh, qg, dsg, st); break;
+                    default: attn_q81_group_row<3>(o, inv, lh, qg, dsg, st); break;
+                    }
+                } else {
+                    switch (h & 3) {
+                    case 0: attn_q81_row<0>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+                    case 1: attn_q81_row<1>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+                    case 2: attn_q81_row<2>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+                    default: attn_q81_row<3>(o, inv, lh, orow, qrow, dsrow, kb0); break;
+                    }
+                }
+            }
+        } else if (q < len) {
+            float *orow = out + (row0 + q) * ld_out + h * d_head;
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = j * 32 + 8 * g + 4 * lh;
+                    if (d < d_head) {
+                        const float4 v = make_float4(o[j][4 * g] * inv, o[j][4 * g + 1] * inv,
+                                                     o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv);
+                        *reinterpret_cast<float4 *>(orow + d) = v;
+                    }
+                }
+        }
     }
 }
 
@@ -563,14 +643,20 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
     int NW = FA_WAVES;
     if (((L.max_len + 32 * NW - 1) / (32 * NW)) * L.n_head * L.n_seg < 256) NW = FA_WAVES_SMALL;
     const int64_t n_qt = (L.max_len + 32 * NW - 1) / (32 * NW);
-    const int64_t n_wg = n_qt * L.n_head * L.n_seg;
+    const bool qz = qo != nullptr;
+    // with the Q8_1 output, 12-wave workgroups that each run a group of four
+    // heads where those still number 256 or more (batch 32: 256, one per CU,
+    // the same waves per CU as 1,024 one-head workgroups): no second pass
+    const bool g4 = qz && NW == FA_WAVES && n_qt * (L.n_head / 4) * L.n_seg >= 256;
+    const int64_t n_wg = n_qt * (g4 ? L.n_head / 4 : L.n_head) * L.n_seg;
     if (n_wg > 0x7fffffff) return hipErrorInvalidValue;
     using KFn = void (*)(const _Float16 *, const _Float16 *, const _Float16 *, const int32_t *,
                          const int32_t *, const uint8_t *, int, int, int, int, float, float *,
                          int64_t, Q81Out, int64_t);
     KFn kern;
-    const bool qz = qo != nullptr;
-    if (NW == FA_WAVES)
+    if (g4)
+        kern = L.p_split ? k_attn<true, FA_WAVES, true, true> : k_attn<false, FA_WAVES, true, true>;
+    else if (NW == FA_WAVES)
         kern = L.p_split ? (qz ? k_attn<true, FA_WAVES, true> : k_attn<true, FA_WAVES, false>)
                          : (qz ? k_attn<false, FA_WAVES, true> : k_attn<false, FA_WAVES, false>);
     else
@@ -584,7 +670,7 @@ hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *
                        key_valid, (int)L.n_head, (int)L.d_head, (int)L.len_pad, (int)n_qt,
                        scale * log2e, out, ld_out, qz ? *qo : q_none, H);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !qz) return e;
+    if (e != hipSuccess || !qz || g4) return e;
     // the blocks that straddle two heads, from the f32 columns just written
     // (rows of the packed segments: 0 .. n_rows - 1, every row a segment's)
     const int64_t groups = n_rows * 3 * (L.n_head / 4);

@@ -144,7 +144,7 @@ hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64
 // EPI_QKV destination planes of layout L in workspace ws.
 EpiParams epi_qkv(const AttnLayout &L, void *ws, const float *qkv_bias, const int32_t *rowmap);
 // With qo: the output's Q8_1 (K = n_head * d_head) instead of the whole f32
-// output -- only the columns of Q8_1 blocks that straddle two heads are
+// output -- at most the columns of Q8_1 blocks that straddle two heads are
 // written to `out` -- over the packed rows 0 .. n_rows - 1 (every row a
 // segment's); needs attn_q81_fusable.
 hipError_t launch_attn(const void *ws, const int32_t *seg_start, const int32_t *seg_len,

@@ -258,8 +258,8 @@ int s2x_attn_run(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
  * out-projection (siglip2_vision.cpp:148 launch_fused_post_fa_cont,
  * siglip2_custom_mmq.cuh:63 launch_quantize_activation).  qs [n_rows][H]
  * int8, ds [n_rows][ld_ds] words as s2x_quantize_q8_1 writes them, the same
- * bits.  `out` (f32 [n_rows][ld_out], 16-byte aligned) is scratch: only the
- * columns of Q8_1 blocks that straddle two heads are written.  The segments
+ * bits.  `out` (f32 [n_rows][ld_out], 16-byte aligned) is scratch: at most
+ * the columns of Q8_1 blocks that straddle two heads are written.  The segments
  * must cover rows 0 .. n_rows - 1. */
 int s2x_attn_run_q8_1(const void *ws, size_t ws_bytes, const int32_t *seg_start_dev,
                       const int32_t *seg_len_dev, const uint8_t *key_valid,

@@ -420,16 +420,20 @@ def test_attention_key_mask(orc):
     assert _attn_case(orc, lens, key_valid=kv, seed=11) < 1e-5
 
 
-@pytest.mark.parametrize("case", ["ragged", "masked", "batch32", "one"])
+@pytest.mark.parametrize("case", ["ragged", "masked", "batch32", "one", "ragged40", "masked36"])
 def test_attention_q8_1_equals_attention_then_quantize(case):
-    """s2x_attn_run_q8_1 (Q8_1 of whole blocks in the attention epilogue,
-    the blocks that straddle two heads in a second pass) gives exactly the
+    """s2x_attn_run_q8_1 (Q8_1 of whole blocks in the attention epilogue;
+    the blocks that straddle two heads in a second pass, or, from 256
+    four-head workgroups up -- batch32, ragged40, masked36 -- by the
+    workgroup that runs the group's four heads in turn) gives exactly the
     bytes of s2x_attn_run followed by s2x_quantize_q8_1."""
     n_head, dh = 16, 72
     H = n_head * dh
-    lens = {"ragged": [729, 1, 64, 130, 255, 128, 33], "masked": [64, 200],
-            "batch32": [729] * 32, "one": [729]}[case]
     rng = np.random.default_rng(17)
+    ragged40 = [int(x) for x in rng.choice([1, 33, 64, 130, 255, 384, 385, 500, 729], 39)] + [729]
+    lens = {"ragged": [729, 1, 64, 130, 255, 128, 33], "masked": [64, 200],
+            "batch32": [729] * 32, "one": [729], "ragged40": ragged40,
+            "masked36": [729] * 36}[case]
     M = int(sum(lens))
     qkv = (rng.standard_normal((M, 3 * H)) * 1.5).astype(np.float32)
     bias = rng.normal(0, 0.5, 3 * H).astype(np.float32)
@@ -441,6 +445,9 @@ def test_attention_q8_1_equals_attention_then_quantize(case):
         kv = np.ones(M, np.uint8)
         kv[40:64] = 0
         kv[64 + 150:] = 0
+    if case == "masked36":  # a tenth of the keys masked, each segment's first kept
+        kv = (rng.random(M) >= 0.1).astype(np.uint8)
+        kv[starts] = 1
     say(f"attention + Q8_1: {case}, M={M}")
     wsb = s2x.lib.s2x_attn_workspace_size(len(lens), max_len, n_head, dh)
     ws = zeros((wsb,), torch.uint8)
