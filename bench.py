@@ -12,7 +12,8 @@ counted) over the GEMM launch durations measured with HIP events on the
 encoder's stream during the timed steps, against MI355X's dense int8 peak.
 The same line carries the other workloads of the path as extra keys:
 `batch1` (one 729-patch image per encode: latency and the GEMM rate at
-M = 729), `gemm_shapes` (the four vision-layer GEMMs alone at M = 729 and
+M = 729), `dp8_share` (4 images per encode, M = 2,916: one GPU's share of
+batch 32 data-parallel over 8 GPUs), `gemm_shapes` (the four vision-layer GEMMs alone at M = 729 and
 M = 23,328: quantize + GEMM per iteration, p50 of HIP-event times) and
 `text_5x64` (the text tower, 5 prompts x 64 tokens).  `cpu_baseline` times
 the CPU oracle (this repository's C restatement of ggml's CPU Q8_0 path) on
@@ -191,6 +192,8 @@ def main():
     extra = {}
     if not args.no_extra:
         extra["batch1"] = bench_batch1(step, sync, gemm_stats, v, s2x, np)
+        if B >= 4:
+            extra["dp8_share"] = bench_share(step, sync, gemm_stats, v, s2x)
         s2x.lib.s2x_vision_destroy(v)
         extra["gemm_shapes"] = bench_gemm_shapes(np, torch, s2x, synth)
         extra["text_5x64"] = bench_text(np, s2x, synth)
@@ -228,6 +231,40 @@ def main():
     }
     rec.update(extra)
     print(json.dumps(rec), flush=True)
+
+
+def bench_share(step, sync, gemm_stats, v, s2x, n_img=4, iters=40):
+    """One GPU's share of a data-parallel batch of 32 over 8 GPUs: 4 images
+    of 27x27 per encode (M = 2,916), pixels resident in HBM; wall time of
+    each synchronised encode and the GEMM rate at that M."""
+    def run():
+        step(n_img)
+        sync()
+    for _ in range(5):
+        run()
+    lat = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        run()
+        lat.append((time.perf_counter() - t0) * 1000.0)
+    gemm_stats()
+    s2x.call("s2x_vision_gemm_timing", v, 1)
+    n_rate = 10
+    for _ in range(n_rate):
+        step(n_img)
+    sync()
+    g_ms, g_ops, _ = gemm_stats()
+    s2x.call("s2x_vision_gemm_timing", v, 0)
+    tops = g_ops / (g_ms / 1000.0) / 1e12
+    p50 = pct(lat, 0.5)
+    log(f"bench: {n_img} images (M = {n_img * 729}): p50 {p50:.3f} ms, "
+        f"{n_img * 1000.0 / p50:.1f} images/s, GEMM {tops:.1f} TOPS")
+    return {"workload": f"SigLIP2-so400m vision tower, {n_img} images x 729 patches, probe "
+                        "pooling: one GPU's share of batch 32 over 8 GPUs",
+            "rows": n_img * 729, "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
+            "images_per_s": round(n_img * 1000.0 / p50, 1), "iters": iters,
+            "gemm_tops": round(tops, 1), "gemm_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "gemm_ms_per_encode": round(g_ms / n_rate, 3)}
 
 
 def bench_batch1(step, sync, gemm_stats, v, s2x, np, iters=60):
