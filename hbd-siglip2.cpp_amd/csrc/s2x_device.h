@@ -122,12 +122,33 @@ __device__ __forceinline__ int group_isum(int v) {
 
 // The Q8_1 rule for one 32-value block given its amax:
 //   d = amax/127, inv = amax ? 127/amax : 0, q = rint_half_even(x*inv)
-// clamped to [-128, 127] (src/cuda/siglip2_custom_mmq.cu:63-76).
+// clamped to [-128, 127] (src/cuda/siglip2_custom_mmq.cu:63-76), the
+// conversion saturating (+inf -> 127, -inf -> -128, NaN -> 0) as
+// __float2int_rn does: the case of a block whose 127 / amax overflows
+// (amax < 127 / FLT_MAX) or whose amax is NaN.
 __device__ __forceinline__ int q8_round(float x, float inv) {
     int q = (int)__builtin_rintf(x * inv);
     q = q > 127 ? 127 : q;
     q = q < -128 ? -128 : q;
     return q;
+}
+// The same for a finite inv, in two VALU operations instead of four.  With
+// |x| <= amax the product is at most 127 (1 + 2^-23) in magnitude, so the
+// clamp never acts, and rint is the rounding of p + 1.5 * 2^23: floats in
+// [2^23, 2^24) are the integers, the add rounds to nearest with ties to
+// even as rint does, and leaves 0x4B400000 + rint(p) as the bits (|p| <
+// 2^22); the offset, a multiple of 256, drops out of the int8 bytes and of
+// integer sums of q.  For the fc1 epilogue, where 16 values of a lane
+// share one block's inv: a wave with a non-finite inv in any lane
+// (q8_any_sat) takes q8_round instead, a branch the others skip (where
+// fewer values share the check -- LayerNorm, the quantizer, attention --
+// the branch measured slower than the two operations it saves).
+__device__ __forceinline__ int q8_round_fast(float x, float inv) {
+    const float p = x * inv;  // rounded to f32 first (no contraction)
+    return (int)(__builtin_bit_cast(uint32_t, p + 12582912.0f) - 0x4B400000u);
+}
+__device__ __forceinline__ bool q8_any_sat(float inv) {
+    return __builtin_amdgcn_ballot_w64(!(inv <= 3.40282347e38f)) != 0;
 }
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {

@@ -185,11 +185,15 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                 const float d = am / 127.0f;
                 const float inv = am != 0.0f ? 127.0f / am : 0.0f;
                 int qi[16], qs = 0;
+                if (q8_any_sat(inv)) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    qi[j] = q8_round(v[j], inv);
-                    qs += qi[j];
+                    for (int j = 0; j < 16; ++j) qi[j] = q8_round(v[j], inv);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) qi[j] = q8_round_fast(v[j], inv);
                 }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) qs += qi[j];
                 qs += dpp_i<0xb1>(qs);
                 const int m = mw + a * 32 + row;
                 if (m < M) {

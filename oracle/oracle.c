@@ -159,9 +159,12 @@ void orc_quantize_q8_1(const float *x, int64_t M, int64_t K, int64_t ldx,
             int sum = 0;
             int8_t *q = qs + m * K_pad + b * ORC_QK;
             for (int j = 0; j < ORC_QK; ++j) {
-                int iq = (int)nearbyintf(v[j] * inv); /* default mode: half-even */
-                if (iq > 127) iq = 127;
-                if (iq < -128) iq = -128;
+                /* default mode: half-even; the conversion saturates as the
+                 * reference's __float2int_rn (+inf -> 127, -inf -> -128,
+                 * NaN -> 0): a block whose 127 / amax overflows (amax <
+                 * 127 / FLT_MAX) forms +-inf products and 0 * inf */
+                const float r = nearbyintf(v[j] * inv);
+                const int iq = r != r ? 0 : r >= 127.0f ? 127 : r <= -128.0f ? -128 : (int)r;
                 q[j] = (int8_t)iq;
                 sum += iq;
             }

@@ -88,6 +88,13 @@ def test_batch32_rows_match_oracle(orc, weights, label):
 @pytest.mark.parametrize("M", [729, 32 * 729])
 def test_gelu_q81_epilogue(orc, weights, M):
     raw, N, K, K_pad, bias = weights["fc1"]
+    # output columns 64..95 (one Q8_1 block): zero weights and bias -10, so
+    # every row's block is GELU(-10) ~ -1.2e-37, below 127 / FLT_MAX: its
+    # 127 / amax overflows and the quants saturate (-128), as the
+    # reference's __float2int_rn does
+    raw, bias = raw.copy(), bias.copy()
+    raw[64:96] = 0
+    bias[64:96] = -10.0
     say(f"fc1 GELU->Q8_1 epilogue M={M}")
     x = np.random.default_rng(33).standard_normal((M, K)).astype(np.float32)
     qs, ds = _quant_gpu(x, K_pad)
@@ -111,6 +118,7 @@ def test_gelu_q81_epilogue(orc, weights, M):
         assert_same(gq, host(q2), "GELU_Q81 quants vs quantize(BIAS_GELU)")
         assert_same(gd, host(d2).view(np.uint16), "GELU_Q81 scales vs quantize(BIAS_GELU)")
         assert not gq[:, N:].any()  # columns N..q_kpad-1 quantize zeros
+        assert (gq[:, 64:96] == -128).all()  # the saturated block
     finally:
         s2x.lib.s2x_weight_destroy(w)
     rows = np.arange(M) if M <= 729 else _rows(M, 48, 34)

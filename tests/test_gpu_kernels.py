@@ -39,6 +39,11 @@ def test_quantize_q8_1_bit_exact(orc, M, K, K_pad):
     if K >= 64:
         x[min(1, M - 1), :32] = np.float32(127.0)
         x[min(1, M - 1), 1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5]
+    if K >= 96:
+        # a block whose 127 / amax overflows (amax < 127 / FLT_MAX): the
+        # saturating conversion (+inf -> 127, -inf -> -128, 0 * inf -> 0)
+        x[min(2, M - 1), 64:96] = 0.0
+        x[min(2, M - 1), 64:68] = [1e-38, -1e-38, 2e-38, -3e-38]
     qs, ds = _quant_gpu(x, K_pad)
     rq, rd = orc.quantize_q8_1(x, K_pad)
     assert_same(host(qs), rq, "qs")

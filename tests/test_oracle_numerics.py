@@ -102,6 +102,52 @@ def test_q8_1_fp16_overflow_of_d(orc):
 
 
 # ------------------------------------------------------------ Q8_0 -------
+def test_q8_1_tiny_amax_saturates(orc):
+    # amax = 1e-38 < 127 / FLT_MAX: 127 / amax overflows to inf, and the
+    # reference's __float2int_rn saturates the +-inf products (0 * inf -> 0)
+    row = np.zeros(32, np.float32)
+    row[0], row[1], row[2] = 1e-38, -1e-38, 5e-39
+    q, ds = _q81(orc, row)
+    assert q[0] == 127 and q[1] == -128 and q[2] == 127 and (q[3:] == 0).all()
+    assert ds[0, 0] == 0.0  # d = amax / 127 is below the f16 range
+
+
+def test_q8_round_by_magic_add_equals_rint():
+    """The device kernels round x * (127 / amax) to int8 by adding 1.5 * 2^23
+    to the f32 product and keeping the low bits (s2x_device.h q8_round).
+    That equals rint (half to even) and never needs the [-128, 127] clamp
+    for every product a Q8_1 block can form: all f32 values of magnitude up
+    to 127.0001 near each half-integer and integer (ties, their float
+    neighbours), plus random products x * inv with |x| <= amax."""
+    magic = np.float32(12582912.0)
+
+    def by_magic(p):
+        s = (p.astype(np.float32) + magic).astype(np.float32)
+        return (s.view(np.uint32).astype(np.int64) - 0x4B400000).astype(np.int64)
+
+    h = np.arange(-255, 256, dtype=np.float64) / 2.0  # -127.5 .. 127.5 step 0.5
+    pts = h.astype(np.float32)
+    near = [pts]
+    for _ in range(4):  # 4 float steps either side of every point
+        near.append(np.nextafter(near[-1], np.float32(np.inf)))
+    below = [pts]
+    for _ in range(4):
+        below.append(np.nextafter(below[-1], np.float32(-np.inf)))
+    p = np.concatenate(near + below)
+    p = p[np.abs(p) <= np.float32(127.0001)]
+    assert np.array_equal(by_magic(p), np.rint(p).astype(np.int64))
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((20000, 32)).astype(np.float32)
+    x[:100] *= np.float32(1e-30)  # tiny blocks
+    x[100:200] *= np.float32(1e30)
+    amax = np.abs(x).max(axis=1, keepdims=True)
+    inv = (np.float32(127.0) / amax).astype(np.float32)
+    prod = (x * inv).astype(np.float32)
+    q = by_magic(prod)
+    assert np.array_equal(q, np.rint(prod).astype(np.int64))
+    assert q.min() >= -127 and q.max() <= 127
+
+
 def test_q8_0_roundf_half_away(orc):
     w = np.zeros((1, 32), np.float32)
     w[0, 0] = 127.0            # d = 1, id = 1
