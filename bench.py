@@ -301,7 +301,8 @@ def bench_batch1(step, sync, gemm_stats, v, s2x, np, iters=60):
         return g_ops / (g_ms / 1000.0) / 1e12, g_ms / n_rate
 
     tops, g_img = rate()
-    # the K-split GEMM option (s2x_vision_set_split_k): other bits, same
+    # the experimental K-split GEMM option (s2x_vision_set_split_k; outside
+    # the parity tolerance, for comparison only): other bits, same
     # arithmetic per K range
     s2x.call("s2x_vision_set_split_k", v, 1)
     lat_split = latencies()
@@ -319,7 +320,11 @@ def bench_batch1(step, sync, gemm_stats, v, s2x, np, iters=60):
             "iters": iters, "gemm_tops": round(tops, 1),
             "gemm_frac": round(tops / INT8_PEAK_TOPS, 4),
             "gemm_ms_per_image": round(g_img, 3),
-            "split_k": {"ms_p50": round(pct(lat_split, 0.5), 3),
+            # experimental option outside the parity tolerance: not a
+            # result for this workload
+            "split_k_experimental": {
+                        "parity": "outside tolerance: embedding cosine 0.9998 < 0.9999",
+                        "ms_p50": round(pct(lat_split, 0.5), 3),
                         "images_per_s": round(1000.0 / pct(lat_split, 0.5), 1),
                         "gemm_tops": round(tops_split, 1),
                         "gemm_frac": round(tops_split / INT8_PEAK_TOPS, 4),
@@ -445,7 +450,8 @@ def bench_text(np, s2x, synth, warm=3, iters=20):
         return lat
 
     lat = timed()
-    # the K-split GEMM option (off by default), for comparison
+    # the experimental K-split GEMM option (off by default; outside the
+    # parity tolerance), for comparison only
     s2x.call("s2x_text_set_split_k", t, 1)
     lat_split = timed()
     s2x.lib.s2x_text_destroy(t)
@@ -455,7 +461,9 @@ def bench_text(np, s2x, synth, warm=3, iters=20):
                         "+ head, host ids in / host embeddings out",
             "ms_p50": round(p50, 3), "ms_p99": round(pct(lat, 0.99), 3),
             "ms_min": round(min(lat), 3), "iters": iters,
-            "ms_p50_split_k": round(pct(lat_split, 0.5), 3)}
+            "split_k_experimental": {
+                "parity": "outside tolerance: embedding cosine 0.99988 < 0.9999",
+                "ms_p50": round(pct(lat_split, 0.5), 3)}}
 
 
 def cpu_baseline(args, hm, px, n_pos, gh, gw):

@@ -100,8 +100,15 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     }
 }
 
-// rowmap[seg_start[s] + pos] = s << 16 | pos for pos < min(seg_len[s],
-// max_len); entries outside [0, n_rows) are skipped
+// Every row starts as ROW_NONE (no segment covers it: the QKV epilogue
+// stores nothing for it), then rowmap[seg_start[s] + pos] = s << 16 | pos
+// for pos < min(seg_len[s], max_len); entries outside [0, n_rows) are
+// skipped.  Both are kernels, so a captured encode replays them.
+__global__ __launch_bounds__(256) void k_rowmap_clear(int32_t *__restrict__ rowmap, int64_t n_rows) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n_rows) rowmap[r] = ROW_NONE;
+}
+
 __global__ __launch_bounds__(256) void k_rowmap(const int32_t *__restrict__ seg_start,
                                                 const int32_t *__restrict__ seg_len,
                                                 int32_t *__restrict__ rowmap, int64_t n_rows) {
@@ -113,8 +120,11 @@ __global__ __launch_bounds__(256) void k_rowmap(const int32_t *__restrict__ seg_
 
 hipError_t launch_rowmap(const int32_t *seg_start, const int32_t *seg_len, int64_t n_seg,
                          int64_t max_len, int32_t *rowmap, int64_t n_rows, hipStream_t stream) {
-    if (n_seg == 0 || max_len == 0) return hipSuccess;
-    if (n_seg > 32767 || max_len > 65535) return hipErrorInvalidValue;
+    if (n_rows == 0) return hipSuccess;
+    if (n_seg > 32767 || max_len > 65535 || n_rows > (int64_t)1 << 40) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rowmap_clear, dim3((unsigned)((n_rows + 255) / 256)), dim3(256), 0, stream,
+                       rowmap, n_rows);
+    if (n_seg == 0 || max_len == 0) return hipGetLastError();
     hipLaunchKernelGGL(k_rowmap, dim3((unsigned)((max_len + 255) / 256), (unsigned)n_seg),
                        dim3(256), 0, stream, seg_start, seg_len, rowmap, n_rows);
     return hipGetLastError();

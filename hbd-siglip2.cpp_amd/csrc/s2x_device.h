@@ -125,9 +125,17 @@ __device__ __forceinline__ int group_isum(int v) {
 // clamped to [-128, 127] (src/cuda/siglip2_custom_mmq.cu:63-76), the
 // conversion saturating (+inf -> 127, -inf -> -128, NaN -> 0) as
 // __float2int_rn does: the case of a block whose 127 / amax overflows
-// (amax < 127 / FLT_MAX) or whose amax is NaN.
+// (amax < 127 / FLT_MAX) or whose amax is NaN.  The conversion is the
+// instruction v_cvt_i32_f32 itself, whose saturation (values beyond the
+// int32 range and +-inf to INT32_MAX / INT32_MIN, NaN to 0) the ISA
+// defines; a C++ conversion of such a value would be undefined.
+__device__ __forceinline__ int cvt_i32_sat(float r) {
+    int q;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+    return q;
+}
 __device__ __forceinline__ int q8_round(float x, float inv) {
-    int q = (int)__builtin_rintf(x * inv);
+    int q = cvt_i32_sat(__builtin_rintf(x * inv));
     q = q > 127 ? 127 : q;
     q = q < -128 ? -128 : q;
     return q;

@@ -113,6 +113,12 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
                                       uint8_t *lds_wave_base) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 16, voff, soff, 0, 0);
 }
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint8_t *lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_wave_base, 4, voff, 0, 0, 0);
+}
+// A per-lane offset past every buffer's range (num_records <= 2^31 - 1):
+// that lane's DMA returns zeros and reads no memory.
+constexpr uint32_t OOB_OFF = 0x80000000u;
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -255,9 +261,10 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                     const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
                     const int m = mw + a * 32 + row, n = nw + c;
                     if (m >= M || n >= N) continue;
+                    const int rm = rmv[i];
+                    if (rm == ROW_NONE) continue;
                     const int hd = n - hd0;
                     const int h = small_div(hd, epi.d_head, inv_dh), d = hd - h * epi.d_head;
-                    const int rm = rmv[i];
                     const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                     const v8h v = *reinterpret_cast<const v8h *>(scr + row * P + c);
                     *reinterpret_cast<v8h *>(dst0 + (sh * epi.len_pad + (rm & 0xffff)) * epi.d_pad + d) = v;
@@ -284,8 +291,10 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                     rm_first = epi.rowmap[mr];
                     rm_last = epi.rowmap[mr + rows - 1];
                 }
-                // one segment, consecutive positions: the common case
-                const bool run = rows > 0 && (rm_last >> 16) == (rm_first >> 16) &&
+                // one segment, consecutive positions: the common case (the
+                // rows between two covered rows of one segment are covered)
+                const bool run = rows > 0 && rm_first != ROW_NONE && rm_last != ROW_NONE &&
+                                 (rm_last >> 16) == (rm_first >> 16) &&
                                  (rm_last & 0xffff) - (rm_first & 0xffff) == rows - 1;
                 const int shift = run ? (rm_first & 0xffff) & 7 : 0;
 #pragma unroll
@@ -316,6 +325,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                     } else {
                         for (int i = 0; i < rows; ++i) {
                             const int rm = epi.rowmap[mr + i];
+                            if (rm == ROW_NONE) continue;
                             const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                             epi.vt[(sh * epi.dv_pad + d) * epi.len_pad + (rm & 0xffff)] = col[i];
                         }
@@ -338,6 +348,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                         const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                         if (m >= M) continue;
                         const int rm = epi.rowmap[m];
+                        if (rm == ROW_NONE) continue;
                         const int64_t sh = (int64_t)(rm >> 16) * epi.n_head + h;
                         const int pos = rm & 0xffff;
                         const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
@@ -471,20 +482,56 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         clip32(((int64_t)(KB_all - kbs) * ldT - n0) * 2), BUF_DW3);
     const __amdgpu_buffer_rsrc_t none = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, 0, BUF_DW3);
 
-    // Issue the DMA of stage g into buffer g % NS.  Reads past M, N or the
-    // planes return zeros (the scalar offset is part of the range check);
-    // blocks past KB in the last stage are fetched and never used.  A stage
-    // past the last is issued through zero-size buffers (no memory is read)
-    // and ROLE (a constant per wave: 1 X scales, 2 W scales, 0 neither) is
-    // a template value, so that no branch splits the K loop.
+    // Issue the DMA of stage g into buffer g % NS.  Rows past M or N return
+    // zeros through the per-lane offset (the vector offset alone exceeds the
+    // range), and a stage past the last is issued through zero-size buffers
+    // (no memory is read).  No read goes past block KB - 1, whatever the
+    // range check does with the scalar offset: a partial last stage (KB %
+    // KS blocks, KB >= KS) is fetched as the window of the last KS blocks,
+    // kpos(g) = KB - KS, so its block kb0 + j lands in slot j + shift of the
+    // stage buffer (shift = kb0 - kpos); a GEMM of fewer than KS blocks has
+    // one partial stage, fetched by the first issue (outside the K loop)
+    // with a zero-size buffer per missing block and out-of-range lanes for
+    // the missing scales.  ROLE (a constant per wave: 1 X scales, 2 W
+    // scales, 0 neither) is a template value, so that no branch splits the
+    // K loop.
     // PART: 0 the X quants, 1 the W quants, 2 the scales, -1 all three
-    auto issue = [&](int g, auto role, auto part) {
+    auto kpos = [&](int g) { return KB >= KS ? min(g * KS, KB - KS) : g * KS; };
+    auto issue = [&](int g, auto role, auto part, auto first) {
         constexpr int ROLE = decltype(role)::value, PART = decltype(part)::value;
         const bool live = g < n_st;
+        uint8_t *sb = lds + (g % NS) * STAGE;
+        if constexpr (decltype(first)::value) {
+            if (KB < KS) {
+                // the only stage, blocks 0 .. KB - 1 of KS
+#pragma unroll
+                for (int t = 0; t < C::QPX; ++t) {
+                    const int i = C::QPX * wave + t, j = i % KS;
+                    dma16(j < KB ? xr_live : none, vqx, j * 32, sb + XQ + j * BM * 32 + (i / KS) * 1024);
+                }
+#pragma unroll
+                for (int t = 0; t < C::QPW; ++t) {
+                    const int i = C::QPW * wave + t, j = i % KS;
+                    dma16(j < KB ? wr_live : none, vqw, j * 32, sb + WQ + j * BN * 32 + (i / KS) * 1024);
+                }
+                if constexpr (ROLE == 1) {
+                    // one 4-byte DMA per ds word: 16 rows x KS words per
+                    // instruction, the words of missing blocks out of range
+#pragma unroll
+                    for (int t = 0; t < 64 / 16; ++t) {
+                        const int row = 64 * wave + 16 * t + (lane >> 2), w = lane & 3;
+                        const uint32_t off = w < KB ? (uint32_t)((row * ld_ds + w) * 4) : OOB_OFF;
+                        dma4(xsr_live, off, sb + XS + (64 * wave + 16 * t) * 16);
+                    }
+                } else if constexpr (ROLE == 2) {
+                    dma16(wsr_live, (lane >> 4) < KB ? vws : OOB_OFF, 0, sb + WS);  // lane: block lane / 16
+                }
+                return;
+            }
+        }
         const __amdgpu_buffer_rsrc_t xr = live ? xr_live : none, wr = live ? wr_live : none;
         const __amdgpu_buffer_rsrc_t xsr = live ? xsr_live : none, wsr = live ? wsr_live : none;
-        uint8_t *sb = lds + (g % NS) * STAGE;
-        const uint32_t k0 = (uint32_t)(g * KS);
+        const uint32_t k0 = (uint32_t)kpos(g);
         if constexpr (PART == 0 || PART < 0) {
 #pragma unroll
             for (int t = 0; t < C::QPX; ++t) {
@@ -523,8 +570,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     const int sx_off = XS + xrow * 16;
     // lanes 32..63 read the zeros after the W scales (at offsets < 1 KB)
     const int sw_off = lh ? WS + KS * BN * 2 : WS + wcol * 2;
-    auto load_frag = [&](const uint8_t *sb, auto jc, Frag<TM> &f) {
-        constexpr int j = decltype(jc)::value;
+    // slot j of the stage buffer (a constant in the K loop; the last
+    // stage's block j + its window shift)
+    auto load_frag = [&](const uint8_t *sb, int j, Frag<TM> &f) {
 #pragma unroll
         for (int a = 0; a < TM; ++a)
             f.a[a] = *reinterpret_cast<const v4i *>(sb + a_off + j * BM * 32 + a * 32 * 32);
@@ -619,9 +667,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
     auto k_loop = [&](auto role) {
-    issue(0, role, All{});
+    issue(0, role, All{}, std::true_type{});
     arrive();  // the first stage visible
-    if constexpr (C::LAT) issue(1, role, All{});
+    if constexpr (C::LAT) issue(1, role, All{}, std::false_type{});
     // stage g computed while stage g + 1 loads; each block's fragments are
     // read right before its MFMAs (the other waves of the SIMD cover the
     // LDS latency)
@@ -637,7 +685,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
                 for (int a = 0; a < TM; ++a) Fs[j].sx[a] = v2i{0, 0};
 #pragma unroll
                 for (int b = 0; b < 2; ++b) Fs[j].sw[b] = v2i{0, 0};
-                load_frag(sb, jc, Fs[j]);
+                load_frag(sb, j, Fs[j]);
             });
             static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value); });
         } else {
@@ -646,25 +694,26 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             // barrier, when every wave of the CU starts reading fragments
             static_for<KS>([&](auto jc) {
                 constexpr int j = decltype(jc)::value;
-                load_frag(sb, jc, F);
+                load_frag(sb, j, F);
                 compute(F, kb0 + j);
-                if constexpr (j < 3) issue(g + 1, role, std::integral_constant<int, j>{});
+                if constexpr (j < 3) issue(g + 1, role, std::integral_constant<int, j>{}, std::false_type{});
             });
         }
         arrive();
         // the latency form's MFMAs may sink below the barrier (its stage is
         // one scheduling region): its next DMA goes out after the barrier,
         // a whole stage before the wait for it
-        if constexpr (C::LAT) issue(g + 2, role, All{});
+        if constexpr (C::LAT) issue(g + 2, role, All{}, std::false_type{});
     }
     {
-        // the last stage: nb = 1 .. KS blocks
+        // the last stage: nb = 1 .. KS blocks, block kb0 + j in slot
+        // j + shift (a partial stage was fetched as the last KS blocks)
         const uint8_t *sb = lds + ((n_st - 1) % NS) * STAGE;
-        const int kb0 = (n_st - 1) * KS, nb = KB - kb0;
+        const int kb0 = (n_st - 1) * KS, nb = KB - kb0, shift = kb0 - kpos(n_st - 1);
         static_for<KS>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             if (j < nb) {
-                load_frag(sb, jc, F);
+                load_frag(sb, j + shift, F);
                 compute(F, kb0 + j);
             }
         });
@@ -769,14 +818,17 @@ __global__ __launch_bounds__(CfgH::NT) __attribute__((amdgpu_waves_per_eu(4))) v
         const int r = 16 * (C::DMA_N / KS * (wave & 3) + t / KS) + (lane >> 2);
         voff[t] = (uint32_t)(r * row_bytes) + (uint32_t)(((lane & 3) ^ swz4(r)) * 16);
     }
+    // blocks past KB (an odd KB's last stage, every block of a stage past
+    // the last) through the zero-size buffer: nothing past the planes is
+    // addressed
     auto issue = [&](int g) {
-        const __amdgpu_buffer_rsrc_t src = g < n_st ? src_live : none;
         uint8_t *sb = lds + (g & 1) * STAGE + (kind == 0 ? XQ : WQ);
         const uint32_t k0 = (uint32_t)(g * KS);
 #pragma unroll
         for (int t = 0; t < C::DMA_N; ++t) {
             const int j = t % KS, grp = C::DMA_N / KS * (wave & 3) + t / KS;
-            dma16(src, voff[t], (k0 + j) * 64, sb + j * BM * 64 + grp * 1024);
+            dma16((int)k0 + j < KB ? src_live : none, voff[t], (k0 + j) * 64,
+                  sb + j * BM * 64 + grp * 1024);
         }
     };
     auto arrive = [&](int g) {

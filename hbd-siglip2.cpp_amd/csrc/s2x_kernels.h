@@ -41,6 +41,9 @@ enum EpiKind {
     EPI_GELU_F16 = 7,  // GELU(mm + bias) rounded to f16 (rows of h_kpad halves)
 };
 
+// row map entry of a GEMM row that no segment covers
+constexpr int32_t ROW_NONE = -1;
+
 struct EpiParams {
     int          kind;
     const float *bias;
@@ -49,7 +52,8 @@ struct EpiParams {
     int64_t      resid_rows;  // 0: row m; >0: row m % resid_rows
     int64_t      dump_kb;     // EPI_DUMP_I: the block whose int32 dot is written
     // EPI_QKV: output columns [q | k | v] (n_head x d_head each); row m is
-    // position rowmap[m] & 0xffff of segment rowmap[m] >> 16
+    // position rowmap[m] & 0xffff of segment rowmap[m] >> 16, or no
+    // position at all (nothing stored) where rowmap[m] is ROW_NONE
     _Float16      *q, *k, *vt;
     const int32_t *rowmap;
     int            n_head, d_head, d_pad, dv_pad, len_pad;

@@ -415,7 +415,10 @@ int s2x_vision_set_attention_fp64(s2x_vision *v, int enable);
  * later ones replay it (up to 4 shapes per encoder).  Results are the same
  * bits either way. */
 int s2x_vision_set_graphs(s2x_vision *v, int enable);
-/* 1 = the vision tower's plain and residual GEMMs of 32+ K blocks (out,
+/* EXPERIMENTAL, outside the parity tolerance: the embeddings it gives reach
+ * cosine 0.9998 of the block-order CPU restatement, below the 0.9999 that
+ * the default path meets.
+ * 1 = the vision tower's plain and residual GEMMs of 32+ K blocks (out,
  * fc2, the head's) run as s2x_mul_mat_q8_0_q8_1_split_k (2 ranges, 4 from
  * 96 blocks), for latency at batch 1; 0 (default) = one block-order sum per
  * output, the oracle's.  No counterpart in the reference (whose GPU GEMMs
@@ -476,7 +479,9 @@ int s2x_text_set_stream(s2x_text *t, void *stream);
 int s2x_text_set_attention_fp64(s2x_text *t, int enable);
 /* As s2x_vision_set_graphs, for the text tower. */
 int s2x_text_set_graphs(s2x_text *t, int enable);
-/* 1 = the text tower's plain and residual GEMMs of 32+ K blocks run as
+/* EXPERIMENTAL, outside the parity tolerance (cosine 0.99988 of the
+ * block-order CPU restatement on the so400m text tower, below 0.9999).
+ * 1 = the text tower's plain and residual GEMMs of 32+ K blocks run as
  * s2x_mul_mat_q8_0_q8_1_split_k (2 ranges, 4 from 96 blocks); 0 (default) =
  * one block-order sum per output, the oracle's.  No counterpart in the
  * reference (whose GPU GEMMs split K by stream-K); a prompt's bits do not

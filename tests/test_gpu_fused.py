@@ -195,6 +195,11 @@ QKV_CASES = {
     "ragged_small": [1, 64, 130, 255, 33, 729, 2],
     "batch32": [729] * 32,
 }
+# padded layouts: segment s starts at s * stride, so rows between a
+# segment's end and the next start belong to no segment (the fused
+# epilogue must store nothing for them)
+QKV_STRIDES = {"gapped_padded": 128}
+QKV_CASES["gapped_padded"] = [100, 128, 1, 77]
 
 
 @pytest.mark.timeout(300)
@@ -202,8 +207,14 @@ QKV_CASES = {
 def test_qkv_attn_prep(orc, weights, case):
     raw, N, K, K_pad, bias = weights["qkv"]
     lens = np.asarray(QKV_CASES[case], np.int32)
-    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
-    M, n_seg, max_len = int(lens.sum()), len(lens), int(lens.max())
+    if case in QKV_STRIDES:
+        stride = QKV_STRIDES[case]
+        starts = (np.arange(len(lens)) * stride).astype(np.int32)
+        M = int(stride * (len(lens) - 1) + lens[-1])
+    else:
+        starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+        M = int(lens.sum())
+    n_seg, max_len = len(lens), int(lens.max())
     say(f"QKV -> attention planes: {case}, M={M}, {n_seg} segments")
     x = np.random.default_rng(36).standard_normal((M, K)).astype(np.float32)
     qs, ds = _quant_gpu(x, K_pad)

@@ -175,24 +175,31 @@ def test_gemm_matches_oracle(orc, gemm_data, label):
     assert n_diff == 0  # same per-block fma order as the oracle: bit-exact
 
 
-# K blocks 1..7 and 13: stage rings of several blocks end part-filled;
-# ragged N and M leave partial edge tiles
+# K blocks 1..7 and 13: stage rings of several blocks end part-filled
+# (fewer than 4 blocks: one partial stage; otherwise the last stage is
+# fetched as the window of the last 4 blocks); ragged N and M leave partial
+# edge tiles.  "small": 6 tiles, the latency form; "wide": 520 tiles of
+# 128 x 128, the throughput form (sampled rows, the last tile's included).
+@pytest.mark.parametrize("form", ["small", "wide"])
 @pytest.mark.parametrize("KB", [1, 2, 3, 4, 5, 7, 13])
-def test_gemm_short_k(orc, KB):
-    M, N, K_pad = 300, 200, 32 * KB
+def test_gemm_short_k(orc, KB, form):
+    M, N = (300, 200) if form == "small" else (8300, 1000)
+    K_pad = 32 * KB
     K = K_pad - (5 if KB > 1 else 0)
     say(f"gemm short K: KB={KB} M={M} N={N}")
     rng = np.random.default_rng(40 + KB)
     raw = synth.quantize_q8_0(rng.normal(0, 0.02, (N, K)).astype(np.float32), K_pad)
     x = rng.standard_normal((M, K)).astype(np.float32)
     qs, ds = _quant_gpu(x, K_pad)
-    rq, rd = orc.quantize_q8_1(x, K_pad)
+    rows = np.arange(M) if form == "small" else np.unique(np.concatenate(
+        [rng.choice(M, 200, replace=False), np.arange(M - 44, M)]))
+    rq, rd = orc.quantize_q8_1(x[rows], K_pad)
     ref = orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd)
     w = _weight(raw, K_pad, N)
     try:
         y = empty((M, N), torch.float32)
         s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, ptr(y), N, None, stream())
-        assert_same(host(y), ref, f"gemm KB={KB}")
+        assert_same(host(y)[rows], ref, f"gemm KB={KB} {form}")
     finally:
         s2x.lib.s2x_weight_destroy(w)
 
