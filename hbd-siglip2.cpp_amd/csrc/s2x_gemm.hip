@@ -6,15 +6,25 @@
 //
 // I_kb is the exact int32 dot of the 32 quants of block kb; dw and dx are the
 // fp16 block scales (src/cuda/siglip2_custom_mmq.cu:259-267 is the same
-// per-block rescale).  Per 32 x 32 output subtile and K block:
-//   * I   = one v_mfma_i32_32x32x32_i8 (exact) accumulating onto the bits of
-//           the float 1.5 * 2^23, then one v_mfma_f32_32x32x8_f16 that
-//           subtracts 1.5 * 2^23 (-2048 x 6144 in k-slot 0): (float)I,
-//           exactly, without a VALU convert;
+// per-block rescale).  The K loop carries acc' = acc * 2^-26 (below); per
+// 32 x 32 output subtile and K block:
+//   * I'  = I * 2^-26: one v_mfma_i32_32x32x32_i8 (exact) accumulating onto
+//           the bits of the float c0 = 0x3E22F983 (1/2pi, an inline
+//           constant: no registers), so that the result read as a float is
+//           c0 + I * 2^-26 exactly (|I| <= 2^19 stays inside c0's binade),
+//           then one v_mfma_f32_32x32x8_f16 adding -c0 as three exact f16
+//           products (every partial sum is a multiple of 2^-26 below 1/4:
+//           exact in any order);
 //   * s   = dx[i] * dw[j] as one v_mfma_f32_32x32x8_f16 whose A holds dx in
 //           k-slot 0 and B holds dw in k-slot 0, every other slot zero: each
 //           output is one exact f16 x f16 product in f32;
-//   * acc = fmaf(I, s, acc) on the VALU.
+//   * acc' = fmaf(I', s, acc') on the VALU.
+// The scaling commutes with every rounding: all terms are multiples of
+// 2^-74 (f16 scales are multiples of 2^-24) and |acc| < 2^19 * 65504^2 *
+// KB < 2^80, so acc' never reaches the subnormals nor acc overflow, and
+// fmaf(I', s, acc') = 2^-26 fmaf(I, s, acc) at every step; the epilogue
+// multiplies by 2^26 (exact).  The outputs are those of the per-block fma
+// chain bit for bit.
 // Three MFMAs (96 matrix-pipe cycles) against 16 VALU instructions (64
 // cycles): the matrix pipe bounds this formulation at a third of the int8
 // MFMA peak.
@@ -26,7 +36,8 @@
 // whose K stages are scheduled for a lone wave's latency instead.  The K
 // loop runs over stages of KS blocks whose operands (X and W quants and
 // scales) arrive by LDS DMA (buffer_load ... lds) into a ring of NS stage
-// buffers, NS - 1 stages ahead; one workgroup barrier per stage.
+// buffers, NS - 1 stages ahead (NS = 2; 3 or 4 in the latency form); one
+// workgroup barrier per stage.
 //
 // Scale layouts: X scales are the Q8_1 ds words of the activation
 // (ds[m * ld_ds + kb] = fp16 d | fp16 s << 16, the block_q8_1 scale pair);
@@ -38,7 +49,9 @@
 //   WQ  [KS][128 rows][32]  W quants, same swizzle
 //   XS  [128][KS] u32        X ds words, a row's KS blocks together (as in
 //                            the ds plane: one 16-byte DMA lane per row)
-//   WS  [KS][128] u16        W scales, then 1 KB of zeros
+//   WS  [KS][128] u16        W scales in the dT plane's column order
+//                            (columns j and j + 32 of each 64-column half
+//                            in one 32-bit word)
 // A fragment read (lane l: row l & 31, chunk l >> 5, 16 bytes) then touches
 // 16 distinct 16-byte bank groups per 16 lanes: no bank conflicts.
 #include "s2x_device.h"
@@ -63,16 +76,17 @@ constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dword
 // than one or two waves): a stage's KS blocks are one scheduling region --
 // all their fragments read up front, their MFMAs interleaved -- with up to
 // 256 VGPRs, so that a lone wave keeps its matrix pipe busy.
-template <int KS_, int NS_, int BM_ = 128, bool LAT_ = false>
+template <int KS_, int NS_, int BM_ = 128, bool LAT_ = false, int TM_ = 1, int TN_ = 2>
 struct Cfg {
-    static constexpr int TM = 1, BM = BM_, KS = KS_, NS = NS_;
+    static constexpr int TM = TM_, TN = TN_, BM = BM_, KS = KS_, NS = NS_;
     static constexpr bool LAT = LAT_;
-    static constexpr int NWAVE = BM / 16, NT = NWAVE * WAVE;
+    // waves of 32 TM x 32 TN outputs, WN of them along N
+    static constexpr int WN = BN / (32 * TN), NWAVE = BM / (32 * TM) * WN, NT = NWAVE * WAVE;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
     static constexpr int XS = WQ + KS * BN * 32;  // [BM][KS] u32 X ds words
-    static constexpr int WS = XS + KS * BM * 4;   // [KS][BN] fp16 W scales, then 1 KB of zeros
-    static constexpr int STAGE = WS + KS * BN * 2 + 1024;
+    static constexpr int WS = XS + KS * BM * 4;   // [KS][BN] fp16 W scales
+    static constexpr int STAGE = WS + KS * BN * 2;
     static constexpr int LDS_BYTES = NS * STAGE;
     static constexpr int WG_PER_CU = 2 * LDS_BYTES <= 163840 ? 2 : 1;
     static constexpr int WPE = LAT ? 2 : WG_PER_CU * NWAVE / 4;  // waves per SIMD
@@ -88,7 +102,7 @@ struct Cfg {
     static_assert(KS == 4, "stage of 4 blocks: one 16-byte ds row per X row");
     static_assert(BM == 128 || BM == 64, "tile rows");
     static_assert(QPX >= 1 && QPW >= 1 && QPX <= KS && QPW <= KS, "DMA split");
-    static_assert(NS == 2, "a ring of two stages: each stage's DMA is waited for in full");
+    static_assert(NS == 2 || (LAT && NS <= 4), "ring: two stages, or up to four in the latency form");
     static_assert(NSX + 1 <= NWAVE, "scale DMA waves");
     static_assert(LDS_BYTES * WG_PER_CU <= 163840, "LDS");
     static_assert(NWAVE * 5120 <= LDS_BYTES, "epilogue scratch");
@@ -142,22 +156,26 @@ __device__ __forceinline__ void tile_of(int T, int m_tiles, int n_tiles, int &tm
 
 // One K block's MFMA operands for a wave's TM x 2 subtiles.  The scale
 // operands are the 4-half (two-dword) f16 vectors of a 32x32x8 MFMA: dword 0
-// holds the scale in its low half (k slot 0 on lanes 0..31, slot 4 on lanes
-// 32..63), dword 1 is always zero.  Lanes 32..63 load the row scale too but
-// a zero column scale, so slot 4 adds nothing.
-template <int TM>
+// holds the scale in its low half (k slot 0 on lanes 0..31), every other
+// half is zero, and lanes 32..63 (k slots 4..7) are zero in both operands,
+// so no product is 0 x inf.
+template <int TM, int TN>
 struct Frag {
-    v4i a[TM], b[2];
-    v2i sx[TM], sw[2];
+    v4i a[TM], b[TN];
+    uint32_t xw[TM], wp;  // the raw ds words and W-scale word (operands built at use)
 };
 
-// Epilogue of one wave's 32 TM x 64 block (rows mw.., columns nw..), from
+// Epilogue of one wave's 32 TM x 32 TN block (rows mw.., columns nw..), from
 // the accumulators in registers; wscr: 5,120 bytes of LDS of this wave.
+// The GELU -> Q8_1 / f16 and QKV epilogues take 32 x 64 blocks (TN = 2).
 constexpr int EPI_SCRATCH = 5120;
-template <int TM, int EPI>
-__device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&bias_v)[2], int lane,
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (&bias_v)[TN], int lane,
                                          int mw, int nw, int M, int N, float *__restrict__ y,
                                          int64_t ldy, const EpiParams &epi, uint8_t *wscr) {
+    static_assert(TN == 2 || EPI == EPI_NONE || EPI == EPI_BIAS || EPI == EPI_BIAS_GELU ||
+                      EPI == EPI_BIAS_RESID || EPI == EPI_DUMP_I,
+                  "32 x 32 waves take the plain epilogues only");
     const int lr = lane & 31, lh = lane >> 5;
     if constexpr (EPI == EPI_GELU_Q81) {
         // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over
@@ -376,7 +394,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
             BUF_DW3);
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
-            float res[2][16];
+            float res[TN][16];
             if constexpr (EPI == EPI_BIAS_RESID) {
                 // residual row of this lane's first row in the half; the
                 // others are at most 27 rows further (one wrap when
@@ -385,7 +403,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                 const int m_first = mw + a * 32 + 4 * lh;
                 const int r_first = rmod ? m_first % R : m_first - mw;
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
+                for (int b = 0; b < TN; ++b) {
                     const int n = nw + b * 32 + lr;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -400,7 +418,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][2][16], const float (&
                 }
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < TN; ++b) {
                 const int n = nw + b * 32 + lr;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -433,7 +451,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    constexpr int TN = C::TN;
+    const int wm = wave / C::WN, wn = wave % C::WN;
     const int lr = lane & 31, lh = lane >> 5;
     const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + BN - 1) / BN;
     int tm, tn;
@@ -564,61 +583,71 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     };
 
     // fragment addresses (bytes within a stage buffer) of this lane
-    const int xrow = wm * 32 * TM + lr, wcol = wn * 64 + lr;
+    const int xrow = wm * 32 * TM + lr, wcol = wn * 32 * TN + lr;
     const int a_off = XQ + xrow * 32 + ((lh ^ swz(lr)) * 16);
     const int b_off = WQ + wcol * 32 + ((lh ^ swz(lr)) * 16);
     const int sx_off = XS + xrow * 16;
-    // lanes 32..63 read the zeros after the W scales (at offsets < 1 KB)
-    const int sw_off = lh ? WS + KS * BN * 2 : WS + wcol * 2;
+    // the 32-bit word of W scales (column j | column j + 32 << 16 of a
+    // 64-column group) holding this lane's columns, and the low half of the
+    // X ds word (the scale d), both masked to zero on lanes 32..63 (k slots
+    // 4..7); a 32 x 32 wave takes the half of the word its columns are
+    const int sw_off = WS + (wn * TN / 2) * 128 + lr * 4;
+    const int sw_sh = TN == 1 ? 16 * (wn & 1) : 0;
+    const uint32_t xmask = lh ? 0u : 0xffffu, wmask = lh ? 0u : ~0u;
     // slot j of the stage buffer (a constant in the K loop; the last
     // stage's block j + its window shift)
-    auto load_frag = [&](const uint8_t *sb, int j, Frag<TM> &f) {
+    auto load_frag = [&](const uint8_t *sb, int j, Frag<TM, TN> &f) {
 #pragma unroll
         for (int a = 0; a < TM; ++a)
             f.a[a] = *reinterpret_cast<const v4i *>(sb + a_off + j * BM * 32 + a * 32 * 32);
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < TN; ++b)
             f.b[b] = *reinterpret_cast<const v4i *>(sb + b_off + j * BN * 32 + b * 32 * 32);
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
-            f.sx[a][0] = *reinterpret_cast<const uint16_t *>(sb + sx_off + j * 4 + a * 32 * 16);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-            f.sw[b][0] = *reinterpret_cast<const uint16_t *>(sb + sw_off + j * BN * 2 + b * 32 * 2);
+        for (int a = 0; a < TM; ++a) f.xw[a] = *reinterpret_cast<const uint32_t *>(sb + sx_off + j * 4 + a * 32 * 16);
+        f.wp = *reinterpret_cast<const uint32_t *>(sb + sw_off + j * BN * 2);
+    };
+    // the scale operands of subtile (a, b), from the raw words: the VALU
+    // work sits with the MFMAs that use it, not with the (early) reads
+    auto sx_op = [&](const Frag<TM, TN> &f, int a) { return v2i{(int)(f.xw[a] & xmask), 0}; };
+    auto sw_op = [&](const Frag<TM, TN> &f, int b) {
+        const uint32_t w = f.wp & wmask;
+        return v2i{(int)(TN == 2 ? (b ? w >> 16 : w & 0xffffu) : (w >> sw_sh) & 0xffffu), 0};
     };
 
-    float acc[TM][2][16];
-    Frag<TM> F;
-#pragma unroll
-    for (int a = 0; a < TM; ++a) F.sx[a] = v2i{0, 0};
-#pragma unroll
-    for (int b = 0; b < 2; ++b) F.sw[b] = v2i{0, 0};
+    float acc[TM][TN][16];
+    Frag<TM, TN> F;
 
     // One K block, subtile k = 2a + b, in three MFMAs and 16 fmas:
-    //   D = X.W^T + 0x4B400000 (int8 MFMA whose accumulator starts at the
-    //       bits of the float 1.5 * 2^23, whose ulp is 1: D read as a float
-    //       is 12582912 + I exactly, |I| <= 32 * 128 * 128 < 2^22);
-    //   I = D - 12582912 (an f16 MFMA adding -2048 x 6144 from k-slot 0 to
-    //       the accumulator D: exact, so I is (float)I_kb);
+    //   D = X.W^T + 0x3E22F983 (int8 MFMA whose accumulator starts at the
+    //       bits of c0 = 1/2pi, an inline constant, whose ulp is 2^-26: D
+    //       read as a float is c0 + I 2^-26 exactly, |I| <= 32 * 128 * 128
+    //       = 2^19 and c0's mantissa 0x22F983 +- 2^19 stays in [0, 2^23));
+    //   I' = D - c0 (an f16 MFMA adding -0.125 x 1, -1119/256 x 2^-7 and
+    //       -387/8192 x 2^-13 from k-slots 0..2 to the accumulator D: exact,
+    //       so I' is I_kb * 2^-26);
     //   s = dx[i] * dw[j] (the scale tile);
-    //   acc = fmaf(I, s, acc) on the VALU.
+    //   acc' = fmaf(I', s, acc') on the VALU.
     // The matrix pipe (3 x 32 cycles) rather than the VALU (16 x 4 cycles)
     // bounds a subtile-block; the convert-on-VALU form it replaces needed 32
     // VALU instructions (128 cycles).  Results are consumed right away (no
     // slot ring inside the wave, which keeps the kernel at <= 128 VGPRs and
     // 4 waves per SIMD): the SIMD's other waves cover the MFMA latency.
-    constexpr int NSUB = 2 * TM;
-    v16i magic;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) magic[r] = 0x4B400000;
-    const v2i cA = {lh ? 0 : 0xE800, 0}, cB = {lh ? 0 : 0x6E00, 0};  // f16 -2048, 6144 in slot 0
-    auto compute = [&](const Frag<TM> &f, int kb) {
+    constexpr int NSUB = TM * TN;
+    // f16 (-0.125, -1119/256, -387/8192, 0) x (1, 2^-7, 2^-13, 0) in k-slots
+    // 0..3, lanes 32..63 (slots 4..7) zero: the products sum to -c0
+    const v2i cA = {lh ? 0 : (int)0xC45FB000u, lh ? 0 : 0xAA0C};
+    const v2i cB = {lh ? 0 : 0x20003C00, lh ? 0 : 0x0800};
+    auto compute = [&](const Frag<TM, TN> &f, int kb) {
         const v16f zf = {};
         const v16i zi = {};
+        // c0's bits in every element: folded into the MFMA as its inline
+        // constant operand (a splat written at the use, so that it is)
+        const v16i magic = 0x3E22F983;
         if constexpr (EPI == EPI_DUMP_I) {
 #pragma unroll
             for (int k = 0; k < NSUB; ++k) {
-                const int a = k >> 1, b = k & 1;
+                const int a = k / TN, b = k % TN;
                 const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], zi, 0, 0, 0);
                 if (kb == (int)epi.dump_kb) {
 #pragma unroll
@@ -633,13 +662,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         } else {
 #pragma unroll
             for (int k = 0; k < NSUB; ++k) {
-                const int a = k >> 1, b = k & 1;
+                const int a = k / TN, b = k % TN;
                 const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], magic, 0, 0, 0);
                 const v16f I = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, cA),
                                                                     __builtin_bit_cast(v4h, cB),
                                                                     __builtin_bit_cast(v16f, D), 0, 0, 0);
-                const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.sx[a]),
-                                                                    __builtin_bit_cast(v4h, f.sw[b]), zf, 0, 0, 0);
+                const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sx_op(f, a)),
+                                                                    __builtin_bit_cast(v4h, sw_op(f, b)), zf, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = fmaf(I[r], S[r], acc[a][b][r]);
             }
@@ -649,24 +678,120 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         if constexpr (!C::LAT) __builtin_amdgcn_sched_barrier(0);
     };
 
-    // the zeros after each stage's W scales (never written by the DMA)
-    if (tid < NS * 64)
-        *reinterpret_cast<v4i *>(lds + (tid >> 6) * STAGE + WS + KS * BN * 2 + (tid & 63) * 16) =
-            v4i{0, 0, 0, 0};
-    float bias_v[2];
+    float bias_v[TN];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < TN; ++b) {
         const int n = n0 + wcol + b * 32;
         bias_v[b] = EPI != EPI_NONE && EPI != EPI_DUMP_I && n < N ? epi.bias[n] : 0.0f;
     }
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < TN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
+    // Latency form, software-pipelined over K blocks (each output's fma
+    // chain is the only serial dependency; a block's MFMAs depend on
+    // nothing of the block before).  Slot j of a stage: read block j + 1's
+    // fragments, issue block j's MFMAs (block dots, scale tiles, then the
+    // conversions, into ring entry j % 2) and run block j - 1's fmas from
+    // ring entry (j - 1) % 2, one MFMA per five VALU instructions, so that
+    // the wave's matrix pipe and VALU work side by side.  Block 3's fmas
+    // run in slot 0 of the next stage (after its barrier); the fmas stay in
+    // block order.
+    struct Ring {
+        v16f I[NSUB], S[NSUB];
+    };
+    auto mfma_group = [&](const Frag<TM, TN> &f, Ring &R) {
+        v16i D[NSUB];
+        const v16f zf = {};
+        const v16i magic = 0x3E22F983;
+#pragma unroll
+        for (int k = 0; k < NSUB; ++k)
+            D[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[k / TN], f.b[k % TN], magic, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NSUB; ++k)
+            R.S[k] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sx_op(f, k / TN)),
+                                                          __builtin_bit_cast(v4h, sw_op(f, k % TN)), zf, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NSUB; ++k)
+            R.I[k] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, cA), __builtin_bit_cast(v4h, cB),
+                                                          __builtin_bit_cast(v16f, D[k]), 0, 0, 0);
+    };
+    auto fma_group = [&](const Ring &R) {
+#pragma unroll
+        for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acc[k / TN][k % TN][r] = fmaf(R.I[k][r], R.S[k][r], acc[k / TN][k % TN][r]);
+    };
+    // the slot's order: fragment reads first, then MFMA / VALU alternating
+    auto slot_order = [&]() {
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 3 * NSUB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+    };
+    // NS - 1 stages in flight: the DMA instructions this wave issues per
+    // stage (a constant of its role), so that the wait for a stage lets
+    // the younger stages' instructions stay outstanding (loads complete in
+    // order)
+    auto k_loop_pipelined = [&](auto role) {
+        constexpr int ROLE = decltype(role)::value;
+        constexpr int DPS = C::QPX + C::QPW + (ROLE != 0 ? 1 : 0);
+        issue(0, role, All{}, std::true_type{});
+        static_for<NS - 1>([&](auto sc) { issue(1 + decltype(sc)::value, role, All{}, std::false_type{}); });
+        wait_vm<(NS - 1) * DPS>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // ring entry 1 starts at zero: the first stage's slot 0 runs its
+        // fmas as fmaf(0, 0, acc) = acc (acc is never -0)
+        Ring R[2];
+#pragma unroll
+        for (int k = 0; k < NSUB; ++k) R[1].I[k] = R[1].S[k] = v16f{};
+        Frag<TM, TN> Fs[2];
+        // every stage but the last: KS blocks, no branch
+        for (int g = 0; g < n_st - 1; ++g) {
+            const uint8_t *sb = lds + (g % NS) * STAGE;
+            load_frag(sb, 0, Fs[0]);
+            static_for<KS>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if constexpr (j + 1 < KS) load_frag(sb, j + 1, Fs[(j + 1) & 1]);
+                mfma_group(Fs[j & 1], R[j & 1]);
+                fma_group(R[(j + 1) & 1]);  // block j - 1 (slot 0: the previous stage's block 3)
+                slot_order();
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            // stage g + 1 landed (stages g + 2 .. g + NS - 1 may still be
+            // in flight), every wave past stage g: its buffer takes stage
+            // g + NS
+            wait_vm<(NS - 2) * DPS>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue(g + NS, role, All{}, std::false_type{});
+        }
+        // the last stage: the previous stage's block 3, then nb = 1 .. KS
+        // blocks one at a time, block kb0 + j in slot j + shift (a partial
+        // stage was fetched as the window of the last KS blocks)
+        fma_group(R[1]);
+        const uint8_t *sb = lds + ((n_st - 1) % NS) * STAGE;
+        const int kb0 = (n_st - 1) * KS, nb = KB - kb0, shift = kb0 - kpos(n_st - 1);
+        static_for<KS>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < nb) {
+                load_frag(sb, j + shift, Fs[0]);
+                mfma_group(Fs[0], R[0]);
+                fma_group(R[0]);
+            }
+        });
+    };
+
     auto k_loop = [&](auto role) {
+    if constexpr (C::LAT && EPI != EPI_DUMP_I) {
+        k_loop_pipelined(role);
+        return;
+    }
     issue(0, role, All{}, std::true_type{});
     arrive();  // the first stage visible
     if constexpr (C::LAT) issue(1, role, All{}, std::false_type{});
@@ -678,15 +803,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         const int kb0 = g * KS;
         if constexpr (C::LAT) {
             // every fragment of the stage first, then its blocks in order
-            Frag<TM> Fs[KS];
-            static_for<KS>([&](auto jc) {
-                constexpr int j = decltype(jc)::value;
-#pragma unroll
-                for (int a = 0; a < TM; ++a) Fs[j].sx[a] = v2i{0, 0};
-#pragma unroll
-                for (int b = 0; b < 2; ++b) Fs[j].sw[b] = v2i{0, 0};
-                load_frag(sb, j, Fs[j]);
-            });
+            Frag<TM, TN> Fs[KS];
+            static_for<KS>([&](auto jc) { load_frag(sb, decltype(jc)::value, Fs[decltype(jc)::value]); });
             static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value); });
         } else {
             // the next stage's DMA in three parts after blocks 0, 1 and 2:
@@ -726,6 +844,16 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     else
         k_loop(std::integral_constant<int, 0>{});
 
+    // acc = acc' * 2^26, exact
+    if constexpr (EPI != EPI_DUMP_I) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = acc[a][b][r] * 67108864.0f;
+    }
+
     // ----------------------------------------------------------------------
     // Epilogue.  The LDS is free scratch once the last (empty) stage's DMA
     // has landed and every wave has read its last fragments.
@@ -734,7 +862,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         wait_vm<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    epilogue<TM, EPI>(acc, bias_v, lane, m0 + wm * 32 * TM, n0 + wn * 64, M, N, y, ldy, epi,
+    epilogue<TM, TN, EPI>(acc, bias_v, lane, m0 + wm * 32 * TM, n0 + wn * 32 * TN, M, N, y, ldy, epi,
                       lds + wave * EPI_SCRATCH);
     // Every DMA this wave issued has landed before the workgroup ends.
     wait_vm<0>();
@@ -890,7 +1018,7 @@ __global__ __launch_bounds__(CfgH::NT) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[0][b][r] = acc_v[b][r];
     }
-    epilogue<1, EPI>(acc, bias_v, lane, m0 + wm * 32, n0 + wn * 64, M, N, y, ldy, epi,
+    epilogue<1, 2, EPI>(acc, bias_v, lane, m0 + wm * 32, n0 + wn * 64, M, N, y, ldy, epi,
                      lds + wave * EPI_SCRATCH);
     wait_vm<0>();
 }
@@ -986,12 +1114,27 @@ hipError_t launch_gemm_split_k(const WeightView &w, const int8_t *xq, const uint
 // form takes out from 19.8 to 14.6 us and fc2 from 58.7 to 42.5 us; rings
 // of 3 or 4 stages, 2-block stages and an imposed MFMA / VALU alternation
 // measured slower.
-using Wide = gemm::Cfg<4, 2>;
-using Small = gemm::Cfg<4, 2, 64, true>;
+#ifndef S2X_WIDE_TM
+#define S2X_WIDE_TM 1
+#endif
+using Wide = gemm::Cfg<4, 2, 128, false, S2X_WIDE_TM>;
+// The latency form's ring: four stages (three in flight) where its
+// workgroups fit one per CU, three stages (two per CU) otherwise.  Where
+// they fit one per CU, the plain / bias / residual epilogues (the out
+// projection and fc2) run 8 waves of 32 x 32 outputs per 64 x 128 tile
+// (Small4W): twice the waves, each with half the MFMA chain.
+using Small4 = gemm::Cfg<4, 4, 64, true>;
+using Small4W = gemm::Cfg<4, 4, 64, true, 1, 1>;
+using Small3 = gemm::Cfg<4, 3, 64, true>;
+
+template <int E>
+static hipError_t run_small(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                            int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream);
 
 static bool use_small(int64_t M, int64_t N) {
     return ((M + 127) / 128) * ((N + 127) / 128) < 2 * 256;
 }
+static bool small_ring4(int64_t M, int64_t N) { return ((M + 63) / 64) * ((N + 127) / 128) <= 256; }
 
 hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
                        int64_t M, float *y, int64_t ldy, const EpiParams &epi,
@@ -1007,8 +1150,8 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
         (epi.kb_split != 0 && (epi.kind != EPI_NONE || epi.kb_split < 0 || epi.y_split < M * ldy)))
         return hipErrorInvalidValue;
 #define S2X_RUN(E)                                                                    \
-    (use_small(M, w.N) ? gemm::run<Small, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
-                       : gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream))
+    (!use_small(M, w.N) ? gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
+                        : run_small<E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream))
     switch (epi.kind) {
     case EPI_NONE: return S2X_RUN(EPI_NONE);
     case EPI_BIAS: return S2X_RUN(EPI_BIAS);
@@ -1040,6 +1183,16 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
     default: return hipErrorInvalidValue;
     }
 #undef S2X_RUN
+}
+
+template <int E>
+static hipError_t run_small(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                            int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    constexpr bool plain = E == EPI_NONE || E == EPI_BIAS || E == EPI_BIAS_GELU || E == EPI_BIAS_RESID ||
+                           E == EPI_DUMP_I;
+    if (!small_ring4(M, w.N)) return gemm::run<Small3, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    if constexpr (plain) return gemm::run<Small4W, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    return gemm::run<Small4, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
 }
 
 hipError_t launch_gemm_f16(const _Float16 *w16, int64_t K_pad, int64_t N, const _Float16 *x16,

@@ -16,7 +16,10 @@ constexpr int64_t MAX_SEG_LEN = 4096;
 // Device view of a repacked Q8_0 weight (K_pad, N).
 struct WeightView {
     const int8_t *qs;     // N rows of K_pad int8 (16-byte aligned)
-    const uint16_t *dT;   // KB rows of ldT fp16 bits of d (transposed)
+    // KB rows of ldT fp16 bits of d (transposed); within each group of 64
+    // columns, column c + j (j < 32) sits at 2 j and c + 32 + j at 2 j + 1,
+    // so one 32-bit word holds the scales of columns j and j + 32
+    const uint16_t *dT;
     int64_t ldT;          // >= round_up(N, GEMM_BN)
     int64_t K_pad;        // multiple of 32
     int64_t N;

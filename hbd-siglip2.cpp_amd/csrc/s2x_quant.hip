@@ -74,8 +74,13 @@ hipError_t launch_quantize_q8_1(const float *x, int64_t K, int64_t M, int64_t ld
 // ---------------------------------------------------------------------------
 // a2: weight repack.  One thread per 34-byte block: the int8 qs go to a
 // 16-byte aligned row-major plane, d's fp16 bits to the transposed plane
-// dT [kb][n] (the GEMM's weight-scale layout).
+// dT [kb][dw_pos(n)] (the GEMM's weight-scale layout: in each group of 64
+// columns, columns j and j + 32 share a 32-bit word).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t dw_pos(int64_t n) {
+    return (n & ~(int64_t)63) | ((n & 31) << 1) | ((n >> 5) & 1);
+}
+
 __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__ raw,
                                                      int64_t n_blocks, int64_t KB,
                                                      int8_t *__restrict__ qs,
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *__restrict__
     if (i >= n_blocks) return;
     const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + i * 34);  // 2-byte aligned
     const int64_t n = i / KB, kb = i - n * KB;
-    dT[kb * ldT + n] = src[0];
+    dT[kb * ldT + dw_pos(n)] = src[0];
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = (uint32_t)src[1 + 2 * j] | ((uint32_t)src[2 + 2 * j] << 16);
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(256) void k_zero_pad_cols(uint16_t *__restrict__ dT
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t w = ldT - N;
     if (i >= KB * w) return;
-    dT[(i / w) * ldT + N + i % w] = 0;
+    dT[(i / w) * ldT + dw_pos(N + i % w)] = 0;
 }
 
 hipError_t launch_repack_q8_0(const void *raw, int64_t K_pad, int64_t N, int8_t *qs,

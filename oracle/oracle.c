@@ -355,6 +355,57 @@ float orc_gelu(float x) {
     return x / (1.0f + exp_cw(t));
 }
 
+/* src/cuda/siglip2_megakernel.cu:276-280: 0.5 x (1 + tanh(g)), same g */
+float orc_gelu_tanhf(float x) {
+    const float GELU_COEF_A = 0.044715f;
+    const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
+    return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+}
+
+/* ggml-cpu GGML_GELU_FP16: the table is built once, on first use */
+static uint16_t gelu_table[1 << 16];
+static int gelu_table_ready = 0;
+
+static void gelu_table_build(void) {
+#pragma omp critical(orc_gelu_table)
+    if (!gelu_table_ready) {
+        for (int i = 0; i < (1 << 16); ++i)
+            gelu_table[i] = orc_fp32_to_fp16(orc_gelu_tanhf(orc_fp16_to_fp32((uint16_t)i)));
+        __atomic_store_n(&gelu_table_ready, 1, __ATOMIC_RELEASE);
+    }
+}
+
+float orc_gelu_ggml(float x) {
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    if (!__atomic_load_n(&gelu_table_ready, __ATOMIC_ACQUIRE)) gelu_table_build();
+    return orc_fp16_to_fp32(gelu_table[orc_fp32_to_fp16(x)]);
+}
+
+static int gelu_mode = 0;
+
+int orc_set_gelu_mode(int mode) {
+    const int old = gelu_mode;
+    gelu_mode = mode;
+    return old;
+}
+
+void orc_gelu_array(int mode, const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        y[i] = mode == 2 ? orc_gelu_ggml(x[i]) : mode == 1 ? orc_gelu_tanhf(x[i]) : orc_gelu(x[i]);
+}
+
+/* the tower restatements' GELU, per orc_set_gelu_mode */
+static void gelu_n(float *u, int64_t n) {
+    if (gelu_mode == 2) {
+        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu_ggml(u[i]);
+    } else if (gelu_mode == 1) {
+        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu_tanhf(u[i]);
+    } else {
+        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu(u[i]);
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* attention                                                                 */
 /* ------------------------------------------------------------------------ */
@@ -630,7 +681,7 @@ void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
 
     orc_layernorm(x, n_pos, H, H, L->ln2_w, L->ln2_b, eps, h, H);
     linear(L->up_w, L->up_b, H, H, F, h, H, n_pos, u, nthreads);
-    for (int64_t i = 0; i < n_pos * F; ++i) u[i] = orc_gelu(u[i]);
+    gelu_n(u, n_pos * F);
     linear_down(L->down_w, L->down_b, F, F_pad, H, u, n_pos, o, down_f16, nthreads);
     for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
 
@@ -718,7 +769,7 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
         linear(m->ho_w, m->ho_b, H, H, H, t, H, 1, a, nthreads);
         orc_layernorm(a, 1, H, H, m->hln_w, m->hln_b, m->eps, a2, H);
         linear(m->hup_w, m->hup_b, H, H, F, a2, H, 1, u, nthreads);
-        for (int64_t i = 0; i < F; ++i) u[i] = orc_gelu(u[i]);
+        gelu_n(u, F);
         linear_down(m->hdown_w, m->hdown_b, F, F_pad, H, u, 1, a2, m->down_f16, nthreads);
         for (int64_t i = 0; i < H; ++i) out[i] = a[i] + a2[i];
         free(q);

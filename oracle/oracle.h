@@ -116,6 +116,27 @@ float orc_tanh_f32(float u);
  * reference's CUDA epilogue uses. */
 float orc_gelu(float x);
 
+/* The reference CUDA epilogue's own formula, 0.5 x (1 + tanhf(g))
+ * (src/cuda/siglip2_megakernel.cu:276-280), with the host libm's tanhf in
+ * place of CUDA's: the "exact fp32" mode, for measuring how far orc_gelu
+ * is from the formula as written. */
+float orc_gelu_tanhf(float x);
+
+/* ggml-cpu's default GELU (GGML_GELU_FP16) [ggml fork dbrain/ggml, commit
+ * not recorded; not in tree], restated from its published source: x <= -10
+ * gives 0, x >= 10 gives x, otherwise the fp16 table entry of fp16(x), the
+ * table holding fp16(ggml_gelu_f32(h)) for every fp16 h, ggml_gelu_f32 the
+ * tanhf form above.  The "ggml-faithful" mode. */
+float orc_gelu_ggml(float x);
+
+/* The GELU the tower restatements apply: 0 orc_gelu (default; the GPU's
+ * formulation, bit for bit), 1 orc_gelu_tanhf, 2 orc_gelu_ggml.  Process-
+ * wide; returns the previous mode. */
+int orc_set_gelu_mode(int mode);
+
+/* y[i] = the mode's GELU of x[i] (modes as orc_set_gelu_mode) */
+void orc_gelu_array(int mode, const float *x, float *y, int64_t n);
+
 /* ---- attention ------------------------------------------------------------ */
 /* softmax(Q K^T * scale [+ mask]) V for one image/sequence, all heads.
  * qkv: n_pos rows of 3*H floats laid out [q | k | v], head h at h*d_head

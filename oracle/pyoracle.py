@@ -64,6 +64,10 @@ def lib():
             "orc_mul_mat_f16_f32": ([_p, _i64, _i64, _p, _i64, _i64, _p, ctypes.c_int], None),
             "orc_layernorm": ([_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64], None),
             "orc_gelu": ([_f32], _f32),
+            "orc_gelu_tanhf": ([_f32], _f32),
+            "orc_gelu_ggml": ([_f32], _f32),
+            "orc_set_gelu_mode": ([ctypes.c_int], ctypes.c_int),
+            "orc_gelu_array": ([ctypes.c_int, _p, _p, _i64], None),
             "orc_tanh_f32": ([_f32], _f32),
             "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
             "orc_resize_pos_embed": ([_p, _i64, _i64, _i64, _i64, _p], None),
@@ -175,6 +179,24 @@ def gelu(x):
     f = lib().orc_gelu
     return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
                     np.float32).reshape(np.shape(x))
+
+
+GELU_EXACT, GELU_TANHF, GELU_GGML = 0, 1, 2
+
+
+def gelu_mode(mode, x):
+    """GELU of an array in one of the oracle's modes: GELU_EXACT (the GPU's
+    formulation), GELU_TANHF (the reference CUDA formula with libm tanhf),
+    GELU_GGML (ggml-cpu's fp16 table)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_gelu_array(mode, _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def set_gelu_mode(mode):
+    """The GELU the tower restatements use; returns the previous mode."""
+    return lib().orc_set_gelu_mode(mode)
 
 
 def tanh_f32(x):
