@@ -521,6 +521,24 @@ int s2x_attn_fp64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
     return e == hipSuccess ? S2X_OK : hip_fail(e, "attn_fp64 launch");
 }
 
+int s2x_attn_1q(const float *q, const float *k, const float *v, int64_t ld,
+                const int32_t *seg_start_dev, const int32_t *seg_len_dev, int64_t n_seg,
+                int64_t max_len, int64_t n_head, int64_t d_head, float scale, float *out,
+                void *stream) {
+    if (n_seg < 0 || max_len <= 0 || n_head <= 0 || d_head <= 0)
+        return fail(S2X_ERR_INVALID_ARG, "attn_1q: bad shape");
+    if (d_head > 128 || max_len > MAX_SEG_LEN || n_seg > 65535 || n_head > 65535)
+        return fail(S2X_ERR_UNSUPPORTED, "attn_1q: d_head <= 128, max_len <= %lld",
+                    (long long)MAX_SEG_LEN);
+    if (n_seg == 0) return S2X_OK;
+    if (!q || !k || !v || !seg_start_dev || !seg_len_dev || !out)
+        return fail(S2X_ERR_INVALID_ARG, "attn_1q: null pointer");
+    if (ld < n_head * d_head) return fail(S2X_ERR_INVALID_ARG, "attn_1q: ld < H");
+    hipError_t e = launch_attn_1q(q, k, v, ld, seg_start_dev, seg_len_dev, n_seg, n_head, d_head,
+                                  scale, out, (hipStream_t)stream);
+    return e == hipSuccess ? S2X_OK : hip_fail(e, "attn_1q launch");
+}
+
 // ---------------------------------------------------------------------------
 // a8 / a11
 // ---------------------------------------------------------------------------

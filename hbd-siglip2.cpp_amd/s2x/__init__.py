@@ -143,6 +143,7 @@ _sig("s2x_attn_run", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i6
 _sig("s2x_attn_run_q8_1", [_p, _sz, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i64, _p, _p, _i64,
                           _p, _i64, _p])
 _sig("s2x_attn_fp64", [_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _i64, _p])
+_sig("s2x_attn_1q", [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _p])
 _sig("s2x_resize_pos_embed", [_p, _i64, _i64, _i64, _i64, _p, _p])
 _sig("s2x_get_rows_q8_0", [_p, _i64, _i64, _p, _i64, _p, _i64, _p, _p])
 _sig("s2x_vision_create", [ctypes.POINTER(VisionWeights), ctypes.POINTER(_p)])

@@ -278,6 +278,19 @@ int s2x_attn_fp64(const float *qkv, int64_t ld_qkv, const float *qkv_bias,
                   int64_t n_head, int64_t d_head, float scale, float *out,
                   int64_t ld_out, void *stream);
 
+/* a9: the MAP probe head's attention, one query over each segment's keys
+ * (the pooling head's ggml_flash_attn_ext with a single query row,
+ * src/siglip2_vision.cpp:249-314): out[s*H + h*d_head + d] =
+ * sum_j softmax_j(f16(q_h) . f16(k_j,h) * scale) * f16(v_j,h)[d], over rows
+ * seg_start[s] .. seg_start[s] + seg_len[s] - 1 of k and v (row stride ld
+ * floats; H = n_head * d_head).  q: H floats shared by every segment.  The
+ * scores and softmax in f32, the PV sums in key-group partials.
+ * seg_len[s] <= max_len <= 4096, d_head <= 128. */
+int s2x_attn_1q(const float *q, const float *k, const float *v, int64_t ld,
+                const int32_t *seg_start_dev, const int32_t *seg_len_dev, int64_t n_seg,
+                int64_t max_len, int64_t n_head, int64_t d_head, float scale, float *out,
+                void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* a8  position-embedding resize (replaces ggml_interpolate(BILINEAR |       */
 /* ANTIALIAS) at src/siglip2_vision.cpp:680-690): anti-aliased bilinear,     */

@@ -410,6 +410,34 @@ static void gelu_n(float *u, int64_t n) {
 /* attention                                                                 */
 /* ------------------------------------------------------------------------ */
 
+/* Q, K, V rounded to fp16 as they enter flash attention (see orc_attention) */
+void orc_attention_1q(const float *q, const float *k, const float *v, int64_t ld,
+                      int64_t n_pos, int64_t n_head, int64_t d_head, float scale,
+                      float *out) {
+    double *s = (double *)malloc(sizeof(double) * (size_t)(n_pos > 0 ? n_pos : 1));
+    for (int64_t h = 0; h < n_head; ++h) {
+        double mx = -INFINITY;
+        for (int64_t j = 0; j < n_pos; ++j) {
+            double acc = 0.0;
+            for (int64_t d = 0; d < d_head; ++d)
+                acc += (double)fp16r(q[h * d_head + d]) * (double)fp16r(k[j * ld + h * d_head + d]);
+            s[j] = acc * (double)scale;
+            if (s[j] > mx) mx = s[j];
+        }
+        double den = 0.0;
+        for (int64_t j = 0; j < n_pos; ++j) {
+            s[j] = exp(s[j] - mx);
+            den += s[j];
+        }
+        for (int64_t d = 0; d < d_head; ++d) {
+            double acc = 0.0;
+            for (int64_t j = 0; j < n_pos; ++j) acc += s[j] * (double)fp16r(v[j * ld + h * d_head + d]);
+            out[h * d_head + d] = (float)(acc / den);
+        }
+    }
+    free(s);
+}
+
 void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
                    int64_t d_head, float scale, const uint8_t *key_valid,
                    float *out) {
@@ -737,35 +765,8 @@ void orc_vision_encode(const orc_vision_model *m, const float *pixels,
         linear(m->hq_w, m->hq_b, H, H, H, m->probe, H, 1, q, nthreads);
         linear(m->hk_w, m->hk_b, H, H, H, x, H, n_pos, k, nthreads);
         linear(m->hv_w, m->hv_b, H, H, H, x, H, n_pos, v, nthreads);
-        /* single-query attention over the n_pos keys; Q, K, V rounded to
-         * fp16 as they enter flash attention (see orc_attention) */
-        {
-            const int64_t nh = m->n_head;
-            for (int64_t h = 0; h < nh; ++h) {
-                double *s = (double *)malloc(sizeof(double) * (size_t)n_pos);
-                double mx = -INFINITY;
-                for (int64_t j = 0; j < n_pos; ++j) {
-                    double acc = 0.0;
-                    for (int64_t d = 0; d < d_head; ++d)
-                        acc += (double)fp16r(q[h * d_head + d]) *
-                               (double)fp16r(k[j * H + h * d_head + d]);
-                    s[j] = acc * (double)kq_scale;
-                    if (s[j] > mx) mx = s[j];
-                }
-                double den = 0.0;
-                for (int64_t j = 0; j < n_pos; ++j) {
-                    s[j] = exp(s[j] - mx);
-                    den += s[j];
-                }
-                for (int64_t d = 0; d < d_head; ++d) {
-                    double acc = 0.0;
-                    for (int64_t j = 0; j < n_pos; ++j)
-                        acc += s[j] * (double)fp16r(v[j * H + h * d_head + d]);
-                    t[h * d_head + d] = (float)(acc / den);
-                }
-                free(s);
-            }
-        }
+        /* single-query attention over the n_pos keys */
+        orc_attention_1q(q, k, v, H, n_pos, m->n_head, d_head, kq_scale, t);
         linear(m->ho_w, m->ho_b, H, H, H, t, H, 1, a, nthreads);
         orc_layernorm(a, 1, H, H, m->hln_w, m->hln_b, m->eps, a2, H);
         linear(m->hup_w, m->hup_b, H, H, F, a2, H, 1, u, nthreads);

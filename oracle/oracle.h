@@ -138,6 +138,14 @@ int orc_set_gelu_mode(int mode);
 void orc_gelu_array(int mode, const float *x, float *y, int64_t n);
 
 /* ---- attention ------------------------------------------------------------ */
+/* The MAP probe head's single-query attention (src/siglip2_vision.cpp:
+ * 249-314): for each head h, softmax_j(f16(q_h) . f16(k_j,h) * scale) .
+ * f16(v_j,h) over n_pos keys, in double (as orc_attention).  k, v: n_pos
+ * rows of stride ld floats, head h at h*d_head; out: H floats. */
+void orc_attention_1q(const float *q, const float *k, const float *v, int64_t ld,
+                      int64_t n_pos, int64_t n_head, int64_t d_head, float scale,
+                      float *out);
+
 /* softmax(Q K^T * scale [+ mask]) V for one image/sequence, all heads.
  * qkv: n_pos rows of 3*H floats laid out [q | k | v], head h at h*d_head
  * (src/siglip2_vision.cpp:201-206).  K and V are rounded to fp16 first, as

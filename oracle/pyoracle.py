@@ -70,6 +70,7 @@ def lib():
             "orc_gelu_array": ([ctypes.c_int, _p, _p, _i64], None),
             "orc_tanh_f32": ([_f32], _f32),
             "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
+            "orc_attention_1q": ([_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p], None),
             "orc_resize_pos_embed": ([_p, _i64, _i64, _i64, _i64, _p], None),
             "orc_nf_target_size": ([_i32, _i32, _i32, _i32, _p, _p], None),
             "orc_nf_preprocess_rgb": ([_p, _i32, _i32, _i32, _i32, _f32, _p, _p, ctypes.c_int,
@@ -203,6 +204,17 @@ def tanh_f32(x):
     f = lib().orc_tanh_f32
     return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()],
                     np.float32).reshape(np.shape(x))
+
+
+def attention_1q(q, k, v, n_head, d_head, scale):
+    """Single-query attention of q (H) over the rows of k and v ([n_pos, H])."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty(n_head * d_head, np.float32)
+    lib().orc_attention_1q(_ptr(q), _ptr(k), _ptr(v), k.shape[1], k.shape[0], n_head, d_head,
+                           scale, _ptr(out))
+    return out
 
 
 def attention(qkv, n_head, d_head, scale, key_valid=None):

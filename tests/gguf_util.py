@@ -7,7 +7,7 @@ import struct
 
 import numpy as np
 
-GT_U32, GT_F32, GT_STRING = 4, 6, 8
+GT_U32, GT_F32, GT_BOOL, GT_STRING, GT_ARRAY = 4, 6, 7, 8, 9
 T_F32, T_F16, T_Q8_0 = 0, 1, 8
 ALIGN = 32
 
@@ -17,31 +17,43 @@ def _str(s):
     return struct.pack("<Q", len(b)) + b
 
 
-def write_gguf(path, kv, tensors):
-    """kv: list of (key, gguf_type, value); tensors: list of (name, ggml_type,
-    ne (innermost first), bytes)."""
+def _value(t, v):
+    if t == GT_U32:
+        return struct.pack("<I", v)
+    if t == GT_F32:
+        return struct.pack("<f", v)
+    if t == GT_BOOL:
+        return struct.pack("<B", 1 if v else 0)
+    if t == GT_STRING:
+        return _str(v)
+    if t == GT_ARRAY:  # v = (element type, list of values)
+        et, items = v
+        return struct.pack("<IQ", et, len(items)) + b"".join(_value(et, x) for x in items)
+    raise ValueError(t)
+
+
+def write_gguf(path, kv, tensors, align=None):
+    """kv: list of (key, gguf_type, value), an array value being (element
+    type, items); tensors: list of (name, ggml_type, ne (innermost first),
+    bytes).  align: data alignment, written as general.alignment (u32) when
+    given (else the default 32, not written)."""
+    if align is not None:
+        kv = list(kv) + [("general.alignment", GT_U32, align)]
+    A = align or ALIGN
     head = bytearray(b"GGUF")
     head += struct.pack("<IQQ", 3, len(tensors), len(kv))
     for key, t, v in kv:
-        head += _str(key) + struct.pack("<I", t)
-        if t == GT_U32:
-            head += struct.pack("<I", v)
-        elif t == GT_F32:
-            head += struct.pack("<f", v)
-        elif t == GT_STRING:
-            head += _str(v)
-        else:
-            raise ValueError(t)
+        head += _str(key) + struct.pack("<I", t) + _value(t, v)
     offs, off = [], 0
     for name, t, ne, data in tensors:
         offs.append(off)
         off += len(data)
-        off = (off + ALIGN - 1) // ALIGN * ALIGN
+        off = (off + A - 1) // A * A
     for (name, t, ne, data), o in zip(tensors, offs):
         head += _str(name) + struct.pack("<I", len(ne))
         head += b"".join(struct.pack("<Q", e) for e in ne)
         head += struct.pack("<IQ", t, o)
-    pad = (-len(head)) % ALIGN
+    pad = (-len(head)) % A
     with open(path, "wb") as f:
         f.write(head)
         f.write(b"\0" * pad)

@@ -254,3 +254,76 @@ def test_names_match_reference_converter():
     every = set(ref["vision_tensors"]) | set(ref["text_tensors"]) | set(ref["metadata"])
     assert lit <= every, lit - every
     assert blk == set(ref["block_tensors"])
+
+
+def _converter_kv(vision_kv, text_kv, c_v, c_t):
+    """Metadata as the reference converter writes it for a file holding both
+    towers (scripts/convert_siglip2_to_gguf.py:306-353, keys and types from
+    tests/golden/converter_names.json), plus gguf-py's general.* keys and a
+    string array: bools, f32 arrays, strings and u32/f32 scalars."""
+    import json
+    import os
+    from gguf_util import GT_ARRAY, GT_BOOL
+    meta = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "converter_names.json")))["metadata"]
+    given = {k: (t, v) for k, t, v in list(vision_kv) + list(text_kv)}
+    kv = [("general.architecture", GT_STR_, "siglip2"), ("general.name", GT_STR_,
+          "siglip2-so400m-patch16-naflex"), ("general.type", GT_STR_, "model"),
+          ("general.file_type", GT_U32_, 7), ("general.quantization_version", GT_U32_, 2)]
+    extra = {"siglip2.has_vision": True, "siglip2.has_text": True,
+             "siglip2.vision.hidden_act": "gelu_pytorch_tanh", "siglip2.text.hidden_act": "gelu_pytorch_tanh",
+             "siglip2.preproc.default_max_num_patches": 256, "siglip2.preproc.rescale_factor": 1 / 255,
+             "siglip2.preproc.image_mean": [0.5, 0.5, 0.5], "siglip2.preproc.image_std": [0.5, 0.5, 0.5]}
+    code = {"bool": GT_BOOL, "uint32": GT_U32_, "float32": GT_F32_, "string": GT_STR_}
+    for key, typ in sorted(meta.items()):
+        if key in given:
+            t, v = given[key]
+            assert t == code[typ], key  # the writer's own keys carry the converter's types
+        elif typ == "array":
+            t, v = GT_ARRAY, (GT_F32_, extra[key])
+        else:
+            t, v = code[typ], extra[key]
+        kv.append((key, t, v))
+    kv.append(("tokenizer.ggml.tokens", GT_ARRAY, (GT_STR_, ["<pad>", "<eos>", "<bos>", "▁a"])))
+    return kv
+
+
+@pytest.mark.parametrize("align", [32, 64])
+def test_gguf_converter_shaped_file(tmp_path, align):
+    """A file shaped like the converter's output: both towers, every
+    metadata key the converter writes with its type (bools, f32 arrays,
+    strings), a string array, and general.alignment; both towers must come
+    back byte for byte."""
+    hv = synth.vision_model(SMALL_V, seed=41)
+    ht = synth.text_model(SMALL_T, seed=42)
+    kv_v, ts_v = vision_tensors(hv)
+    kv_t, ts_t = text_tensors(ht)
+    kv = _converter_kv(kv_v, kv_t, SMALL_V, SMALL_T)
+    path = tmp_path / "both.gguf"
+    write_gguf(path, kv, ts_v + ts_t, align=align)
+    st, g = _open(path)
+    assert st == 0, s2x.lib.s2x_last_error()
+    try:
+        w = s2x.VisionWeights()
+        s2x.call("s2x_gguf_vision_weights", g, ctypes.byref(w))
+        c = SMALL_V
+        H, F, Fp = c.hidden, c.inter, c.inter_pad
+        assert (w.hidden, w.n_layer, w.n_side) == (H, c.n_layer, c.n_side)
+        assert _bytes(w.patch_w, _q8_bytes(c.patch_dim, H)) == hv.tensors["patch_w"].tobytes()
+        assert _bytes(w.probe, 4 * H) == hv.tensors["probe"].tobytes()
+        _check_layers(w, hv, H, F, Fp)
+        tw = s2x.TextWeights()
+        s2x.call("s2x_gguf_text_weights", g, ctypes.byref(tw))
+        assert (tw.hidden, tw.n_layer, tw.vocab) == (SMALL_T.hidden, SMALL_T.n_layer, SMALL_T.vocab)
+        _check_layers(tw, ht, SMALL_T.hidden, SMALL_T.inter, SMALL_T.inter_pad)
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+
+
+def test_gguf_rejects_non_power_of_two_alignment(tmp_path):
+    hv = synth.vision_model(SMALL_V, seed=43)
+    kv, ts = vision_tensors(hv)
+    path = tmp_path / "bad_align.gguf"
+    write_gguf(path, kv + [("general.alignment", GT_U32_, 48)], ts)
+    st, g = _open(path)
+    assert st != 0 and "alignment" in s2x.lib.s2x_last_error().decode()

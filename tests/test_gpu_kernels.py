@@ -577,3 +577,43 @@ def test_get_rows_q8_0(orc):
     s2x.call("s2x_get_rows_q8_0", ptr(td), 1152, 500, ptr(idd), 70, ptr(pd), 35, ptr(out), stream())
     deq = orc.dequantize_q8_0(table, 500, 1152)
     assert np.array_equal(host(out), deq[ids] + pos[np.arange(70) % 35])
+
+
+# --------------------------------------------------- MAP head attention ----
+@pytest.mark.parametrize("lens", [[256], [729], [1024], [729, 1, 64, 130, 1024, 255, 576]],
+                         ids=["n256", "n729", "n1024", "ragged"])
+def test_attention_1q_vs_oracle(orc, lens):
+    """k_attn_1q (the probe head's one-query attention) through s2x_attn_1q,
+    keys and values in rows of stride 2H as the head's K/V GEMM writes them,
+    against the oracle's single-query attention (Q, K, V rounded to f16,
+    float64 softmax): within 1e-5 of max|out| per segment."""
+    n_head, dh = 16, 72
+    H = n_head * dh
+    rng = np.random.default_rng(sum(lens))
+    M = int(sum(lens))
+    q = rng.standard_normal(H).astype(np.float32)
+    kv = (rng.standard_normal((M, 2 * H)) * 1.5).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    L = np.asarray(lens, np.int32)
+    say(f"attn_1q: segments {lens}")
+    qd, kvd, sd, ld = dev(q), dev(kv), dev(starts), dev(L)
+    out = empty((len(lens), H), torch.float32)
+    scale = np.float32(1.0 / np.sqrt(np.float32(dh)))
+    kp = kvd.data_ptr()
+    s2x.call("s2x_attn_1q", ptr(qd), ctypes.c_void_p(kp), ctypes.c_void_p(kp + 4 * H), 2 * H, ptr(sd),
+             ptr(ld), len(lens), int(L.max()), n_head, dh, ctypes.c_float(scale), ptr(out), stream())
+    og = host(out)
+    for i, (s, n) in enumerate(zip(starts, L)):
+        ref = orc.attention_1q(q, kv[s:s + n, :H], kv[s:s + n, H:], n_head, dh, scale)
+        err = np.abs(og[i] - ref).max() / np.abs(ref).max()
+        assert err <= 1e-5, (i, n, err)
+
+
+def test_attention_1q_rejects_bad_arguments():
+    f = s2x.lib.s2x_attn_1q
+    t = empty((16,), torch.float32)
+    p = ptr(t)
+    assert f(p, p, p, 1152, p, p, 1, 4097, 16, 72, ctypes.c_float(0.1), p, stream()) != 0  # max_len
+    assert f(p, p, p, 1152, p, p, 1, 100, 4, 129, ctypes.c_float(0.1), p, stream()) != 0   # d_head
+    assert f(p, p, p, 1151, p, p, 1, 100, 16, 72, ctypes.c_float(0.1), p, stream()) != 0   # ld < H
+    assert f(p, p, p, 1152, p, p, 0, 100, 16, 72, ctypes.c_float(0.1), p, stream()) == 0   # no segments

@@ -362,3 +362,23 @@ def test_attention_single_key_returns_v(orc):
     qkv = np.random.default_rng(15).standard_normal((1, 3 * 72)).astype(np.float32)
     out = orc.attention(qkv, 1, 72, np.float32(0.3))
     assert np.array_equal(out[0], qkv[0, 144:].astype(np.float16).astype(np.float32))
+
+
+def test_attention_1q_float64_and_multi_query(orc):
+    """The MAP head's single-query attention: against the float64 softmax
+    reference, and equal to the multi-query restatement's row whose query it
+    is (keys and values taken from rows of stride ld = 2H, as the head lays
+    them out)."""
+    rng = np.random.default_rng(16)
+    n_head, dh, n = 4, 72, 300
+    H = n_head * dh
+    q = rng.standard_normal(H).astype(np.float32)
+    kv = (rng.standard_normal((n, 2 * H)) * 1.3).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(72))
+    out = orc.attention_1q(q, kv[:, :H], kv[:, H:], n_head, dh, scale)
+    qkv = np.concatenate([np.tile(q, (n, 1)), kv], axis=1)
+    assert np.abs(out - _attn_ref(qkv, n_head, dh, scale)[0]).max() < 1e-6
+    assert np.array_equal(out, orc.attention(qkv, n_head, dh, scale)[0])
+    # one key: the output is that key's f16 value row
+    one = orc.attention_1q(q, kv[:1, :H], kv[:1, H:], n_head, dh, scale)
+    assert np.array_equal(one, kv[0, H:].astype(np.float16).astype(np.float32))
