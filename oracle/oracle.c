@@ -7,6 +7,7 @@
  * appear only as explicit fmaf() calls.
  */
 #include "oracle.h"
+#include "cpu_q8.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -244,6 +245,47 @@ void orc_mul_mat_q8_0_q8_1(const void *w, int64_t K_pad, int64_t N,
     free(xd);
 }
 
+/* The CPU baseline's GEMM kernel (orc_set_gemm_kernel): 0 the loop above,
+ * 1 cpu_q8.c's VNNI kernel (the same bits) where the CPU has it, with each
+ * weight repacked on first use and kept (keyed by its address) */
+static int gemm_kernel = 0;
+#define ORC_WCACHE 512
+static struct {
+    const void *raw;
+    int64_t K_pad, N;
+    cq8_weight *w;
+} wcache[ORC_WCACHE];
+static int wcache_n = 0;
+
+int orc_set_gemm_kernel(int k) {
+    const int old = gemm_kernel;
+    gemm_kernel = k == 1 && cq8_have_vnni() ? 1 : 0;
+    return old;
+}
+
+void orc_clear_gemm_cache(void) {
+    for (int i = 0; i < wcache_n; ++i) cq8_free(wcache[i].w);
+    wcache_n = 0;
+}
+
+static cq8_weight *cached_weight(const void *w, int64_t K_pad, int64_t N) {
+    cq8_weight *r = NULL;
+#pragma omp critical(orc_wcache)
+    {
+        for (int i = 0; i < wcache_n && !r; ++i)
+            if (wcache[i].raw == w && wcache[i].K_pad == K_pad && wcache[i].N == N) r = wcache[i].w;
+        if (!r && wcache_n < ORC_WCACHE) {
+            r = cq8_prepare(w, K_pad, N);
+            wcache[wcache_n].raw = w;
+            wcache[wcache_n].K_pad = K_pad;
+            wcache[wcache_n].N = N;
+            wcache[wcache_n].w = r;
+            ++wcache_n;
+        }
+    }
+    return r;
+}
+
 void orc_mul_mat_q8_0_f32(const void *w, int64_t K_pad, int64_t N,
                           const float *x, int64_t K, int64_t ldx, int64_t M,
                           float *y, int nthreads) {
@@ -251,7 +293,11 @@ void orc_mul_mat_q8_0_f32(const void *w, int64_t K_pad, int64_t N,
     int8_t *qs = (int8_t *)malloc((size_t)(M * K_pad));
     uint16_t *ds = (uint16_t *)malloc(sizeof(uint16_t) * 2 * (size_t)(M * nb));
     orc_quantize_q8_1(x, M, K, ldx, K_pad, qs, ds);
-    orc_mul_mat_q8_0_q8_1(w, K_pad, N, qs, ds, M, y, nthreads);
+    cq8_weight *cw = gemm_kernel == 1 ? cached_weight(w, K_pad, N) : NULL;
+    if (cw)
+        cq8_mul_mat(cw, qs, ds, M, y, orc_threads(nthreads));
+    else
+        orc_mul_mat_q8_0_q8_1(w, K_pad, N, qs, ds, M, y, nthreads);
     free(qs);
     free(ds);
 }
@@ -397,13 +443,10 @@ void orc_gelu_array(int mode, const float *x, float *y, int64_t n) {
 
 /* the tower restatements' GELU, per orc_set_gelu_mode */
 static void gelu_n(float *u, int64_t n) {
-    if (gelu_mode == 2) {
-        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu_ggml(u[i]);
-    } else if (gelu_mode == 1) {
-        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu_tanhf(u[i]);
-    } else {
-        for (int64_t i = 0; i < n; ++i) u[i] = orc_gelu(u[i]);
-    }
+    const int mode = gelu_mode;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        u[i] = mode == 2 ? orc_gelu_ggml(u[i]) : mode == 1 ? orc_gelu_tanhf(u[i]) : orc_gelu(u[i]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -450,6 +493,11 @@ void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
             k16[p * H + i] = fp16r(qkv[p * 3 * H + H + i]);
             v16[p * H + i] = fp16r(qkv[p * 3 * H + 2 * H + i]);
         }
+    /* K per head as [d][key] (kt[(h * d_head + d) * n_pos + j]): each score
+     * is still summed over d in order, 8 keys side by side */
+    float *kt = (float *)malloc(sizeof(float) * (size_t)(n_pos * H));
+    for (int64_t p = 0; p < n_pos; ++p)
+        for (int64_t i = 0; i < H; ++i) kt[i * n_pos + p] = k16[p * H + i];
 #pragma omp parallel for schedule(static) collapse(2)
     for (int64_t h = 0; h < n_head; ++h) {
         for (int64_t i = 0; i < n_pos; ++i) {
@@ -458,13 +506,23 @@ void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
              * K vec-dot type [ggml, not in tree] */
             float q[512];
             for (int64_t d = 0; d < d_head && d < 512; ++d) q[d] = fp16r(qkv[i * 3 * H + h * d_head + d]);
+            for (int64_t j0 = 0; j0 < n_pos; j0 += 8) {
+                const int64_t nj = n_pos - j0 < 8 ? n_pos - j0 : 8;
+                double a8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for (int64_t d = 0; d < d_head; ++d) {
+                    const float *kr = kt + (h * d_head + d) * n_pos + j0;
+                    const double qd = (double)q[d];
+                    if (nj == 8) {
+                        for (int jj = 0; jj < 8; ++jj) a8[jj] += qd * (double)kr[jj];
+                    } else {
+                        for (int jj = 0; jj < nj; ++jj) a8[jj] += qd * (double)kr[jj];
+                    }
+                }
+                for (int jj = 0; jj < nj; ++jj) s[j0 + jj] = a8[jj] * (double)scale;
+            }
             double mx = -INFINITY;
             for (int64_t j = 0; j < n_pos; ++j) {
                 if (key_valid && !key_valid[j]) { s[j] = -INFINITY; continue; }
-                const float *k = k16 + j * H + h * d_head;
-                double acc = 0.0;
-                for (int64_t d = 0; d < d_head; ++d) acc += (double)q[d] * (double)k[d];
-                s[j] = acc * (double)scale;
                 if (s[j] > mx) mx = s[j];
             }
             double den = 0.0;
@@ -472,17 +530,22 @@ void orc_attention(const float *qkv, int64_t n_pos, int64_t n_head,
                 s[j] = (s[j] == -INFINITY) ? 0.0 : exp(s[j] - mx);
                 den += s[j];
             }
-            for (int64_t d = 0; d < d_head; ++d) {
-                double acc = 0.0;
-                for (int64_t j = 0; j < n_pos; ++j)
-                    if (s[j] != 0.0) acc += s[j] * (double)v16[j * H + h * d_head + d];
-                out[i * H + h * d_head + d] = (float)(acc / den);
+            /* each output's sum in key order (the d loop inside: the same
+             * sums, read along V's rows) */
+            double acc[512];
+            for (int64_t d = 0; d < d_head; ++d) acc[d] = 0.0;
+            for (int64_t j = 0; j < n_pos; ++j) {
+                if (s[j] == 0.0) continue;
+                const float *vr = v16 + j * H + h * d_head;
+                for (int64_t d = 0; d < d_head; ++d) acc[d] += s[j] * (double)vr[d];
             }
+            for (int64_t d = 0; d < d_head; ++d) out[i * H + h * d_head + d] = (float)(acc[d] / den);
             free(s);
         }
     }
     free(k16);
     free(v16);
+    free(kt);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -674,6 +737,7 @@ static void linear(const void *w, const float *bias, int64_t K, int64_t K_pad,
                    int nthreads) {
     orc_mul_mat_q8_0_f32(w, K_pad, N, x, K, ldx, M, y, nthreads);
     if (bias)
+#pragma omp parallel for schedule(static)
         for (int64_t m = 0; m < M; ++m)
             for (int64_t n = 0; n < N; ++n) y[m * N + n] = y[m * N + n] + bias[n];
 }
@@ -686,6 +750,7 @@ static void linear_down(const void *w, const float *bias, int64_t F, int64_t F_p
         return;
     }
     orc_mul_mat_f16_f32((const uint16_t *)w, F, N, x, F, M, y, nthreads);
+#pragma omp parallel for schedule(static)
     for (int64_t m = 0; m < M; ++m)
         for (int64_t n = 0; n < N; ++n) y[m * N + n] = y[m * N + n] + bias[n];
 }
@@ -705,12 +770,14 @@ void orc_encoder_block(const orc_layer *L, int32_t H, int32_t F, int32_t F_pad,
     linear(L->qkv_w, L->qkv_b, H, H, 3 * H, h, H, n_pos, qkv, nthreads);
     orc_attention(qkv, n_pos, n_head, d_head, kq_scale, key_valid, att);
     linear(L->o_w, L->o_b, H, H, H, att, H, n_pos, o, nthreads);
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
 
     orc_layernorm(x, n_pos, H, H, L->ln2_w, L->ln2_b, eps, h, H);
     linear(L->up_w, L->up_b, H, H, F, h, H, n_pos, u, nthreads);
     gelu_n(u, n_pos * F);
     linear_down(L->down_w, L->down_b, F, F_pad, H, u, n_pos, o, down_f16, nthreads);
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n_pos * H; ++i) x[i] = o[i] + x[i];
 
     free(h);

@@ -137,6 +137,14 @@ int orc_set_gelu_mode(int mode);
 /* y[i] = the mode's GELU of x[i] (modes as orc_set_gelu_mode) */
 void orc_gelu_array(int mode, const float *x, float *y, int64_t n);
 
+/* The GEMM kernel of orc_mul_mat_q8_0_f32 (and so of the towers): 0 the
+ * scalar loop of orc_mul_mat_q8_0_q8_1 (default), 1 the AVX-512 VNNI kernel
+ * of cpu_q8.c where the CPU has it (the same bits; for the CPU baseline).
+ * Returns the previous kernel.  orc_clear_gemm_cache frees the repacked
+ * weights kernel 1 keeps per weight address. */
+int orc_set_gemm_kernel(int k);
+void orc_clear_gemm_cache(void);
+
 /* ---- attention ------------------------------------------------------------ */
 /* The MAP probe head's single-query attention (src/siglip2_vision.cpp:
  * 249-314): for each head h, softmax_j(f16(q_h) . f16(k_j,h) * scale) .

@@ -68,6 +68,9 @@ def lib():
             "orc_gelu_ggml": ([_f32], _f32),
             "orc_set_gelu_mode": ([ctypes.c_int], ctypes.c_int),
             "orc_gelu_array": ([ctypes.c_int, _p, _p, _i64], None),
+            "orc_set_gemm_kernel": ([ctypes.c_int], ctypes.c_int),
+            "orc_clear_gemm_cache": ([], None),
+            "cq8_have_vnni": ([], ctypes.c_int),
             "orc_tanh_f32": ([_f32], _f32),
             "orc_attention": ([_p, _i64, _i64, _i64, _f32, _p, _p], None),
             "orc_attention_1q": ([_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p], None),
@@ -193,6 +196,17 @@ def gelu_mode(mode, x):
     y = np.empty_like(x)
     lib().orc_gelu_array(mode, _ptr(x), _ptr(y), x.size)
     return y
+
+
+def set_gemm_kernel(k):
+    """The towers' GEMM kernel: 0 the scalar restatement (default), 1 the
+    AVX-512 VNNI kernel of cpu_q8.c (same bits) where the CPU has it.
+    Returns the previous kernel."""
+    return lib().orc_set_gemm_kernel(k)
+
+
+def have_vnni():
+    return bool(lib().cq8_have_vnni())
 
 
 def set_gelu_mode(mode):
