@@ -210,16 +210,39 @@ __device__ __forceinline__ float tanh_f32(float u) {
     return __builtin_copysignf(r, u);
 }
 
-// GELU tanh form: the reference's inner argument
+// x / y correctly rounded, for the operands of gelu_tanh only: y = 1 + e with
+// e in [0, e^87] (y in [1, 2^126): 1 / y is normal), and y = 2 exactly
+// whenever |x| < 2^-25.  Markstein's division (P. Markstein, IA-64 and
+// Elementary Functions, 2000, ch. 8): v_rcp_f32 (within 1 ulp of 1 / y),
+// one Newton step r1 = r0 + r0 (1 - y r0), the quotient q0 = x r1 and its
+// correction by the exact remainder x - y q0.  Outside this domain it can
+// miss the rounding: y with an all-ones significand (when v_rcp_f32 returns
+// the lower neighbour of 1 / y, the Newton step stays there), or a remainder
+// below the normal range (|x| < 2^-100 with y not a power of two).  Every
+// float x in [-2^10, -2^7) and with 2^-30 <= |x| < 2^7 was checked against
+// the IEEE quotient through gelu_tanh itself; below 2^-30 y is 2, above 2^7
+// it is 1 or the constant of the clamp.  Six VALU operations where the
+// general IEEE division takes ten.
+__device__ __forceinline__ float div_gelu(float x, float y) {
+    const float r0 = __builtin_amdgcn_rcpf(y);
+    const float r1 = fmaf(fmaf(-y, r0, 1.0f), r0, r0);
+    const float q0 = x * r1;
+    return fmaf(fmaf(-y, q0, x), r1, q0);
+}
+
+// GELU tanh form: the reference's inner argument g
 // (src/cuda/siglip2_megakernel.cu:276-280) through 0.5 x (1 + tanh(g)) =
-// x / (1 + e^(-2g)) -- one exp_cw, one IEEE division, no branch; the same
-// operations as the CPU restatement, so the bits agree.
+// x / (1 + e^(-2g)) -- one exp_cw, one division, no branch; the same
+// operations as the CPU restatement, so the bits agree.  t = -2 g is
+// formed as ((-2 sqrt(2/pi)) x) (1 + a x x): scaling by -2 commutes with
+// each rounding, so these are the bits of -2 * g.  The clamp's upper end,
+// 87, keeps 1 + e^t below 2^126 (the domain of div_gelu); e^-17 is already
+// below half an ulp of 1, so the lower end (-100) changes nothing.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
-    const float g = SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x);
-    const float t = fminf(fmaxf(-2.0f * g, -100.0f), 100.0f);
-    return x / (1.0f + exp_cw(t));
+    const float t = ((-2.0f * SQRT_2_OVER_PI) * x) * (1.0f + GELU_COEF_A * x * x);
+    return div_gelu(x, 1.0f + exp_cw(fminf(fmaxf(t, -100.0f), 87.0f)));
 }
 
 // a / b for 0 <= a < 2^20 and b >= 1, exact: the float estimate a * (1/b)

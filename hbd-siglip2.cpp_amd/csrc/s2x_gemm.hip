@@ -168,9 +168,11 @@ struct Frag {
 // Epilogue of one wave's 32 TM x 32 TN block (rows mw.., columns nw..), from
 // the accumulators in registers; wscr: 5,120 bytes of LDS of this wave.
 // The GELU -> Q8_1 / f16 and QKV epilogues take 32 x 64 blocks (TN = 2).
+// The product is acc * scale (a power of two: exact), so that mm + bias is
+// one fmaf(acc, scale, bias), the same bits as (acc * scale) + bias.
 constexpr int EPI_SCRATCH = 5120;
 template <int TM, int TN, int EPI>
-__device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (&bias_v)[TN], int lane,
+__device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], float scale, const float (&bias_v)[TN], int lane,
                                          int mw, int nw, int M, int N, float *__restrict__ y,
                                          int64_t ldy, const EpiParams &epi, uint8_t *wscr) {
     static_assert(TN == 2 || EPI == EPI_NONE || EPI == EPI_BIAS || EPI == EPI_BIAS_GELU ||
@@ -181,7 +183,10 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
         // GELU(mm + bias), then Q8_1 exactly as k_quantize_q8_1 over
         // rows of q_kpad values (columns >= N are zeros): each 32 x 32
         // subtile is one quant block per row; it goes through LDS so that
-        // lane pairs own a row (16 values each)
+        // lane pairs own a row (16 values each).  Columns >= N need no
+        // branch: their W quants arrive as zeros (rows past N) and their
+        // W scales are the zeroed padding of the dT plane, so acc is +0,
+        // the bias 0, and GELU(+0) = +0.
         constexpr int P = 36;  // floats per scratch row
         float *scr = reinterpret_cast<float *>(wscr);
         const int row = lane >> 1, half = lane & 1;
@@ -191,11 +196,10 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
             for (int b = 0; b < 2; ++b) {
                 const int nb0 = nw + b * 32;  // first column of this quant block
                 if (nb0 >= epi.q_kpad) continue;  // wave-uniform
-                const int n = nb0 + lr;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + lr] =
-                        n < N ? gelu_tanh(acc[a][b][r] + bias_v[b]) : 0.0f;
+                        gelu_tanh(fmaf(acc[a][b][r], scale, bias_v[b]));
                 float v[16];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -246,7 +250,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
                     const int m = mw + a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     if (m < M)
                         epi.h_out[(int64_t)m * epi.h_ld + n] =
-                            n < N ? f32_to_f16(gelu_tanh(acc[a][b][r] + bias_v[b])) : (_Float16)0.0f;
+                            n < N ? f32_to_f16(gelu_tanh(fmaf(acc[a][b][r], scale, bias_v[b]))) : (_Float16)0.0f;
                 }
             }
     } else if constexpr (EPI == EPI_QKV) {
@@ -273,7 +277,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
                         scr[(8 * (r >> 2) + 4 * lh + (r & 3)) * P + b * 32 + lr] =
-                            f32_to_f16(acc[a][b][r] + bias_v[b]);
+                            f32_to_f16(fmaf(acc[a][b][r], scale, bias_v[b]));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int id = lane + 64 * i, row = id >> 3, c = (id & 7) * 8;
@@ -322,7 +326,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             scr[(b * 32 + lr) * PT + shift + 8 * q + 4 * lh + j] =
-                                f32_to_f16(acc[a][b][4 * q + j] + bias_v[b]);
+                                f32_to_f16(fmaf(acc[a][b][4 * q + j], scale, bias_v[b]));
                 if (rows > 0 && n < N) {
                     const _Float16 *col = scr + lane * PT;
                     if (run) {
@@ -371,7 +375,7 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
                         const int pos = rm & 0xffff;
                         const int64_t off = part < 2 ? (sh * epi.len_pad + pos) * epi.d_pad + d
                                                      : (sh * epi.dv_pad + d) * epi.len_pad + pos;
-                        dst[off] = f32_to_f16(acc[a][b][r] + bias_v[b]);
+                        dst[off] = f32_to_f16(fmaf(acc[a][b][r], scale, bias_v[b]));
                     }
             }
         }
@@ -422,13 +426,15 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], const float (
                 const int n = nw + b * 32 + lr;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float v = acc[a][b][r];
-                    if (EPI == EPI_BIAS) {
-                        v = v + bias_v[b];
+                    float v = acc[a][b][r];  // EPI_DUMP_I: the raw bits
+                    if (EPI == EPI_NONE) {
+                        v = v * scale;
+                    } else if (EPI == EPI_BIAS) {
+                        v = fmaf(v, scale, bias_v[b]);
                     } else if (EPI == EPI_BIAS_GELU) {
-                        v = gelu_tanh(v + bias_v[b]);
+                        v = gelu_tanh(fmaf(v, scale, bias_v[b]));
                     } else if (EPI == EPI_BIAS_RESID) {
-                        v = (v + bias_v[b]) + res[b][r];
+                        v = fmaf(v, scale, bias_v[b]) + res[b][r];
                     }
                     const int mr = a * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     const uint32_t off = n < N ? (uint32_t)(mr * (int)ldy + n) * 4u : OOB;
@@ -844,16 +850,6 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     else
         k_loop(std::integral_constant<int, 0>{});
 
-    // acc = acc' * 2^26, exact
-    if constexpr (EPI != EPI_DUMP_I) {
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][b][r] = acc[a][b][r] * 67108864.0f;
-    }
-
     // ----------------------------------------------------------------------
     // Epilogue.  The LDS is free scratch once the last (empty) stage's DMA
     // has landed and every wave has read its last fragments.
@@ -862,7 +858,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
         wait_vm<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    epilogue<TM, TN, EPI>(acc, bias_v, lane, m0 + wm * 32 * TM, n0 + wn * 32 * TN, M, N, y, ldy, epi,
+    // acc = acc' * 2^26 (exact), folded into the epilogue's first operation
+    epilogue<TM, TN, EPI>(acc, 67108864.0f, bias_v, lane, m0 + wm * 32 * TM, n0 + wn * 32 * TN, M, N, y, ldy, epi,
                       lds + wave * EPI_SCRATCH);
     // Every DMA this wave issued has landed before the workgroup ends.
     wait_vm<0>();
@@ -1018,7 +1015,7 @@ __global__ __launch_bounds__(CfgH::NT) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[0][b][r] = acc_v[b][r];
     }
-    epilogue<1, 2, EPI>(acc, bias_v, lane, m0 + wm * 32, n0 + wn * 64, M, N, y, ldy, epi,
+    epilogue<1, 2, EPI>(acc, 1.0f, bias_v, lane, m0 + wm * 32, n0 + wn * 64, M, N, y, ldy, epi,
                      lds + wave * EPI_SCRATCH);
     wait_vm<0>();
 }

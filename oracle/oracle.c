@@ -397,7 +397,8 @@ float orc_gelu(float x) {
     const float GELU_COEF_A = 0.044715f;
     const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
     const float g = SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x);
-    const float t = fminf(fmaxf(-2.0f * g, -100.0f), 100.0f);
+    /* the upper clamp keeps 1 + e^t below 2^126 */
+    const float t = fminf(fmaxf(-2.0f * g, -100.0f), 87.0f);
     return x / (1.0f + exp_cw(t));
 }
 
@@ -437,6 +438,7 @@ int orc_set_gelu_mode(int mode) {
 }
 
 void orc_gelu_array(int mode, const float *x, float *y, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > 65536)
     for (int64_t i = 0; i < n; ++i)
         y[i] = mode == 2 ? orc_gelu_ggml(x[i]) : mode == 1 ? orc_gelu_tanhf(x[i]) : orc_gelu(x[i]);
 }

@@ -386,6 +386,40 @@ def test_standalone_epilogues(orc):
     assert_same(host(y), orc.gelu(mm + b), "bias_gelu")
 
 
+# Every float whose GELU goes through a division by y = 1 + e^t other than
+# y = 2 (|x| < 2^-30) or y = 1 (x >= 2^7), plus a stretch of the clamped
+# y = 1 + e^87: [2^-30, 2^7), its negatives and [-2^10, -2^7).
+GELU_RANGES = [(0x30800000, 0x43000000), (0xB0800000, 0xC3000000), (0xC3000000, 0xC4800000)]
+
+
+def test_gelu_every_float_in_the_division_domain(orc):
+    """The GPU GELU (its division is Markstein's, on v_rcp_f32) equals the
+    oracle's (an IEEE division) bit for bit on 645 M floats: all of them
+    in the ranges where the quotient is not a division by 1 or 2."""
+    chunk = 1 << 25
+    zero = zeros((1,), torch.float32)
+    y = empty((chunk,), torch.float32)
+    total = bad = 0
+    for lo, hi in GELU_RANGES:
+        for a in range(lo, hi, chunk):
+            b = min(a + chunk, hi)
+            x = np.arange(a, b, dtype=np.uint32).view(np.float32)
+            xd = dev(x)
+            s2x.call("s2x_bias_gelu", ptr(xd), ptr(zero), ptr(y), 1, b - a, stream())
+            got = host(y[:b - a]).view(np.uint32)
+            ref = orc.gelu_mode(orc.GELU_EXACT, x).view(np.uint32)
+            miss = np.flatnonzero(got != ref)
+            if len(miss):
+                say(f"gelu: {len(miss)} of {b - a} differ from 0x{a:08x}; first "
+                    f"x={x[miss[0]]!r} got 0x{got[miss[0]]:08x} ref 0x{ref[miss[0]]:08x}")
+            total += b - a
+            bad += len(miss)
+            del xd
+    say(f"gelu: {total} floats, {bad} differ")
+    assert total == sum(hi - lo for lo, hi in GELU_RANGES) == 645_922_816
+    assert bad == 0
+
+
 def _attn_case(orc, lens, n_head=16, dh=72, key_valid=None, seed=10):
     H = n_head * dh
     rng = np.random.default_rng(seed)
