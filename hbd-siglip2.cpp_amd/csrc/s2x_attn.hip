@@ -301,7 +301,8 @@ __global__ __launch_bounds__(256) void k_quant_straddle(const float *__restrict_
     const int64_t kb = 9 * (i / 3) + 2 + 2 * (i % 3);
     const int64_t c = kb * QK + sub * 4;
     const float4 t = *reinterpret_cast<const float4 *>(x + m * ldx + c);
-    float a = fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w)));
+    // from 0, as a running fmaxf: NaNs are passed over, a block of NaNs has amax 0
+    float a = fmaxf(fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))), 0.0f);
     a = group8_max(a);
     const float d = a / 127.0f;
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;

@@ -86,6 +86,11 @@ __device__ __forceinline__ float group8_max(float v) {
     v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
     return fmaxf(v, dpp_f<0x141>(v));
 }
+__device__ __forceinline__ uint32_t group8_umax(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0xb1>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x4e>((int)v));
+    return max(v, (uint32_t)dpp_i<0x141>((int)v));
+}
 __device__ __forceinline__ int group8_isum(int v) {
     v = v + dpp_i<0xb1>(v);
     v = v + dpp_i<0x4e>(v);
@@ -157,6 +162,34 @@ __device__ __forceinline__ int q8_round_fast(float x, float inv) {
 }
 __device__ __forceinline__ bool q8_any_sat(float inv) {
     return __builtin_amdgcn_ballot_w64(!(inv <= 3.40282347e38f)) != 0;
+}
+
+// The block scales d = a / 127 and inv = 127 / a (0 for a = 0) of a block
+// amax a >= 0, equal to the IEEE quotients bit for bit where q8_scales_ok(a)
+// holds (a = 0 or 2^-100 <= a <= 2^100), in about half the VALU operations
+// of two IEEE divisions.  Markstein's division (P. Markstein, IA-64 and
+// Elementary Functions, 2000, ch. 8):
+//   d:   q0 = a RN(1/127), corrected by the exact remainder a - 127 q0 --
+//        a / 127 for every positive float a;
+//   inv: r0 = v_rcp_f32(a) (within 1 ulp of 1 / a), the quotient p0 =
+//        127 r0 corrected by its exact remainder 127 - a p0 -- 127 / a for
+//        every significand of a and either float next to 1 / a as r0 (with
+//        the numerator fixed at 127 the correction needs no Newton step on
+//        r0); every step scales exactly by a power of two while its values
+//        stay normal, which holds for a in [2^-121, 2^126].
+// Both were checked over those inputs on the CPU
+// (tests/test_q8_scales_division.py).
+__device__ __forceinline__ bool q8_scales_ok(float a) {
+    return a == 0.0f || (a >= 0x1p-100f && a <= 0x1p100f);
+}
+__device__ __forceinline__ void q8_scales(float a, float &d, float &inv) {
+    const float r127 = 0x1.020408p-7f;  // RN(1/127)
+    const float q0 = a * r127;
+    d = fmaf(fmaf(-127.0f, q0, a), r127, q0);
+    const float r0 = __builtin_amdgcn_rcpf(a);
+    const float p0 = 127.0f * r0;
+    const float p = fmaf(fmaf(-a, p0, 127.0f), r0, p0);
+    inv = a != 0.0f ? p : 0.0f;
 }
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {

@@ -67,8 +67,8 @@ constexpr int BN = 128;  // output tile columns
 constexpr int GM = 8;    // tile-row group of the tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
-// BM x 128 tiles (BM 128 or 64), BM / 16 waves of 32 x 64 outputs (BM / 32
-// along M, 2 along N); stages of KS K blocks in a ring of NS stage buffers
+// BM x 128 tiles (BM 128, 64 or 32), waves of 32 TM x 32 TN outputs (BM /
+// 32 TM along M, 128 / 32 TN along N); stages of KS K blocks in a ring of NS stage buffers
 // (NS - 1 stages in flight).  Throughput form (LAT false): as many
 // workgroups per CU as two rings allow, each K block its own scheduling
 // region, <= 128 VGPRs (4 waves per SIMD cover each other's latency).
@@ -84,8 +84,11 @@ struct Cfg {
     static constexpr int WN = BN / (32 * TN), NWAVE = BM / (32 * TM) * WN, NT = NWAVE * WAVE;
     static constexpr int XQ = 0;                  // [KS][BM][32] X quants
     static constexpr int WQ = XQ + KS * BM * 32;  // [KS][BN][32] W quants
-    static constexpr int XS = WQ + KS * BN * 32;  // [BM][KS] u32 X ds words
-    static constexpr int WS = XS + KS * BM * 4;   // [KS][BN] fp16 W scales
+    // [XS_ROWS][KS] u32 X ds words: at least 64 rows, the rows one X-scale
+    // DMA instruction writes (rows past a 32-row tile are never read)
+    static constexpr int XS_ROWS = BM < 64 ? 64 : BM;
+    static constexpr int XS = WQ + KS * BN * 32;
+    static constexpr int WS = XS + KS * XS_ROWS * 4;  // [KS][BN] fp16 W scales
     static constexpr int STAGE = WS + KS * BN * 2;
     static constexpr int LDS_BYTES = NS * STAGE;
     static constexpr int WG_PER_CU = 2 * LDS_BYTES <= 163840 ? 2 : 1;
@@ -97,10 +100,10 @@ struct Cfg {
     // of 64 rows each, wave NSX the W scales.  The issue cost of these
     // instructions, not their bytes, is what the K loop feels, hence the
     // scales in as few of them as their 16-byte rows allow.
-    static constexpr int NSX = BM / 64;
+    static constexpr int NSX = BM < 64 ? 1 : BM / 64;
     static constexpr int QPX = KS * (BM / 32) / NWAVE, QPW = KS * (BN / 32) / NWAVE;
     static_assert(KS == 4, "stage of 4 blocks: one 16-byte ds row per X row");
-    static_assert(BM == 128 || BM == 64, "tile rows");
+    static_assert(BM == 128 || BM == 64 || (BM == 32 && LAT && TN == 1), "tile rows");
     static_assert(QPX >= 1 && QPW >= 1 && QPX <= KS && QPW <= KS, "DMA split");
     static_assert(NS == 2 || (LAT && NS <= 4), "ring: two stages, or up to four in the latency form");
     static_assert(NSX + 1 <= NWAVE, "scale DMA waves");
@@ -1119,9 +1122,13 @@ using Wide = gemm::Cfg<4, 2, 128, false, S2X_WIDE_TM>;
 // workgroups fit one per CU, three stages (two per CU) otherwise.  Where
 // they fit one per CU, the plain / bias / residual epilogues (the out
 // projection and fc2) run 8 waves of 32 x 32 outputs per 64 x 128 tile
-// (Small4W): twice the waves, each with half the MFMA chain.
+// (Small4W): twice the waves, each with half the MFMA chain.  Where even
+// those tiles number fewer than the CUs (out and fc2 at M = 729: 108 of
+// them), 32 x 128 tiles of 4 such waves (Small4T) spread the rows over
+// twice the workgroups: the same per-output K order, without splitting K.
 using Small4 = gemm::Cfg<4, 4, 64, true>;
 using Small4W = gemm::Cfg<4, 4, 64, true, 1, 1>;
+using Small4T = gemm::Cfg<4, 4, 32, true, 1, 1>;
 using Small3 = gemm::Cfg<4, 3, 64, true>;
 
 template <int E>
@@ -1132,6 +1139,7 @@ static bool use_small(int64_t M, int64_t N) {
     return ((M + 127) / 128) * ((N + 127) / 128) < 2 * 256;
 }
 static bool small_ring4(int64_t M, int64_t N) { return ((M + 63) / 64) * ((N + 127) / 128) <= 256; }
+static bool small_rows32(int64_t M, int64_t N) { return ((M + 63) / 64) * ((N + 127) / 128) < 256; }
 
 hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
                        int64_t M, float *y, int64_t ldy, const EpiParams &epi,
@@ -1188,7 +1196,10 @@ static hipError_t run_small(const WeightView &w, const int8_t *xq, const uint32_
     constexpr bool plain = E == EPI_NONE || E == EPI_BIAS || E == EPI_BIAS_GELU || E == EPI_BIAS_RESID ||
                            E == EPI_DUMP_I;
     if (!small_ring4(M, w.N)) return gemm::run<Small3, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
-    if constexpr (plain) return gemm::run<Small4W, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    if constexpr (plain) {
+        if (small_rows32(M, w.N)) return gemm::run<Small4T, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+        return gemm::run<Small4W, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    }
     return gemm::run<Small4, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
 }
 

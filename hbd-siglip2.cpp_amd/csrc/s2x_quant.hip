@@ -11,6 +11,8 @@
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
+#include <type_traits>
+
 namespace s2x {
 
 // ---------------------------------------------------------------------------
@@ -45,7 +47,8 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(
         v2 = c + 2 < K ? xr[c + 2] : 0.0f;
         v3 = c + 3 < K ? xr[c + 3] : 0.0f;
     }
-    float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    // from 0, as a running fmaxf: NaNs are passed over, a block of NaNs has amax 0
+    float a = fmaxf(fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3))), 0.0f);
     a = group8_max(a);
     const float d = a / 127.0f;
     const float inv = a != 0.0f ? 127.0f / a : 0.0f;
@@ -210,6 +213,15 @@ __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr,
 // barrier in front of the first row is most of a wave's time).  Each wave
 // walks rows row, row + 4 * gridDim.x, ... and loads its next row before
 // reducing the current one, so HBM reads overlap the reductions.
+// vec4: bit 0 x rows 16-byte aligned, bit 1 y rows, bit 2 w and b.
+// The Q8_1 blocks are quantized with q8_scales and the two-operation
+// rounding, then, in a wave where a block's amax fails q8_scales_ok, again
+// with the IEEE divisions and the saturating rounding, over the same bytes.
+// That amax is taken on the bit patterns of |x| (for non-negative floats
+// the integer order is the numeric one, and a NaN sorts above +inf), so a
+// block holding a NaN or an infinity fails too: where none does, every
+// value is finite and at most amax in magnitude, the two-operation
+// rounding's domain, and the amax equals fmaxf's.  The same bits either way.
 template <bool QUANT, bool WRITE_Y, int NIT, bool WREG>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
@@ -228,10 +240,17 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
+            if ((vec4 & 4) && c < H) {  // (H % 32 == 0: c + 3 < H)
+                const float4 tw = w ? *reinterpret_cast<const float4 *>(w + c) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+                const float4 tb = b ? *reinterpret_cast<const float4 *>(b + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                wr[it][0] = tw.x; wr[it][1] = tw.y; wr[it][2] = tw.z; wr[it][3] = tw.w;
+                br[it][0] = tb.x; br[it][1] = tb.y; br[it][2] = tb.z; br[it][3] = tb.w;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                wr[it][j] = w && c + j < H ? w[c + j] : 1.0f;
-                br[it][j] = b && c + j < H ? b[c + j] : 0.0f;
+                for (int j = 0; j < 4; ++j) {
+                    wr[it][j] = w && c + j < H ? w[c + j] : 1.0f;
+                    br[it][j] = b && c + j < H ? b[c + j] : 0.0f;
+                }
             }
         }
     } else {
@@ -272,9 +291,13 @@ __global__ __launch_bounds__(256) void k_layernorm(
         }
         const float var = (float)(wave_dsum(s2) / (double)H);
         const float scale = 1.0f / sqrtf(var + eps);
+        // every pass normalized first (o), then written; the quantization's
+        // form is chosen once per row
+        float o[NIT][4], am[NIT];
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
+            am[it] = 0.0f;
             if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
             float wa[4], ba[4];
             if constexpr (WREG) {
@@ -289,34 +312,63 @@ __global__ __launch_bounds__(256) void k_layernorm(
                 wa[0] = wv.x; wa[1] = wv.y; wa[2] = wv.z; wa[3] = wv.w;
                 ba[0] = bv.x; ba[1] = bv.y; ba[2] = bv.z; ba[3] = bv.w;
             }
-            float o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float t = (v[it][j] - mean) * scale;
                 if (w) t = t * wa[j];
                 if (b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
-                o[j] = t;
+                o[it][j] = t;
             }
             if (WRITE_Y) {
                 float *yr = y + row * ldy + c;
                 if (vec4 & 2) {
-                    *reinterpret_cast<float4 *>(yr) = make_float4(o[0], o[1], o[2], o[3]);
+                    *reinterpret_cast<float4 *>(yr) = make_float4(o[it][0], o[it][1], o[it][2], o[it][3]);
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) yr[j] = o[j];
+                    for (int j = 0; j < 4; ++j) yr[j] = o[it][j];
                 }
             }
             if (QUANT) {
-                float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-                a = group8_max(a);
-                const float d = a / 127.0f;
-                const float inv = a != 0.0f ? 127.0f / a : 0.0f;
-                const int q0 = q8_round(o[0], inv), q1 = q8_round(o[1], inv);
-                const int q2 = q8_round(o[2], inv), q3 = q8_round(o[3], inv);
-                *reinterpret_cast<uint32_t *>(q.qs + row * H + c) = pack4_i8(q0, q1, q2, q3);
-                const int sq = group8_isum(q0 + q1 + q2 + q3);
-                if ((lane & 7) == 0) store_scales(q, row, c / QK, q.ld_ds, d, sq);
+                uint32_t ab = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ab = max(ab, __builtin_bit_cast(uint32_t, o[it][j]) & 0x7fffffffu);
+                am[it] = __builtin_bit_cast(float, group8_umax(ab));
             }
+        }
+        if constexpr (QUANT) {
+            bool fast = true;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) fast = fast && q8_scales_ok(am[it]);
+            const auto quantize = [&](auto fast_c) {
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const int64_t c = (int64_t)it * 256 + lane * 4;
+                    if (c >= H) continue;
+                    float d, inv;
+                    int qv[4];
+                    if constexpr (decltype(fast_c)::value) {
+                        q8_scales(am[it], d, inv);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) qv[j] = q8_round_fast(o[it][j], inv);
+                    } else {
+                        // the amax as a running fmaxf from 0 takes it (a NaN
+                        // is passed over; a block of NaNs has amax 0)
+                        float a = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) a = fmaxf(a, fabsf(o[it][j]));
+                        a = group8_max(a);
+                        d = a / 127.0f;
+                        inv = a != 0.0f ? 127.0f / a : 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) qv[j] = q8_round(o[it][j], inv);
+                    }
+                    *reinterpret_cast<uint32_t *>(q.qs + row * H + c) = pack4_i8(qv[0], qv[1], qv[2], qv[3]);
+                    const int sq = group8_isum(qv[0] + qv[1] + qv[2] + qv[3]);
+                    if ((lane & 7) == 0) store_scales(q, row, c / QK, q.ld_ds, d, sq);
+                }
+            };
+            quantize(std::true_type{});
+            if (__builtin_amdgcn_ballot_w64(!fast) != 0) quantize(std::false_type{});
         }
 #pragma unroll
         for (int it = 0; it < NIT; ++it)
@@ -357,6 +409,7 @@ hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
     if (M == 0) return hipSuccess;
     int vec4 = ((ldx & 3) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     if (y && ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0)) vec4 |= 2;
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) vec4 |= 4;
     if (H <= 0 || H % QK != 0 || H > LN_MAXIT * 256 || (!q && !y)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)std::min<int64_t>((M + 3) / 4, LN_MAX_BLOCKS));
     const bool quant = q != nullptr;

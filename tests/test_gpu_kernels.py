@@ -100,6 +100,65 @@ def test_layernorm_quantize(orc, M, H, ldx, has_w, has_b):
     assert np.array_equal(host(y2), yg)
 
 
+def _same_or_both_nan(a, b):
+    return np.array_equal(a, b, equal_nan=True)
+
+
+def test_quantize_q8_1_nan_and_inf_blocks(orc):
+    """Blocks with NaNs (one, or all 32: amax 0, as a running max from 0
+    takes it), infinities and values whose 127 / amax overflows."""
+    x = np.random.default_rng(11).standard_normal((6, 256)).astype(np.float32)
+    x[0, 0:32] = np.nan
+    x[1, 32 + 5] = np.nan
+    x[2, 64 + 7] = np.inf
+    x[3, 96 + 1] = -np.inf
+    x[4, 128:160] = 0.0
+    x[4, 128:132] = [1e-38, -2e-38, 3e-39, 0.0]
+    x[5, 160:192] = -0.0
+    x[5, 192:224] = np.float32(2.0 ** -110)
+    qs, ds = _quant_gpu(x, 256)
+    rq, rd = orc.quantize_q8_1(x, 256)
+    assert_same(host(qs), rq, "qs")
+    assert_same(host(ds).view(np.uint16), rd, "ds")
+
+
+def test_layernorm_quantize_special_blocks(orc):
+    """LayerNorm + Q8_1 where blocks leave the fast form's domain -- a NaN
+    input row, w = inf and w = NaN columns, blocks of w = 0 with tiny or
+    zero b (amax below 2^-100, or 127 / amax overflowing) -- next to
+    ordinary rows: the same bytes as the oracle's LayerNorm then quantizer."""
+    H, M = 1152, 40
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((M, H)) * 2 + 0.3).astype(np.float32)
+    w = rng.normal(1, 0.02, H).astype(np.float32)
+    b = rng.normal(0, 0.02, H).astype(np.float32)
+    x[3, 100] = np.nan
+    w[200] = np.inf
+    w[300] = np.nan
+    w[320:352] = 0.0
+    b[320:352] = 0.0
+    b[321] = 1e-38
+    w[352:384] = 0.0
+    b[352:384] = np.float32(2.0 ** -110)
+    w[384:416] = 0.0
+    b[384:416] = 0.0
+    for m_rows in (M, 5000):  # registers for w and b; w and b in LDS
+        xs = np.ascontiguousarray(np.tile(x, (m_rows // M + 1, 1))[:m_rows])
+        say(f"layernorm special blocks M={m_rows}")
+        xd, wd, bd = dev(xs), dev(w), dev(b)
+        qs = empty((m_rows, H), torch.int8)
+        ds = empty((m_rows, H // 32, 2), torch.int16)
+        y = empty((m_rows, H), torch.float32)
+        s2x.call("s2x_layernorm_quantize_q8_1", ptr(xd), H, m_rows, H, ptr(wd), ptr(bd),
+                 ctypes.c_float(1e-6), ptr(qs), ptr(ds), ptr(y), H, stream())
+        yg = host(y)
+        ref = orc.layernorm(xs, w, b, 1e-6)
+        assert _same_or_both_nan(yg, ref), "layernorm"
+        rq, rd = orc.quantize_q8_1(ref)
+        assert_same(host(qs), rq, "ln qs")
+        assert_same(host(ds).view(np.uint16), rd, "ln ds")
+
+
 def _weight(raw, k_pad, n):
     w = ctypes.c_void_p()
     s2x.call("s2x_weight_create", raw.ctypes.data, 1, k_pad, n, None, ctypes.byref(w))
