@@ -569,4 +569,15 @@ int s2x_gguf_text_weights(s2x_gguf *g, s2x_text_weights *w) {
     return S2X_OK;
 }
 
+int s2x_gguf_score_params(s2x_gguf *g, float *logit_scale, float *logit_bias) {
+    if (!g || !logit_scale || !logit_bias) return fail(S2X_ERR_INVALID_ARG, "gguf_score_params: null argument");
+    // mm.logit_scale / mm.logit_bias: one F32 value each (src/siglip2_score.cpp:71-72)
+    const float *s = nullptr, *b = nullptr;
+    int st;
+    if ((st = bind_vec(g, "mm.logit_scale", 1, &s)) || (st = bind_vec(g, "mm.logit_bias", 1, &b))) return st;
+    *logit_scale = s[0];
+    *logit_bias = b[0];
+    return S2X_OK;
+}
+
 }  // extern "C"

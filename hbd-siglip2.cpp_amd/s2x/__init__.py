@@ -166,6 +166,7 @@ _sig("s2x_gguf_open", [ctypes.c_char_p, ctypes.POINTER(_p)])
 _sig("s2x_gguf_close", [_p], None)
 _sig("s2x_gguf_vision_weights", [_p, ctypes.POINTER(VisionWeights)])
 _sig("s2x_gguf_text_weights", [_p, ctypes.POINTER(TextWeights)])
+_sig("s2x_gguf_score_params", [_p, ctypes.POINTER(_f32), ctypes.POINTER(_f32)])
 _sig("s2x_text_create", [ctypes.POINTER(TextWeights), ctypes.POINTER(_p)])
 _sig("s2x_text_destroy", [_p], None)
 _sig("s2x_text_set_stream", [_p, _p])

@@ -406,6 +406,10 @@ int s2x_gguf_open(const char *path, s2x_gguf **out);
 void s2x_gguf_close(s2x_gguf *g);
 int s2x_gguf_vision_weights(s2x_gguf *g, s2x_vision_weights *out);
 int s2x_gguf_text_weights(s2x_gguf *g, s2x_text_weights *out);
+/* The contrastive head's scalars mm.logit_scale (exponentiated by the
+ * scorer) and mm.logit_bias (read_score_params,
+ * src/siglip2_score.cpp:17-74). */
+int s2x_gguf_score_params(s2x_gguf *g, float *logit_scale, float *logit_bias);
 
 typedef struct s2x_vision s2x_vision;
 typedef struct s2x_text s2x_text;

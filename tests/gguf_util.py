@@ -141,3 +141,9 @@ def text_tensors(hm):
     for i, L in enumerate(hm.layers):
         ts += _layer_tensors("t", i, L, H, F, Fp)
     return kv, ts
+
+
+def score_tensors(logit_scale, logit_bias):
+    """The contrastive head's scalars as the converter writes them: F32 [1]."""
+    return [_f32("mm.logit_scale", np.array([logit_scale], np.float32), [1]),
+            _f32("mm.logit_bias", np.array([logit_bias], np.float32), [1])]

@@ -327,3 +327,30 @@ def test_gguf_rejects_non_power_of_two_alignment(tmp_path):
     write_gguf(path, kv + [("general.alignment", GT_U32_, 48)], ts)
     st, g = _open(path)
     assert st != 0 and "alignment" in s2x.lib.s2x_last_error().decode()
+
+
+def test_gguf_score_params(tmp_path):
+    """mm.logit_scale / mm.logit_bias come back as written; a file without
+    them is an error, not zeros."""
+    from gguf_util import score_tensors
+    hm = synth.text_model(SMALL_T, seed=3)
+    kv, ts = text_tensors(hm)
+    path = tmp_path / "s.gguf"
+    write_gguf(path, kv, ts + score_tensors(2.302585, -10.25))
+    st, g = _open(path)
+    assert st == 0
+    try:
+        sc, bi = ctypes.c_float(), ctypes.c_float()
+        assert s2x.lib.s2x_gguf_score_params(g, ctypes.byref(sc), ctypes.byref(bi)) == 0
+        assert sc.value == np.float32(2.302585) and bi.value == np.float32(-10.25)
+    finally:
+        s2x.lib.s2x_gguf_close(g)
+    path2 = tmp_path / "n.gguf"
+    write_gguf(path2, kv, ts)
+    st, g = _open(path2)
+    try:
+        sc, bi = ctypes.c_float(), ctypes.c_float()
+        assert s2x.lib.s2x_gguf_score_params(g, ctypes.byref(sc), ctypes.byref(bi)) != 0
+        assert b"mm.logit_scale" in s2x.lib.s2x_last_error()
+    finally:
+        s2x.lib.s2x_gguf_close(g)
