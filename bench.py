@@ -217,13 +217,13 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,0.02) Q8_0 weights, uniform[-1,1] patches)",
-        "config": {"workload": "SigLIP2-so400m vision tower, 27 blocks, Q8_0, batch 32 x 729 "
-                               "patches (27x27), probe pooling", "global_batch": B,
+        "config": {"workload": f"SigLIP2-so400m vision tower, 27 blocks, Q8_0, batch {B} x {n_pos} "
+                               f"patches ({gh}x{gw}), probe pooling", "global_batch": B,
                    "seq_len": n_pos, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
-                     "traffic": traffic_per_launch(),
+                     "traffic": traffic_per_launch() if (B, n_pos) == (32, 729) else None,
                      "kernel": KERNEL,
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "launches": int(g_launches)},
