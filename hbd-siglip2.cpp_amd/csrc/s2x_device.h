@@ -300,21 +300,4 @@ __device__ __forceinline__ int xcd_linear(int bid, int G) {
     return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
-// Output tile order: XCD-aware (gfx950 dispatches workgroup i to XCD i % 8,
-// so consecutive tile ids are given to the same XCD) and grouped (GM rows of
-// tiles walk N together) so an XCD's concurrent workgroups share X and W
-// tiles in its L2.
-template <int GM>
-__device__ __forceinline__ void tile_coords(int bid, int G, int m_tiles, int n_tiles,
-                                            int &tm, int &tn) {
-    const int t = xcd_linear(bid, G);
-    const int group_size = GM * n_tiles;
-    const int group = t / group_size;
-    const int first_m = group * GM;
-    const int gm = min(GM, m_tiles - first_m);
-    const int in_group = t - group * group_size;
-    tm = first_m + in_group % gm;
-    tn = in_group / gm;
-}
-
 }  // namespace s2x

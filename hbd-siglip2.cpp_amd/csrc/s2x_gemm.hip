@@ -65,6 +65,7 @@ namespace gemm {
 
 constexpr int BN = 128;  // output tile columns
 constexpr int GM = 8;    // tile-row group of the tile order
+constexpr int RM_N_TILES = 12;  // at most this many column tiles: row-major tile order
 constexpr int BUF_DW3 = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 
 // BM x 128 tiles (BM 128, 64 or 32), waves of 32 TM x 32 TN outputs (BM /
@@ -146,8 +147,17 @@ __device__ __forceinline__ int clip32(int64_t bytes) {
     return (int)(bytes < 0 ? 0 : bytes > 0x7fffffff ? 0x7fffffff : bytes);
 }
 
-// Output tile of logical index T: groups of GM row tiles walk N together.
+// Output tile of logical index T: groups of GM row tiles walk N together;
+// where N has few tiles (N = 1,152: 9), row-major, so the workgroups that
+// share a row tile's X panel (every column tile of it) are dispatched side
+// by side and stream its K blocks through the L2 together (batch-32
+// out-projection and fc2: 31 % and 15 % fewer bytes fetched, same time).
 __device__ __forceinline__ void tile_of(int T, int m_tiles, int n_tiles, int &tm, int &tn) {
+    if (n_tiles <= RM_N_TILES) {
+        tm = T / n_tiles;
+        tn = T - tm * n_tiles;
+        return;
+    }
     const int group_size = GM * n_tiles;
     const int group = T / group_size;
     const int first_m = group * GM;
