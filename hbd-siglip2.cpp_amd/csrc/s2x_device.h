@@ -66,6 +66,8 @@ __device__ __forceinline__ float group_sum(float v) {
 // 0x00-0xff, row_half_mirror 0x141 (lane i <-> 7 - i within 8), row_mirror
 // 0x140 (i <-> 15 - i within 16), row_bcast15 0x142 / row_bcast31 0x143
 // (last lane of the previous row / of lanes 0-31 into the rows of ROW_MASK).
+// dpp_i / dpp_f: lanes outside ROW_MASK read 0 (with a full mask the
+// compiler folds the exchange into the max / add that consumes it).
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
@@ -74,10 +76,14 @@ template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, dpp_i<CTRL, ROW_MASK>(__builtin_bit_cast(int, v)));
 }
+// dpp_d: lanes outside ROW_MASK come back undefined (no zero is written into
+// them first; a 64-bit add takes no DPP operand, so each zero would cost two
+// moves): callers read only the lanes the mask covers.
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ double dpp_d(double v) {
     const long long b = __builtin_bit_cast(long long, v);
-    const int lo = dpp_i<CTRL, ROW_MASK>((int)b), hi = dpp_i<CTRL, ROW_MASK>((int)(b >> 32));
+    const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, ROW_MASK, 0xf, false);
     return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
 // max / sum over aligned groups of 8 lanes, result in every lane of the group
@@ -98,7 +104,10 @@ __device__ __forceinline__ int group8_isum(int v) {
 }
 // Sum over the wave (64 lanes), returned wave-uniform.  The summation order
 // differs from a butterfly; a double sum of f32 terms is exact to ~1e-16
-// relative either way.
+// relative either way.  Row sums in every lane, then rows 1 and 3 add the
+// sums of rows 0 and 2 (row_bcast:15) and rows 2 and 3 add lane 31's
+// (row_bcast:31): lane 63 holds the total; the lanes outside the masks of
+// those two steps are never read again.
 __device__ __forceinline__ double wave_dsum(double v) {
     v = v + dpp_d<0xb1>(v);
     v = v + dpp_d<0x4e>(v);

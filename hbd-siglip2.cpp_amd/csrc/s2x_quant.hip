@@ -185,6 +185,15 @@ constexpr int LN_MAXIT = 8;        // H <= 8 * 256
 constexpr int LN_MAX_BLOCKS = 3072;  // resident-size grid; blocks stride over the rows
 constexpr int64_t LN_WREG_ROWS = 4096;
 
+// Whether pass it holds the lane's columns c .. c + 3 (c = 256 it + 4 lane):
+// with NIT = ceil(H / 256), every pass before the last lies inside the row,
+// so only the last one tests c (a compile-time true elsewhere: no exec-mask
+// branch in those passes).
+template <int NIT>
+__device__ __forceinline__ bool ln_cols(int it, int64_t c, int64_t H) {
+    return it < NIT - 1 || c < H;
+}
+
 // 4 columns per lane per 256-column pass; a missing row (ok false) or a
 // column past H reads as zeros
 template <int NIT>
@@ -195,7 +204,7 @@ __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr,
         const int64_t c = (int64_t)it * 256 + lane * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
-        if (ok && c < H) {
+        if (ok && ln_cols<NIT>(it, c, H)) {
             if (vec4 & 1) {
                 const float4 t = *reinterpret_cast<const float4 *>(xr + c);
                 v[it][0] = t.x; v[it][1] = t.y; v[it][2] = t.z; v[it][3] = t.w;
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
-            if ((vec4 & 4) && c < H) {  // (H % 32 == 0: c + 3 < H)
+            if ((vec4 & 4) && ln_cols<NIT>(it, c, H)) {  // (H % 32 == 0: c + 3 < H)
                 const float4 tw = w ? *reinterpret_cast<const float4 *>(w + c) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
                 const float4 tb = b ? *reinterpret_cast<const float4 *>(b + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 wr[it][0] = tw.x; wr[it][1] = tw.y; wr[it][2] = tw.z; wr[it][3] = tw.w;
@@ -272,7 +281,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
-            if (c < H)
+            if (ln_cols<NIT>(it, c, H))
                 s = s + (((double)v[it][0] + (double)v[it][1]) +
                          ((double)v[it][2] + (double)v[it][3]));
         }
@@ -281,7 +290,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int64_t c = (int64_t)it * 256 + lane * 4;
-            if (c < H) {
+            if (ln_cols<NIT>(it, c, H)) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float t = v[it][j] - mean;
@@ -292,49 +301,58 @@ __global__ __launch_bounds__(256) void k_layernorm(
         const float var = (float)(wave_dsum(s2) / (double)H);
         const float scale = 1.0f / sqrtf(var + eps);
         // every pass normalized first (o), then written; the quantization's
-        // form is chosen once per row
+        // form is chosen once per row.  With both w and b (the model's
+        // LayerNorms) the affine step has no per-element test: the loop is
+        // instantiated for that case and for the general one.
         float o[NIT][4], am[NIT];
+        const auto normalize = [&](auto aff_c) {
+            constexpr bool AFF = decltype(aff_c)::value;
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int64_t c = (int64_t)it * 256 + lane * 4;
-            am[it] = 0.0f;
-            if (c >= H) continue;  // H % 32 == 0: whole 8-lane groups skip together
-            float wa[4], ba[4];
-            if constexpr (WREG) {
+            for (int it = 0; it < NIT; ++it) {
+                const int64_t c = (int64_t)it * 256 + lane * 4;
+                am[it] = 0.0f;
+                if (!ln_cols<NIT>(it, c, H)) continue;  // H % 32 == 0: whole 8-lane groups skip together
+                float wa[4], ba[4];
+                if constexpr (WREG) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        wa[j] = wr[it][j];
+                        ba[j] = br[it][j];
+                    }
+                } else {
+                    const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
+                    const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
+                    wa[0] = wv.x; wa[1] = wv.y; wa[2] = wv.z; wa[3] = wv.w;
+                    ba[0] = bv.x; ba[1] = bv.y; ba[2] = bv.z; ba[3] = bv.w;
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    wa[j] = wr[it][j];
-                    ba[j] = br[it][j];
+                    float t = (v[it][j] - mean) * scale;
+                    if (AFF || w) t = t * wa[j];
+                    if (AFF || b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
+                    o[it][j] = t;
                 }
-            } else {
-                const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
-                const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
-                wa[0] = wv.x; wa[1] = wv.y; wa[2] = wv.z; wa[3] = wv.w;
-                ba[0] = bv.x; ba[1] = bv.y; ba[2] = bv.z; ba[3] = bv.w;
-            }
+                if (WRITE_Y) {
+                    float *yr = y + row * ldy + c;
+                    if (vec4 & 2) {
+                        *reinterpret_cast<float4 *>(yr) = make_float4(o[it][0], o[it][1], o[it][2], o[it][3]);
+                    } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float t = (v[it][j] - mean) * scale;
-                if (w) t = t * wa[j];
-                if (b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
-                o[it][j] = t;
-            }
-            if (WRITE_Y) {
-                float *yr = y + row * ldy + c;
-                if (vec4 & 2) {
-                    *reinterpret_cast<float4 *>(yr) = make_float4(o[it][0], o[it][1], o[it][2], o[it][3]);
-                } else {
+                        for (int j = 0; j < 4; ++j) yr[j] = o[it][j];
+                    }
+                }
+                if (QUANT) {
+                    uint32_t ab = 0;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) yr[j] = o[it][j];
+                    for (int j = 0; j < 4; ++j) ab = max(ab, __builtin_bit_cast(uint32_t, o[it][j]) & 0x7fffffffu);
+                    am[it] = __builtin_bit_cast(float, group8_umax(ab));
                 }
             }
-            if (QUANT) {
-                uint32_t ab = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) ab = max(ab, __builtin_bit_cast(uint32_t, o[it][j]) & 0x7fffffffu);
-                am[it] = __builtin_bit_cast(float, group8_umax(ab));
-            }
-        }
+        };
+        if (w && b)
+            normalize(std::true_type{});
+        else
+            normalize(std::false_type{});
         if constexpr (QUANT) {
             bool fast = true;
 #pragma unroll
@@ -343,7 +361,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
                     const int64_t c = (int64_t)it * 256 + lane * 4;
-                    if (c >= H) continue;
+                    if (!ln_cols<NIT>(it, c, H)) continue;
                     float d, inv;
                     int qv[4];
                     if constexpr (decltype(fast_c)::value) {
