@@ -951,35 +951,58 @@ hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bi
 // ---------------------------------------------------------------------------
 // single-query attention for the MAP probe head (src/siglip2_vision.cpp:
 // 249-295): the probe query against one segment's keys, Q, K and V rounded to
-// f16 as the reference's FA inputs are.  One workgroup per (head, segment).
+// f16 as the reference's FA inputs are.  One workgroup of 1,024 threads per
+// (head, segment): a key per thread for the scores (729 keys: one pass), the
+// max and the sum reduced per wave and then over the 16 waves, and the PV
+// product over 56 key groups x 18 four-column chunks (d_head 72), the groups'
+// partial sums added in group order.  At batch 1 the 16 workgroups are the
+// whole launch, so the work per thread, not the thread count, sets its time.
 // ---------------------------------------------------------------------------
 constexpr int A1_MAXLEN = (int)MAX_SEG_LEN;
-constexpr int A1_GROUPS = 16;  // key groups of the PV pass
+constexpr int A1_NT = 1024;                     // threads per workgroup
+constexpr int A1_NW = A1_NT / 64;               // waves per workgroup
+constexpr int A1_GROUPS = A1_NT / 18;           // key groups of the PV pass (d_head 72)
 
-__global__ __launch_bounds__(256) void k_attn_1q(
+// DH: d_head when known at compile time (the model's 72: the key row's
+// loads all issued before its fmas), 0 for any other (runtime d_head).
+template <int DH>
+__global__ __launch_bounds__(A1_NT) void k_attn_1q(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     int64_t ld, const int32_t *__restrict__ seg_start, const int32_t *__restrict__ seg_len,
-    int n_head, int d_head, float scale, float *__restrict__ out) {
+    int n_head, int d_head_rt, float scale, float *__restrict__ out) {
+    const int d_head = DH ? DH : d_head_rt;
     __shared__ float p[A1_MAXLEN];
-    __shared__ float red[256];
+    __shared__ float red[A1_NW];
     __shared__ float part[A1_GROUPS][128];
+    __shared__ float qf[128];
     const int h = blockIdx.x, sg = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int len = seg_len[sg];
     const int64_t row0 = seg_start[sg];
     const int H = n_head * d_head;
-    __shared__ float qf[128];
     const float *qh = q + h * d_head;
-    if (threadIdx.x < d_head) qf[threadIdx.x] = (float)f32_to_f16(qh[threadIdx.x]);
+    if (tid < d_head) qf[tid] = (float)f32_to_f16(qh[tid]);
     __syncthreads();
     // one key per thread; with d_head % 4 == 0 and 16-byte aligned rows the
     // row is read as float4 (same fma order over d)
     const bool v4 = (d_head % 4 == 0) && (ld % 4 == 0) &&
                     ((reinterpret_cast<uintptr_t>(k) & 15) == 0);
     float mx = -INFINITY;
-    for (int j = threadIdx.x; j < len; j += 256) {
+    for (int j = tid; j < len; j += A1_NT) {
         const float *kr = k + (row0 + j) * ld + h * d_head;
         float acc = 0.0f;
-        if (v4) {
+        if (DH) {
+            float4 t[DH / 4];
+#pragma unroll
+            for (int i = 0; i < DH / 4; ++i) t[i] = *reinterpret_cast<const float4 *>(kr + 4 * i);
+#pragma unroll
+            for (int i = 0; i < DH / 4; ++i) {
+                acc = fmaf(qf[4 * i], (float)f32_to_f16(t[i].x), acc);
+                acc = fmaf(qf[4 * i + 1], (float)f32_to_f16(t[i].y), acc);
+                acc = fmaf(qf[4 * i + 2], (float)f32_to_f16(t[i].z), acc);
+                acc = fmaf(qf[4 * i + 3], (float)f32_to_f16(t[i].w), acc);
+            }
+        } else if (v4) {
             for (int d = 0; d < d_head; d += 4) {
                 const float4 t = *reinterpret_cast<const float4 *>(kr + d);
                 acc = fmaf(qf[d], (float)f32_to_f16(t.x), acc);
@@ -994,37 +1017,37 @@ __global__ __launch_bounds__(256) void k_attn_1q(
         p[j] = s;
         mx = fmaxf(mx, s);
     }
-    red[threadIdx.x] = mx;
+    mx = group_max<64>(mx);
+    if ((tid & 63) == 0) red[wave] = mx;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-        __syncthreads();
-    }
     mx = red[0];
-    __syncthreads();
+#pragma unroll
+    for (int w = 1; w < A1_NW; ++w) mx = fmaxf(mx, red[w]);
     float sum = 0.0f;
-    for (int j = threadIdx.x; j < len; j += 256) {
+    for (int j = tid; j < len; j += A1_NT) {
         const float e = expf(p[j] - mx);
         p[j] = e;
         sum += e;
     }
-    red[threadIdx.x] = sum;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const float den = red[0];
+    sum = group_sum<64>(sum);
+    __syncthreads();  // every wave has read red[] (the max) before it is reused
+    if ((tid & 63) == 0) red[wave] = sum;
+    __syncthreads();  // ... and the p[] writes are visible to the PV pass
+    float den = red[0];
+#pragma unroll
+    for (int w = 1; w < A1_NW; ++w) den = den + red[w];
     // out[d] = sum_j p_j v[j][d] / den: threads = key groups x 4-column
-    // chunks of the head (d_head 72: 14 groups x 18 chunks), each group's
-    // partial sums then added in group order
+    // chunks of the head, each group's partial sums then added in group order
     const int nch = (d_head + 3) / 4;
-    const int ng = min(256 / nch, A1_GROUPS);
-    const int grp = threadIdx.x / nch, ch = threadIdx.x - grp * nch;
+    const int ng = min(A1_NT / nch, A1_GROUPS);
+    const int grp = tid / nch, ch = tid - grp * nch;
     if (grp < ng) {
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const float *vh = v + h * d_head + 4 * ch;
         if (v4 && (reinterpret_cast<uintptr_t>(v) & 15) == 0) {
+            // (unrolled: several rows' loads in flight; each a[i] still
+            // takes its keys in order)
+#pragma unroll 8
             for (int j = grp; j < len; j += ng) {
                 const float4 t = *reinterpret_cast<const float4 *>(vh + (row0 + j) * ld);
                 const float pj = p[j];
@@ -1047,10 +1070,10 @@ __global__ __launch_bounds__(256) void k_attn_1q(
             if (4 * ch + i < d_head) part[grp][4 * ch + i] = a[i];
     }
     __syncthreads();
-    if (threadIdx.x < d_head) {
-        float acc = part[0][threadIdx.x];
-        for (int g = 1; g < ng; ++g) acc = acc + part[g][threadIdx.x];
-        out[(int64_t)sg * H + h * d_head + threadIdx.x] = acc / den;
+    if (tid < d_head) {
+        float acc = part[0][tid];
+        for (int g = 1; g < ng; ++g) acc = acc + part[g][tid];
+        out[(int64_t)sg * H + h * d_head + tid] = acc / den;
     }
 }
 
@@ -1060,7 +1083,8 @@ hipError_t launch_attn_1q(const float *q, const float *k, const float *v, int64_
                           hipStream_t stream) {
     if (n_seg == 0) return hipSuccess;
     if (d_head > 128) return hipErrorInvalidValue;  // the PV partial sums hold 128 dims
-    hipLaunchKernelGGL(k_attn_1q, dim3((unsigned)n_head, (unsigned)n_seg), dim3(256), 0, stream,
+    const bool dh72 = d_head == 72 && ld % 4 == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0;
+    hipLaunchKernelGGL(dh72 ? k_attn_1q<72> : k_attn_1q<0>, dim3((unsigned)n_head, (unsigned)n_seg), dim3(A1_NT), 0, stream,
                        q, k, v, ld, seg_start, seg_len, (int)n_head, (int)d_head, scale, out);
     return hipGetLastError();
 }
