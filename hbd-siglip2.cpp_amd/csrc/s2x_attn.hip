@@ -991,7 +991,7 @@ __global__ __launch_bounds__(A1_NT) void k_attn_1q(
     for (int j = tid; j < len; j += A1_NT) {
         const float *kr = k + (row0 + j) * ld + h * d_head;
         float acc = 0.0f;
-        if (DH) {
+        if constexpr (DH != 0) {
             float4 t[DH / 4];
 #pragma unroll
             for (int i = 0; i < DH / 4; ++i) t[i] = *reinterpret_cast<const float4 *>(kr + 4 * i);
