@@ -102,6 +102,20 @@ __device__ __forceinline__ int group8_isum(int v) {
     v = v + dpp_i<0x4e>(v);
     return v + dpp_i<0x141>(v);
 }
+// the same over aligned groups of 16 lanes (the two 8-lane halves of a
+// row, joined by row_mirror)
+__device__ __forceinline__ float group16_max(float v) {
+    v = group8_max(v);
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+__device__ __forceinline__ uint32_t group16_umax(uint32_t v) {
+    v = group8_umax(v);
+    return max(v, (uint32_t)dpp_i<0x140>((int)v));
+}
+__device__ __forceinline__ int group16_isum(int v) {
+    v = group8_isum(v);
+    return v + dpp_i<0x140>(v);
+}
 // Sum over the wave (64 lanes), returned wave-uniform.  The summation order
 // differs from a butterfly; a double sum of f32 terms is exact to ~1e-16
 // relative either way.  Row sums in every lane, then rows 1 and 3 add the

@@ -185,32 +185,48 @@ constexpr int LN_MAXIT = 8;        // H <= 8 * 256
 constexpr int LN_MAX_BLOCKS = 3072;  // resident-size grid; blocks stride over the rows
 constexpr int64_t LN_WREG_ROWS = 4096;
 
-// Whether pass it holds the lane's columns c .. c + 3 (c = 256 it + 4 lane):
-// with NIT = ceil(H / 256), every pass before the last lies inside the row,
-// so only the last one tests c (a compile-time true elsewhere: no exec-mask
-// branch in those passes).
-template <int NIT>
+// Columns per lane in pass it: 4 (256 columns a pass), or TW in the last
+// pass.  TW 2 serves rows of 256 k + 128 columns (H = 1,152: four passes of
+// 4 columns and one of 2, every lane busy in each) -- the 4-column form's
+// last pass would leave half the lanes idle.  A Q8_1 block is then 8 lanes
+// of a 4-column pass or 16 of a 2-column one.
+template <int NIT, int TW>
+__device__ __forceinline__ constexpr int ln_w(int it) {
+    return it == NIT - 1 ? TW : 4;
+}
+// Whether pass it holds the lane's columns c .. c + ln_w(it) - 1 (c = 256
+// it + ln_w(it) lane): with NIT = ceil(H / 256), every pass before the last
+// lies inside the row, and so does a last pass of 2 columns (H = 256 (NIT -
+// 1) + 128), so only a last pass of 4 tests c (a compile-time true
+// elsewhere: no exec-mask branch in those passes).
+template <int NIT, int TW>
 __device__ __forceinline__ bool ln_cols(int it, int64_t c, int64_t H) {
-    return it < NIT - 1 || c < H;
+    return it < NIT - 1 || TW == 2 || c < H;
 }
 
-// 4 columns per lane per 256-column pass; a missing row (ok false) or a
-// column past H reads as zeros
-template <int NIT>
+// ln_w(it) columns per lane per pass (the rest of v[it] zero); a missing
+// row (ok false) or a column past H reads as zeros
+template <int NIT, int TW>
 __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr, int64_t H,
                                             int lane, bool ok, int vec4) {
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-        const int64_t c = (int64_t)it * 256 + lane * 4;
+        constexpr int W4 = 4;
+        const int W = ln_w<NIT, TW>(it);
+        const int64_t c = (int64_t)it * 256 + lane * W;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[it][j] = 0.0f;
-        if (ok && ln_cols<NIT>(it, c, H)) {
-            if (vec4 & 1) {
+        for (int j = 0; j < W4; ++j) v[it][j] = 0.0f;
+        if (ok && ln_cols<NIT, TW>(it, c, H)) {
+            if ((vec4 & 1) && W == 4) {
                 const float4 t = *reinterpret_cast<const float4 *>(xr + c);
                 v[it][0] = t.x; v[it][1] = t.y; v[it][2] = t.z; v[it][3] = t.w;
+            } else if ((vec4 & 1) && W == 2) {
+                const float2 t = *reinterpret_cast<const float2 *>(xr + c);
+                v[it][0] = t.x; v[it][1] = t.y;
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) v[it][j] = xr[c + j];
+                for (int j = 0; j < W4; ++j)
+                    if (j < W) v[it][j] = xr[c + j];
             }
         }
     }
@@ -231,7 +247,7 @@ __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr,
 // block holding a NaN or an infinity fails too: where none does, every
 // value is finite and at most amax in magnitude, the two-operation
 // rounding's domain, and the amax equals fmaxf's.  The same bits either way.
-template <bool QUANT, bool WRITE_Y, int NIT, bool WREG>
+template <bool QUANT, bool WRITE_Y, int NIT, bool WREG, int TW>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
     const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
@@ -242,14 +258,15 @@ __global__ __launch_bounds__(256) void k_layernorm(
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     // the first row's loads in flight before w and b are fetched
     float v[NIT][4], wr[NIT][4], br[NIT][4];
-    ln_load_row<NIT>(v, x + row * ldx, H, lane, row < M, vec4);
+    ln_load_row<NIT, TW>(v, x + row * ldx, H, lane, row < M, vec4);
     if constexpr (WREG) {
         // few rows per wave: w and b of the lane's own columns in registers,
         // no staging barrier in front of the first row
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
-            const int64_t c = (int64_t)it * 256 + lane * 4;
-            if ((vec4 & 4) && ln_cols<NIT>(it, c, H)) {  // (H % 32 == 0: c + 3 < H)
+            const int W = ln_w<NIT, TW>(it);
+            const int64_t c = (int64_t)it * 256 + lane * W;
+            if ((vec4 & 4) && W == 4 && ln_cols<NIT, TW>(it, c, H)) {  // (H % 32 == 0: c + 3 < H)
                 const float4 tw = w ? *reinterpret_cast<const float4 *>(w + c) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
                 const float4 tb = b ? *reinterpret_cast<const float4 *>(b + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 wr[it][0] = tw.x; wr[it][1] = tw.y; wr[it][2] = tw.z; wr[it][3] = tw.w;
@@ -257,8 +274,8 @@ __global__ __launch_bounds__(256) void k_layernorm(
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    wr[it][j] = w && c + j < H ? w[c + j] : 1.0f;
-                    br[it][j] = b && c + j < H ? b[c + j] : 0.0f;
+                    wr[it][j] = w && j < W && c + j < H ? w[c + j] : 1.0f;
+                    br[it][j] = b && j < W && c + j < H ? b[c + j] : 0.0f;
                 }
             }
         }
@@ -273,26 +290,33 @@ __global__ __launch_bounds__(256) void k_layernorm(
     for (; row < M; row += stride) {  // wave-uniform
         float vn[NIT][4];
         const int64_t next = row + stride;
-        ln_load_row<NIT>(vn, x + next * ldx, H, lane, next < M, vec4);
+        ln_load_row<NIT, TW>(vn, x + next * ldx, H, lane, next < M, vec4);
         // sums in double, as ggml's CPU norm accumulates: the f32 mean and
         // variance then equal the CPU's (the double sum's rounding, whatever
         // its order, is ~1e-16 relative and vanishes in the f32 conversion)
         double s = 0.0;
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
-            const int64_t c = (int64_t)it * 256 + lane * 4;
-            if (ln_cols<NIT>(it, c, H))
-                s = s + (((double)v[it][0] + (double)v[it][1]) +
-                         ((double)v[it][2] + (double)v[it][3]));
+            const int W = ln_w<NIT, TW>(it);
+            const int64_t c = (int64_t)it * 256 + lane * W;
+            if (ln_cols<NIT, TW>(it, c, H)) {
+                if (W == 4)
+                    s = s + (((double)v[it][0] + (double)v[it][1]) +
+                             ((double)v[it][2] + (double)v[it][3]));
+                else
+                    s = s + ((double)v[it][0] + (double)v[it][1]);
+            }
         }
         const float mean = (float)(wave_dsum(s) / (double)H);
         double s2 = 0.0;
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
-            const int64_t c = (int64_t)it * 256 + lane * 4;
-            if (ln_cols<NIT>(it, c, H)) {
+            const int W = ln_w<NIT, TW>(it);
+            const int64_t c = (int64_t)it * 256 + lane * W;
+            if (ln_cols<NIT, TW>(it, c, H)) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    if (j >= W) continue;
                     const float t = v[it][j] - mean;
                     s2 = s2 + (double)(t * t);
                 }
@@ -309,9 +333,10 @@ __global__ __launch_bounds__(256) void k_layernorm(
             constexpr bool AFF = decltype(aff_c)::value;
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
-                const int64_t c = (int64_t)it * 256 + lane * 4;
+                const int W = ln_w<NIT, TW>(it);
+                const int64_t c = (int64_t)it * 256 + lane * W;
                 am[it] = 0.0f;
-                if (!ln_cols<NIT>(it, c, H)) continue;  // H % 32 == 0: whole 8-lane groups skip together
+                if (!ln_cols<NIT, TW>(it, c, H)) continue;  // H % 32 == 0: whole 8-lane groups skip together
                 float wa[4], ba[4];
                 if constexpr (WREG) {
 #pragma unroll
@@ -319,14 +344,23 @@ __global__ __launch_bounds__(256) void k_layernorm(
                         wa[j] = wr[it][j];
                         ba[j] = br[it][j];
                     }
-                } else {
+                } else if (W == 4) {
                     const float4 wv = *reinterpret_cast<const float4 *>(sw + c);
                     const float4 bv = *reinterpret_cast<const float4 *>(sb + c);
                     wa[0] = wv.x; wa[1] = wv.y; wa[2] = wv.z; wa[3] = wv.w;
                     ba[0] = bv.x; ba[1] = bv.y; ba[2] = bv.z; ba[3] = bv.w;
+                } else {
+                    const float2 wv = *reinterpret_cast<const float2 *>(sw + c);
+                    const float2 bv = *reinterpret_cast<const float2 *>(sb + c);
+                    wa[0] = wv.x; wa[1] = wv.y; wa[2] = wa[3] = 1.0f;
+                    ba[0] = bv.x; ba[1] = bv.y; ba[2] = ba[3] = 0.0f;
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    if (j >= W) {
+                        o[it][j] = 0.0f;
+                        continue;
+                    }
                     float t = (v[it][j] - mean) * scale;
                     if (AFF || w) t = t * wa[j];
                     if (AFF || b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
@@ -334,18 +368,22 @@ __global__ __launch_bounds__(256) void k_layernorm(
                 }
                 if (WRITE_Y) {
                     float *yr = y + row * ldy + c;
-                    if (vec4 & 2) {
+                    if ((vec4 & 2) && W == 4) {
                         *reinterpret_cast<float4 *>(yr) = make_float4(o[it][0], o[it][1], o[it][2], o[it][3]);
+                    } else if ((vec4 & 2) && W == 2) {
+                        *reinterpret_cast<float2 *>(yr) = make_float2(o[it][0], o[it][1]);
                     } else {
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) yr[j] = o[it][j];
+                        for (int j = 0; j < 4; ++j)
+                            if (j < W) yr[j] = o[it][j];
                     }
                 }
                 if (QUANT) {
                     uint32_t ab = 0;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) ab = max(ab, __builtin_bit_cast(uint32_t, o[it][j]) & 0x7fffffffu);
-                    am[it] = __builtin_bit_cast(float, group8_umax(ab));
+                    for (int j = 0; j < 4; ++j)
+                        if (j < W) ab = max(ab, __builtin_bit_cast(uint32_t, o[it][j]) & 0x7fffffffu);
+                    am[it] = __builtin_bit_cast(float, W == 4 ? group8_umax(ab) : group16_umax(ab));
                 }
             }
         };
@@ -360,29 +398,40 @@ __global__ __launch_bounds__(256) void k_layernorm(
             const auto quantize = [&](auto fast_c) {
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
-                    const int64_t c = (int64_t)it * 256 + lane * 4;
-                    if (!ln_cols<NIT>(it, c, H)) continue;
+                    const int W = ln_w<NIT, TW>(it);
+                    const int64_t c = (int64_t)it * 256 + lane * W;
+                    if (!ln_cols<NIT, TW>(it, c, H)) continue;
                     float d, inv;
-                    int qv[4];
+                    int qv[4] = {0, 0, 0, 0};
                     if constexpr (decltype(fast_c)::value) {
                         q8_scales(am[it], d, inv);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) qv[j] = q8_round_fast(o[it][j], inv);
+                        for (int j = 0; j < 4; ++j)
+                            if (j < W) qv[j] = q8_round_fast(o[it][j], inv);
                     } else {
                         // the amax as a running fmaxf from 0 takes it (a NaN
                         // is passed over; a block of NaNs has amax 0)
                         float a = 0.0f;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) a = fmaxf(a, fabsf(o[it][j]));
-                        a = group8_max(a);
+                        for (int j = 0; j < 4; ++j)
+                            if (j < W) a = fmaxf(a, fabsf(o[it][j]));
+                        a = W == 4 ? group8_max(a) : group16_max(a);
                         d = a / 127.0f;
                         inv = a != 0.0f ? 127.0f / a : 0.0f;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) qv[j] = q8_round(o[it][j], inv);
+                        for (int j = 0; j < 4; ++j)
+                            if (j < W) qv[j] = q8_round(o[it][j], inv);
                     }
-                    *reinterpret_cast<uint32_t *>(q.qs + row * H + c) = pack4_i8(qv[0], qv[1], qv[2], qv[3]);
-                    const int sq = group8_isum(qv[0] + qv[1] + qv[2] + qv[3]);
-                    if ((lane & 7) == 0) store_scales(q, row, c / QK, q.ld_ds, d, sq);
+                    int sq;
+                    if (W == 4) {
+                        *reinterpret_cast<uint32_t *>(q.qs + row * H + c) = pack4_i8(qv[0], qv[1], qv[2], qv[3]);
+                        sq = group8_isum(qv[0] + qv[1] + qv[2] + qv[3]);
+                    } else {
+                        *reinterpret_cast<uint16_t *>(q.qs + row * H + c) =
+                            (uint16_t)((qv[0] & 0xff) | ((qv[1] & 0xff) << 8));
+                        sq = group16_isum(qv[0] + qv[1]);
+                    }
+                    if ((lane & (32 / W - 1)) == 0) store_scales(q, row, c / QK, q.ld_ds, d, sq);
                 }
             };
             quantize(std::true_type{});
@@ -395,18 +444,18 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
 }
 
-template <int NIT, bool WREG>
+template <int NIT, bool WREG, int TW>
 void launch_ln_cfg(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
                    const float *b, float eps, bool quant, const Q81Out &qo, float *y,
                    int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
     if (quant && y)
-        hipLaunchKernelGGL((k_layernorm<true, true, NIT, WREG>), grid, dim3(256), 0, stream, x, H,
+        hipLaunchKernelGGL((k_layernorm<true, true, NIT, WREG, TW>), grid, dim3(256), 0, stream, x, H,
                            M, ldx, w, b, eps, qo, y, ldy, vec4);
     else if (quant)
-        hipLaunchKernelGGL((k_layernorm<true, false, NIT, WREG>), grid, dim3(256), 0, stream, x,
+        hipLaunchKernelGGL((k_layernorm<true, false, NIT, WREG, TW>), grid, dim3(256), 0, stream, x,
                            H, M, ldx, w, b, eps, qo, y, ldy, vec4);
     else
-        hipLaunchKernelGGL((k_layernorm<false, true, NIT, WREG>), grid, dim3(256), 0, stream, x,
+        hipLaunchKernelGGL((k_layernorm<false, true, NIT, WREG, TW>), grid, dim3(256), 0, stream, x,
                            H, M, ldx, w, b, eps, qo, y, ldy, vec4);
 }
 
@@ -414,11 +463,17 @@ template <int NIT>
 void launch_ln_nit(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
                    const float *b, float eps, bool quant, const Q81Out &qo, float *y,
                    int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
-    // registers for w and b below LN_WREG_ROWS rows (at most ~1.5 rows per wave)
-    if (M <= LN_WREG_ROWS)
-        launch_ln_cfg<NIT, true>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
+    // registers for w and b below LN_WREG_ROWS rows (at most ~1.5 rows per wave);
+    // rows of 256 k + 128 columns end on a pass of 2 columns per lane
+    const bool wreg = M <= LN_WREG_ROWS, tail2 = H % 256 == 128;
+    if (wreg && tail2)
+        launch_ln_cfg<NIT, true, 2>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
+    else if (wreg)
+        launch_ln_cfg<NIT, true, 4>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
+    else if (tail2)
+        launch_ln_cfg<NIT, false, 2>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
     else
-        launch_ln_cfg<NIT, false>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
+        launch_ln_cfg<NIT, false, 4>(x, H, M, ldx, w, b, eps, quant, qo, y, ldy, vec4, grid, stream);
 }
 
 hipError_t launch_layernorm(const float *x, int64_t H, int64_t M, int64_t ldx,
