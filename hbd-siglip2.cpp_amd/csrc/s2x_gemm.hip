@@ -660,8 +660,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     auto compute = [&](const Frag<TM, TN> &f, int kb) {
         const v16f zf = {};
         const v16i zi = {};
-        // c0's bits in every element: folded into the MFMA as its inline
-        // constant operand (a splat written at the use, so that it is)
+        // c0's bits in every element (the latency form's splat; the
+        // throughput form names the inline constant itself, below)
         const v16i magic = 0x3E22F983;
         if constexpr (EPI == EPI_DUMP_I) {
 #pragma unroll
@@ -682,7 +682,24 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 #pragma unroll
             for (int k = 0; k < NSUB; ++k) {
                 const int a = k / TN, b = k % TN;
-                const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], magic, 0, 0, 0);
+                v16i D;
+                if constexpr (!C::LAT) {
+                    // The accumulator operand as the inline constant 1/2pi
+                    // (0x3E22F983) in the instruction: LLVM folds the splat
+                    // only where one MFMA uses it, and otherwise keeps it in
+                    // 16 VGPRs that every block dot reads -- at <= 128 VGPRs
+                    // for 4 waves per SIMD.  Written this way the K loop
+                    // takes ~100 VGPRs.  The one reader of D is the
+                    // conversion MFMA right below, with D exactly as its
+                    // accumulator operand: the dependency the compiler
+                    // itself schedules back to back with no wait states
+                    // (an MFMA whose srcC exactly overlaps the previous
+                    // MFMA's result); no VALU instruction reads D.
+                    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494"
+                                 : "=&v"(D) : "v"(f.a[a]), "v"(f.b[b]));
+                } else {
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], magic, 0, 0, 0);
+                }
                 const v16f I = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, cA),
                                                                     __builtin_bit_cast(v4h, cB),
                                                                     __builtin_bit_cast(v16f, D), 0, 0, 0);
