@@ -657,7 +657,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     // 0..3, lanes 32..63 (slots 4..7) zero: the products sum to -c0
     const v2i cA = {lh ? 0 : (int)0xC45FB000u, lh ? 0 : 0xAA0C};
     const v2i cB = {lh ? 0 : 0x20003C00, lh ? 0 : 0x0800};
-    auto compute = [&](const Frag<TM, TN> &f, int kb) {
+    // hook(): called once the block's last block dot is issued (where the
+    // throughput form reads the next block's fragments)
+    auto compute = [&](const Frag<TM, TN> &f, int kb, auto &&hook) {
         const v16f zf = {};
         const v16i zi = {};
         // c0's bits in every element (the latency form's splat; the
@@ -668,6 +670,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             for (int k = 0; k < NSUB; ++k) {
                 const int a = k / TN, b = k % TN;
                 const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], zi, 0, 0, 0);
+                if (k == NSUB - 1) hook();
                 if (kb == (int)epi.dump_kb) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -700,6 +703,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
                 } else {
                     D = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[a], f.b[b], magic, 0, 0, 0);
                 }
+                if (k == NSUB - 1) hook();
                 const v16f I = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, cA),
                                                                     __builtin_bit_cast(v4h, cB),
                                                                     __builtin_bit_cast(v16f, D), 0, 0, 0);
@@ -841,15 +845,22 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             // every fragment of the stage first, then its blocks in order
             Frag<TM, TN> Fs[KS];
             static_for<KS>([&](auto jc) { load_frag(sb, decltype(jc)::value, Fs[decltype(jc)::value]); });
-            static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value); });
+            static_for<KS>([&](auto jc) { compute(Fs[decltype(jc)::value], kb0 + decltype(jc)::value, [] {}); });
         } else {
             // the next stage's DMA in three parts after blocks 0, 1 and 2:
             // spread over the stage rather than in one burst after the
-            // barrier, when every wave of the CU starts reading fragments
+            // barrier, when every wave of the CU starts reading fragments.
+            // Block j + 1's fragments are read once block j's last block
+            // dot is issued (into the registers of the other fragment set:
+            // the K loop has the VGPRs since the block dots' accumulator
+            // operand is an inline constant).
+            Frag<TM, TN> Fp[2];
+            load_frag(sb, 0, Fp[0]);
             static_for<KS>([&](auto jc) {
                 constexpr int j = decltype(jc)::value;
-                load_frag(sb, j, F);
-                compute(F, kb0 + j);
+                compute(Fp[j & 1], kb0 + j, [&] {
+                    if constexpr (j + 1 < KS) load_frag(sb, j + 1, Fp[(j + 1) & 1]);
+                });
                 if constexpr (j < 3) issue(g + 1, role, std::integral_constant<int, j>{}, std::false_type{});
             });
         }
@@ -868,7 +879,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
             constexpr int j = decltype(jc)::value;
             if (j < nb) {
                 load_frag(sb, j + shift, F);
-                compute(F, kb0 + j);
+                compute(F, kb0 + j, [] {});
             }
         });
     }
