@@ -24,6 +24,7 @@
 #include "s2x_device.h"
 #include "s2x_kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace s2x {
@@ -794,7 +795,10 @@ __global__ __launch_bounds__(64) void k_attn_f64(
 // d of 64 rows touches distinct banks), the scores and then the
 // probabilities as doubles, all in dynamic LDS; no conversion in the inner
 // loops, and a thread tests each probability against zero once for all of
-// its output columns.
+// its output columns.  Launches of few (head, segment) pairs (the text
+// batch: 80) split each pair's queries over up to 4 workgroups (gridDim.z),
+// every one staging the whole segment: the work is fp64 arithmetic and LDS
+// reads per query, and one workgroup per pair leaves most CUs idle.
 constexpr int A64S_P = 73;
 constexpr int A64S_LDS = (3 * A64_T * A64S_P + A64_T * (A64_T + 1) + 2 * A64_T) * 8;
 constexpr int A64S_NT = 1024;                // threads per workgroup
@@ -813,7 +817,10 @@ __global__ __launch_bounds__(A64S_NT) void k_attn_f64_short(
     double *mx_s = &S[A64_T][0], *den_s = mx_s + A64_T;
     const int h = blockIdx.x, sg = blockIdx.y;
     const int len = seg_len[sg];
-    if (len <= 0) return;  // whole workgroup: nothing to write
+    // this workgroup's queries: [qa, qb) of the segment
+    const int q_per = (len + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int qa = (int)blockIdx.z * q_per, qb = min(len, qa + q_per);
+    if (qa >= qb) return;  // whole workgroup: nothing to write
     const int64_t row0 = seg_start[sg];
     const int H = n_head * d_head;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -850,54 +857,70 @@ __global__ __launch_bounds__(A64S_NT) void k_attn_f64_short(
         }
     }
     __syncthreads();
-    // scores: wave w takes queries w + 16 u (u < 4), lane j the key j: four
-    // independent sums (each in d order) share one read of the key's row
+    // scores: wave w takes queries qa + w + 16 u (u < 4), lane j the key j:
+    // four independent sums (each in d order) share one read of the key's row
     const bool key_ok = lane < len && (key_valid == nullptr || key_valid[row0 + lane] != 0);
     static_assert(A64S_NT / 64 * 4 == A64_T, "one query group per wave");
-    if (wave < len) {
-        double acc[4] = {0.0, 0.0, 0.0, 0.0};
-        int qi[4];
+    if (qa + wave < qb) {
+        // U = the wave's queries in range (1 .. 4), a template value so that
+        // no sum is computed for a query of another workgroup
+        const auto scores = [&](auto uc) {
+            constexpr int U = decltype(uc)::value;
+            double acc[U];
+            int qi[U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) qi[u] = wave + 16 * u;
+            for (int u = 0; u < U; ++u) {
+                acc[u] = 0.0;
+                qi[u] = qa + wave + 16 * u;
+            }
 #pragma unroll 8
-        for (int d = 0; d < d_head; ++d) {
-            const double k = ks[lane][d];
+            for (int d = 0; d < d_head; ++d) {
+                const double k = ks[lane][d];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[u] = acc[u] + qs[qi[u]][d] * k;
-        }
+                for (int u = 0; u < U; ++u) acc[u] = acc[u] + qs[qi[u]][d] * k;
+            }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (qi[u] < len) S[qi[u]][lane] = key_ok ? acc[u] * scale : -INFINITY;
+            for (int u = 0; u < U; ++u) S[qi[u]][lane] = key_ok ? acc[u] * scale : -INFINITY;
+        };
+        const int n_u = (qb - qa - wave + 15) / 16;
+        if (n_u >= 4)
+            scores(std::integral_constant<int, 4>{});
+        else if (n_u == 3)
+            scores(std::integral_constant<int, 3>{});
+        else if (n_u == 2)
+            scores(std::integral_constant<int, 2>{});
+        else
+            scores(std::integral_constant<int, 1>{});
     }
     __syncthreads();
-    if (tid < len) {
+    if (tid >= qa && tid < qb) {
         double m = -INFINITY;
         for (int j = 0; j < len; ++j) m = fmax(m, S[tid][j]);
         mx_s[tid] = m;
     }
     __syncthreads();
-    for (int i = tid; i < len * A64_T; i += A64S_NT) {
-        const int q = i >> 6, j = i & 63;
+    for (int i = tid; i < (qb - qa) * A64_T; i += A64S_NT) {
+        const int q = qa + (i >> 6), j = i & 63;
         if (j < len) {
             const double sc = S[q][j];
             S[q][j] = sc == -INFINITY ? 0.0 : exp(sc - mx_s[q]);
         }
     }
     __syncthreads();
-    if (tid < len) {
+    if (tid >= qa && tid < qb) {
         double den = 0.0;
         for (int j = 0; j < len; ++j) den = den + S[tid][j];
         den_s[tid] = den;
     }
     __syncthreads();
-    // PV: thread t takes query t / 16 and the columns d = t % 16 + 16 c, so
-    // a probability read once serves A64S_C outputs
+    // PV: thread t takes query qa + t / 16 and the columns d = t % 16 + 16 c,
+    // so a probability read once serves A64S_C outputs
     {
-        const int q = tid >> 4, d0 = tid & 15;
+        const int q = qa + (tid >> 4), d0 = tid & 15;
         double acc[A64S_C];
 #pragma unroll
         for (int c = 0; c < A64S_C; ++c) acc[c] = 0.0;
-        if (q < len) {
+        if (q < qb) {
 #pragma unroll 2
             for (int j = 0; j < len; ++j) {
                 const double p = S[q][j];
@@ -937,7 +960,11 @@ hipError_t launch_attn_f64(const float *qkv, int64_t ld_qkv, const float *qkv_bi
             if (e != hipSuccess) return e;
             attr_set = true;
         }
-        hipLaunchKernelGGL(k_attn_f64_short, dim3((unsigned)n_head, (unsigned)n_seg),
+        // queries split over up to 4 workgroups while the pairs number
+        // fewer than 256 (5 prompts x 16 heads: 3 each, 240 workgroups)
+        const int64_t pairs = n_head * n_seg;
+        const unsigned qsplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(4, 256 / pairs));
+        hipLaunchKernelGGL(k_attn_f64_short, dim3((unsigned)n_head, (unsigned)n_seg, qsplit),
                            dim3(A64S_NT), A64S_LDS, stream, qkv, ld_qkv, qkv_bias, seg_start, seg_len, key_valid, (int)n_head,
                            (int)d_head, (double)scale, out, ld_out);
         return hipGetLastError();
