@@ -409,6 +409,46 @@ __device__ __forceinline__ void epilogue(float (&acc)[TM][TN][16], float scale, 
                 ? clip32((rmod ? epi.resid_rows : (int64_t)(M - mw)) * epi.ld_resid * 4)
                 : 0,
             BUF_DW3);
+        // Every row of the wave's block inside M and a plain residual (not
+        // the position rows): the lane's first row and its column in the
+        // vector offset (out of range past N), the row steps 8 (r >> 2) +
+        // (r & 3) as scalar offsets -- no address arithmetic per element.
+        // Rows past M stay with the form below, whose vector offsets alone
+        // carry every row.
+        if (mw + 32 * TM <= M && !rmod && EPI != EPI_DUMP_I && EPI != EPI_BIAS_GELU) {
+            const uint32_t sy = (uint32_t)ldy * 4u, sr = (uint32_t)epi.ld_resid * 4u;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b) {
+                    const int n = nw + b * 32 + lr;
+                    const int r0 = a * 32 + 4 * lh;
+                    const uint32_t vy = n < N ? (uint32_t)(r0 * (int)ldy + n) * 4u : OOB;
+                    float res[16];
+                    if constexpr (EPI == EPI_BIAS_RESID) {
+                        const uint32_t vr = n < N ? (uint32_t)(r0 * (int)epi.ld_resid + n) * 4u : OOB;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t dm = (uint32_t)(8 * (r >> 2) + (r & 3));
+                            res[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, vr, dm * sr, 0));
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float v = acc[a][b][r];
+                        if (EPI == EPI_NONE) {
+                            v = v * scale;
+                        } else if (EPI == EPI_BIAS) {
+                            v = fmaf(v, scale, bias_v[b]);
+                        } else if (EPI == EPI_BIAS_RESID) {
+                            v = fmaf(v, scale, bias_v[b]) + res[r];
+                        }
+                        const uint32_t dm = (uint32_t)(8 * (r >> 2) + (r & 3));
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vy, dm * sy, 0);
+                    }
+                }
+            return;
+        }
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
             float res[TN][16];
