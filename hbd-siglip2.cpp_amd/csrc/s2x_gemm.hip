@@ -1184,6 +1184,212 @@ hipError_t launch_gemm_split_k(const WeightView &w, const int8_t *xq, const uint
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// GEMMs of at most 8 rows (the pooling head's one query per image at batch
+// 1, the text head's prompts).  The MFMA forms give each 32 x 32 output
+// block one wave that walks the whole K chain (the head's fc2 at M = 1: 36
+// waves for 135 blocks each), so such a GEMM takes the chain's latency on a
+// few CUs.  Here a workgroup owns CW columns of every row: its threads first
+// compute the int32 block dots of all (column, block) pairs at once -- v_dot4
+// over int8, exact, each W block read once for every row -- into LDS, then
+// one thread per output runs acc = fmaf((float)I_kb, dx_kb * dw_kb, acc) over
+// the blocks in order.  That is the MFMA forms' chain (whose 2^-26 scaling
+// is exact), so the bits are theirs.  CW = 8 columns (plain, bias, GELU and
+// residual epilogues: the head's N = 1,152 GEMMs in 144 workgroups), or 32
+// where the epilogue quantizes 32-column blocks (GELU -> Q8_1).
+// ---------------------------------------------------------------------------
+constexpr int GV_MAX_M = 8;
+constexpr int GV_NT = 256;
+constexpr int GV_IT = 8;    // (column, block) pairs per thread: CW KB <= 2,048
+constexpr int GV_XIT = 12;  // 16-byte X chunks per thread: M K_pad <= 49,152
+constexpr int GV_LDS_MAX = 96 * 1024;
+
+// position of column n's scale in a dT row (WeightView: columns c + j and
+// c + 32 + j of each 64-column group share a 32-bit word)
+__device__ __forceinline__ int gv_dw_pos(int n) { return (n & ~63) | ((n & 31) << 1) | ((n >> 5) & 1); }
+
+template <int CW>
+static int64_t gv_lds_bytes(int64_t M, int64_t K_pad) {
+    const int64_t KB = K_pad / QK;
+    return M * K_pad + 4 * (M * KB + CW * KB + M * CW * KB + M * 32);
+}
+
+template <int CW, int EPI>
+__global__ __launch_bounds__(GV_NT) void k_gemv(const int8_t *__restrict__ xq,
+                                                const uint32_t *__restrict__ xds, int64_t ld_ds,
+                                                const int8_t *__restrict__ wq,
+                                                const uint16_t *__restrict__ wdT, int64_t ldT,
+                                                int K_pad, int M, int N, float *__restrict__ y,
+                                                int64_t ldy, EpiParams epi) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int KB = K_pad / QK, tid = threadIdx.x, n0 = blockIdx.x * CW;
+    int8_t *xs = reinterpret_cast<int8_t *>(lds);                    // [M][K_pad]
+    float *dxs = reinterpret_cast<float *>(lds + (int64_t)M * K_pad);  // [M][KB]
+    float *dws = dxs + M * KB;                                         // [CW][KB], 0 past N
+    float *ib = dws + CW * KB;                                         // [M][CW][KB]
+    float *vr = ib + M * CW * KB;                                      // [M][32] (GELU -> Q8_1)
+
+    // every load issued before the first is awaited: the W blocks of this
+    // thread's pairs (pair i: column i / KB, block i % KB), the X chunks
+    // and both planes of scales
+    int4 wv[GV_IT][2];
+#pragma unroll
+    for (int j = 0; j < GV_IT; ++j) {
+        const int i = tid + j * GV_NT, c = i / KB, kb = i - c * KB;
+        wv[j][0] = wv[j][1] = int4{0, 0, 0, 0};
+        if (i < CW * KB && n0 + c < N) {
+            const int4 *p = reinterpret_cast<const int4 *>(wq + (int64_t)(n0 + c) * K_pad + kb * QK);
+            wv[j][0] = p[0];
+            wv[j][1] = p[1];
+        }
+    }
+    // (unconditional loads of clamped indices, so that none waits behind a
+    // branch: X rows of K_pad bytes back to back, the X ds words of pair i
+    // = (row i / KB, block i % KB), the W scale of pair i)
+    const int xch = M * (K_pad / 16);
+    int4 xv[GV_XIT];
+#pragma unroll
+    for (int j = 0; j < GV_XIT; ++j)
+        xv[j] = reinterpret_cast<const int4 *>(xq)[min(tid + j * GV_NT, xch - 1)];
+    uint32_t dxv[GV_IT];
+    uint16_t dwv[GV_IT];
+#pragma unroll
+    for (int j = 0; j < GV_IT; ++j) {
+        const int i = tid + j * GV_NT;
+        const int ix = min(i, M * KB - 1), iw = min(i, CW * KB - 1);
+        dxv[j] = xds[(int64_t)(ix / KB) * ld_ds + ix % KB];
+        dwv[j] = wdT[(int64_t)(iw % KB) * ldT + gv_dw_pos(min(n0 + iw / KB, N - 1))];
+    }
+    // (the stores as unconditional: a thread past the end rewrites the last
+    // element with the value it already holds -- no branch for the loads to
+    // sink into)
+#pragma unroll
+    for (int j = 0; j < GV_XIT; ++j) reinterpret_cast<int4 *>(xs)[min(tid + j * GV_NT, xch - 1)] = xv[j];
+#pragma unroll
+    for (int j = 0; j < GV_IT; ++j) {
+        const int i = tid + j * GV_NT;
+        const int ix = min(i, M * KB - 1), iw = min(i, CW * KB - 1);
+        dxs[ix] = f16_bits_to_f32((uint16_t)(dxv[j] & 0xffffu));
+        dws[iw] = n0 + iw / KB < N ? f16_bits_to_f32(dwv[j]) : 0.0f;
+    }
+    __syncthreads();
+
+    // the block dots, each W block against every row
+#pragma unroll
+    for (int j = 0; j < GV_IT; ++j) {
+        const int i = tid + j * GV_NT;
+        const int c = i / KB, kb = i - c * KB;
+        for (int m = 0; m < (i < CW * KB ? M : 0); ++m) {
+            const int4 *xp = reinterpret_cast<const int4 *>(xs + (int64_t)m * K_pad + kb * QK);
+            const int4 x0 = xp[0], x1 = xp[1];
+            int d = __builtin_amdgcn_sdot4(x0.x, wv[j][0].x, 0, false);
+            d = __builtin_amdgcn_sdot4(x0.y, wv[j][0].y, d, false);
+            d = __builtin_amdgcn_sdot4(x0.z, wv[j][0].z, d, false);
+            d = __builtin_amdgcn_sdot4(x0.w, wv[j][0].w, d, false);
+            d = __builtin_amdgcn_sdot4(x1.x, wv[j][1].x, d, false);
+            d = __builtin_amdgcn_sdot4(x1.y, wv[j][1].y, d, false);
+            d = __builtin_amdgcn_sdot4(x1.z, wv[j][1].z, d, false);
+            d = __builtin_amdgcn_sdot4(x1.w, wv[j][1].w, d, false);
+            ib[(m * CW + c) * KB + kb] = (float)d;  // |d| <= 2^19: exact
+        }
+    }
+    __syncthreads();
+
+    // the chains: output (m, c) for thread m CW + c
+    const int m = tid / CW, c = tid % CW, n = n0 + c;
+    if (m < M) {
+        const float *ip = ib + (m * CW + c) * KB, *xp = dxs + m * KB, *wp = dws + c * KB;
+        float acc = 0.0f;
+        for (int kb = 0; kb < KB; ++kb) acc = fmaf(ip[kb], xp[kb] * wp[kb], acc);  // dx dw: exact
+        const bool live = n < N;
+        const float bias = EPI != EPI_NONE && live ? epi.bias[n] : 0.0f;
+        float *yo = y + (int64_t)m * ldy + n;
+        if constexpr (EPI == EPI_NONE) {
+            if (live) *yo = acc;
+        } else if constexpr (EPI == EPI_BIAS) {
+            if (live) *yo = acc + bias;
+        } else if constexpr (EPI == EPI_BIAS_GELU) {
+            if (live) *yo = gelu_tanh(acc + bias);
+        } else if constexpr (EPI == EPI_BIAS_RESID) {
+            if (live) *yo = (acc + bias) + epi.resid[(int64_t)m * epi.ld_resid + n];
+        } else if constexpr (EPI == EPI_GELU_Q81) {
+            // columns past N quantize zeros: GELU(+0) = +0
+            vr[m * 32 + c] = live ? gelu_tanh(acc + bias) : 0.0f;
+        }
+    }
+    if constexpr (EPI == EPI_GELU_Q81) {
+        static_assert(CW == 32, "one Q8_1 block of columns per workgroup");
+        __syncthreads();
+        // row m's block n0 / 32, as the MFMA forms' epilogue quantizes it
+        if (tid < M) {
+            const float *v = vr + tid * 32;
+            float a = 0.0f;
+            for (int k = 0; k < 32; ++k) a = fmaxf(a, fabsf(v[k]));
+            const float d = a / 127.0f;
+            const float inv = a != 0.0f ? 127.0f / a : 0.0f;
+            int s = 0;
+            uint32_t *qo = reinterpret_cast<uint32_t *>(epi.q_out8 + (int64_t)tid * epi.q_kpad + n0);
+            for (int k = 0; k < 32; k += 4) {
+                const int q0 = q8_round(v[k], inv), q1 = q8_round(v[k + 1], inv);
+                const int q2 = q8_round(v[k + 2], inv), q3 = q8_round(v[k + 3], inv);
+                qo[k / 4] = pack4_i8(q0, q1, q2, q3);
+                s += q0 + q1 + q2 + q3;
+            }
+            epi.q_ds[(int64_t)tid * epi.q_ldds + n0 / QK] =
+                (uint32_t)f32_to_f16_bits(d) | ((uint32_t)f32_to_f16_bits((float)s * d) << 16);
+        }
+    }
+}
+
+template <int CW, int EPI>
+static hipError_t run_gemv(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                           int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    auto kern = k_gemv<CW, EPI>;
+    static bool attr_set = false;  // idempotent; a racing second call repeats it harmlessly
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, GV_LDS_MAX);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int64_t cols = EPI == EPI_GELU_Q81 ? epi.q_kpad : w.N;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((cols + CW - 1) / CW)), dim3(GV_NT),
+                       (unsigned)gv_lds_bytes<CW>(M, w.K_pad), stream, xq, xds, ld_ds, w.qs, w.dT,
+                       w.ldT, (int)w.K_pad, (int)M, (int)w.N, y, ldy, epi);
+    return hipGetLastError();
+}
+
+// The GEMV form takes M <= 8 rows with a plain, bias, GELU, residual (not
+// the position rows) or GELU -> Q8_1 epilogue and no K split, where its
+// per-thread unrolls and LDS hold the sizes.
+template <int CW>
+static bool gv_fits(int64_t M, const WeightView &w) {
+    const int64_t KB = w.K_pad / QK;
+    return M <= GV_MAX_M && CW * KB <= GV_IT * GV_NT && M * KB <= GV_IT * GV_NT &&
+           M * (w.K_pad / 16) <= GV_XIT * GV_NT && gv_lds_bytes<CW>(M, w.K_pad) <= GV_LDS_MAX;
+}
+static bool use_gemv(int64_t M, const WeightView &w, const EpiParams &epi) {
+    switch (epi.kind) {
+    case EPI_NONE: return epi.kb_split == 0 && gv_fits<8>(M, w);
+    case EPI_BIAS:
+    case EPI_BIAS_GELU: return gv_fits<8>(M, w);
+    case EPI_BIAS_RESID: return epi.resid_rows == 0 && gv_fits<8>(M, w);
+    case EPI_GELU_Q81: return gv_fits<32>(M, w);
+    default: return false;
+    }
+}
+
+template <int E>
+static hipError_t run_gemv_epi(const WeightView &w, const int8_t *xq, const uint32_t *xds, int64_t ld_ds,
+                               int64_t M, float *y, int64_t ldy, const EpiParams &epi, hipStream_t stream) {
+    if constexpr (E == EPI_GELU_Q81)
+        return run_gemv<32, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    else if constexpr (E == EPI_NONE || E == EPI_BIAS || E == EPI_BIAS_GELU || E == EPI_BIAS_RESID)
+        return run_gemv<8, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream);
+    else
+        return hipErrorInvalidValue;  // (use_gemv admits no other epilogue)
+}
+
 // Stage configurations: 4-block stages in a ring of 2.  Wide: 128 x 128
 // tiles, two workgroups per CU, for GEMMs of enough tiles to fill the chip.
 // Small: 64 x 128 tiles in the latency form, for GEMMs of fewer 128 x 128
@@ -1232,9 +1438,10 @@ hipError_t launch_gemm(const WeightView &w, const int8_t *xq, const uint32_t *xd
         C::BM * ld_ds * 4 > 0x7fffffff || C::BM * ldy * 4 > 0x7fffffff ||
         (epi.kb_split != 0 && (epi.kind != EPI_NONE || epi.kb_split < 0 || epi.y_split < M * ldy)))
         return hipErrorInvalidValue;
-#define S2X_RUN(E)                                                                    \
-    (!use_small(M, w.N) ? gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
-                        : run_small<E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream))
+#define S2X_RUN(E)                                                                     \
+    (use_gemv(M, w, epi) ? run_gemv_epi<E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream)  \
+     : !use_small(M, w.N) ? gemm::run<C, E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream) \
+                          : run_small<E>(w, xq, xds, ld_ds, M, y, ldy, epi, stream))
     switch (epi.kind) {
     case EPI_NONE: return S2X_RUN(EPI_NONE);
     case EPI_BIAS: return S2X_RUN(EPI_BIAS);

@@ -271,6 +271,61 @@ def test_qkv_attn_prep_rejects_bad_arguments(weights):
         s2x.lib.s2x_weight_destroy(w)
 
 
+# ------------------------------------------------ at most 8 rows ------------
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("label", ["out", "fc1", "fc2"])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_small_m_gemm_epilogues(orc, weights, label, M):
+    # GEMMs of at most 8 rows (the pooling head's one query per image, the
+    # text head) take the form that computes the block dots side by side and
+    # runs each output's fma chain in one thread: plain, bias, GELU, the
+    # in-place residual and (fc1) GELU -> Q8_1, against the oracle bit for
+    # bit, and the plain rows equal to the same rows of a 9-row GEMM (the
+    # MFMA latency form)
+    raw, N, K, K_pad, bias = weights[label]
+    say(f"small-M gemm {label} M={M}")
+    rng = np.random.default_rng(40 + M)
+    x = rng.standard_normal((9, K)).astype(np.float32)
+    qs, ds = _quant_gpu(x, K_pad)  # M-row GEMMs read the first M rows of the 9
+    bd = dev(bias)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    rdv = dev(res)
+    w = _weight(raw, K_pad, N)
+    try:
+        yg = host(_mm(w, qs, ds, M, N))
+        y9 = host(_mm(w, qs, ds, 9, N))
+        e = s2x.Epilogue()
+        e.kind, e.bias = s2x.EPI_BIAS, bd.data_ptr()
+        yb = host(_mm(w, qs, ds, M, N, e))
+        e.kind = s2x.EPI_BIAS_GELU
+        yq = host(_mm(w, qs, ds, M, N, e))
+        e.kind, e.resid, e.ld_resid = s2x.EPI_BIAS_RESID, rdv.data_ptr(), N
+        _mm(w, qs, ds, M, N, e, rdv)  # in place on the residual rows
+        yr = host(rdv)
+        if label == "fc1":
+            q_out = torch.full((M, INTER_PAD), 0x55, dtype=torch.int8, device="cuda:0")
+            q_ds = torch.full((M, INTER_PAD // 32, 2), 0x5555, dtype=torch.int16, device="cuda:0")
+            e = s2x.Epilogue()
+            e.kind, e.bias = s2x.EPI_GELU_Q81, bd.data_ptr()
+            e.q_out, e.q_ds, e.q_kpad = q_out.data_ptr(), q_ds.data_ptr(), INTER_PAD
+            s2x.call("s2x_mul_mat_q8_0_q8_1", w, ptr(qs), ptr(ds), M, None, 0, ctypes.byref(e),
+                     stream())
+            gq, gd = host(q_out), host(q_ds).view(np.uint16)
+    finally:
+        s2x.lib.s2x_weight_destroy(w)
+    rq, rd = orc.quantize_q8_1(x[:M], K_pad)
+    ref = orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd)
+    assert_same(yg, ref, f"{label} M={M} plain vs oracle")
+    assert_same(yg, y9[:M], f"{label} M={M} plain vs the 9-row GEMM")
+    assert_same(yb, ref + bias, f"{label} M={M} bias")
+    assert_same(yq, orc.gelu(ref + bias), f"{label} M={M} bias + GELU")
+    assert_same(yr, (ref + bias) + res, f"{label} M={M} in-place residual")
+    if label == "fc1":
+        ref_q, ref_d = orc.quantize_q8_1(orc.gelu(ref + bias), INTER_PAD)
+        assert_same(gq, ref_q, f"fc1 M={M} GELU_Q81 quants")
+        assert_same(gd, ref_d, f"fc1 M={M} GELU_Q81 scales")
+
+
 # ------------------------------------------------------------- residuals ----
 @pytest.mark.timeout(300)
 @pytest.mark.parametrize("M", [729, 32 * 729])
