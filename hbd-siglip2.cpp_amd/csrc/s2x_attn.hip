@@ -1016,6 +1016,12 @@ __global__ __launch_bounds__(A1_NT) void k_attn_1q(
                     ((reinterpret_cast<uintptr_t>(k) & 15) == 0);
     float mx = -INFINITY;
     for (int j = tid; j < len; j += A1_NT) {
+        // q is read from LDS in each pass (a broadcast read): hoisted out of
+        // the loop into registers beside the key row it exceeded the 128
+        // registers of a 1,024-thread workgroup and went to scratch memory,
+        // reloaded in the loop (the 729-key batch-1 launch 15.8 -> 11.2 us
+        // with this, same bits)
+        asm volatile("" ::: "memory");
         const float *kr = k + (row0 + j) * ld + h * d_head;
         float acc = 0.0f;
         if constexpr (DH != 0) {
