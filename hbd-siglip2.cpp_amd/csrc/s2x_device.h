@@ -203,7 +203,7 @@ __device__ __forceinline__ bool q8_any_sat(float inv) {
 // Both were checked over those inputs on the CPU
 // (tests/test_q8_scales_division.py).
 __device__ __forceinline__ bool q8_scales_ok(float a) {
-    return a == 0.0f || (a >= 0x1p-100f && a <= 0x1p100f);
+    return (a == 0.0f) | ((a >= 0x1p-100f) & (a <= 0x1p100f));  // (bitwise: no branches)
 }
 __device__ __forceinline__ void q8_scales(float a, float &d, float &inv) {
     const float r127 = 0x1.020408p-7f;  // RN(1/127)

@@ -247,7 +247,10 @@ __device__ __forceinline__ void ln_load_row(float (&v)[NIT][4], const float *xr,
 // block holding a NaN or an infinity fails too: where none does, every
 // value is finite and at most amax in magnitude, the two-operation
 // rounding's domain, and the amax equals fmaxf's.  The same bits either way.
-template <bool QUANT, bool WRITE_Y, int NIT, bool WREG, int TW>
+// AFF: w and b both present (the model's LayerNorms), a kernel of its own:
+// instantiated inside one kernel with the general case, the two affine
+// forms were merged into one with two selects per element.
+template <bool QUANT, bool WRITE_Y, int NIT, bool WREG, int TW, bool AFF>
 __global__ __launch_bounds__(256) void k_layernorm(
     const float *__restrict__ x, int64_t H, int64_t M, int64_t ldx,
     const float *__restrict__ w, const float *__restrict__ b, float eps, Q81Out q,
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(256) void k_layernorm(
         // instantiated for that case and for the general one.
         float o[NIT][4], am[NIT];
         const auto normalize = [&](auto aff_c) {
-            constexpr bool AFF = decltype(aff_c)::value;
+            constexpr bool AFC = decltype(aff_c)::value;
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int W = ln_w<NIT, TW>(it);
@@ -371,8 +374,8 @@ __global__ __launch_bounds__(256) void k_layernorm(
                         continue;
                     }
                     float t = (v[it][j] - mean) * scale;
-                    if (AFF || w) t = t * wa[j];
-                    if (AFF || b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
+                    if (AFC || w) t = t * wa[j];
+                    if (AFC || b) t = t + ba[j];  // skipped, not + 0.0f, which would turn -0 into +0
                     o[it][j] = t;
                 }
                 if (WRITE_Y) {
@@ -396,14 +399,14 @@ __global__ __launch_bounds__(256) void k_layernorm(
                 }
             }
         };
-        if (w && b)
+        if constexpr (AFF)
             normalize(std::true_type{});
         else
             normalize(std::false_type{});
         if constexpr (QUANT) {
             bool fast = true;
 #pragma unroll
-            for (int it = 0; it < NIT; ++it) fast = fast && q8_scales_ok(am[it]);
+            for (int it = 0; it < NIT; ++it) fast = fast & q8_scales_ok(am[it]);  // (no branch per pass)
             const auto quantize = [&](auto fast_c) {
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
@@ -457,15 +460,18 @@ template <int NIT, bool WREG, int TW>
 void launch_ln_cfg(const float *x, int64_t H, int64_t M, int64_t ldx, const float *w,
                    const float *b, float eps, bool quant, const Q81Out &qo, float *y,
                    int64_t ldy, int vec4, dim3 grid, hipStream_t stream) {
-    if (quant && y)
-        hipLaunchKernelGGL((k_layernorm<true, true, NIT, WREG, TW>), grid, dim3(256), 0, stream, x, H,
-                           M, ldx, w, b, eps, qo, y, ldy, vec4);
-    else if (quant)
-        hipLaunchKernelGGL((k_layernorm<true, false, NIT, WREG, TW>), grid, dim3(256), 0, stream, x,
-                           H, M, ldx, w, b, eps, qo, y, ldy, vec4);
+    using KFn = void (*)(const float *, int64_t, int64_t, int64_t, const float *, const float *, float,
+                         Q81Out, float *, int64_t, int);
+    KFn kern;
+    if (w && b)
+        kern = quant && y ? k_layernorm<true, true, NIT, WREG, TW, true>
+               : quant    ? k_layernorm<true, false, NIT, WREG, TW, true>
+                          : k_layernorm<false, true, NIT, WREG, TW, true>;
     else
-        hipLaunchKernelGGL((k_layernorm<false, true, NIT, WREG, TW>), grid, dim3(256), 0, stream, x,
-                           H, M, ldx, w, b, eps, qo, y, ldy, vec4);
+        kern = quant && y ? k_layernorm<true, true, NIT, WREG, TW, false>
+               : quant    ? k_layernorm<true, false, NIT, WREG, TW, false>
+                          : k_layernorm<false, true, NIT, WREG, TW, false>;
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, x, H, M, ldx, w, b, eps, qo, y, ldy, vec4);
 }
 
 template <int NIT>
