@@ -238,11 +238,13 @@ def test_gemm_matches_oracle(orc, gemm_data, label):
 # (fewer than 4 blocks: one partial stage; otherwise the last stage is
 # fetched as the window of the last 4 blocks); ragged N and M leave partial
 # edge tiles.  "small": 6 tiles, the latency form; "wide": 520 tiles of
-# 128 x 128, the throughput form (sampled rows, the last tile's included).
-@pytest.mark.parametrize("form", ["small", "wide"])
+# 128 x 128, the throughput form (sampled rows, the last tile's included);
+# "rows5": 5 rows, the form of block dots side by side and one fma chain per
+# output, with N = 203 ending on a partial group of 8 columns.
+@pytest.mark.parametrize("form", ["small", "wide", "rows5"])
 @pytest.mark.parametrize("KB", [1, 2, 3, 4, 5, 7, 13])
 def test_gemm_short_k(orc, KB, form):
-    M, N = (300, 200) if form == "small" else (8300, 1000)
+    M, N = {"small": (300, 200), "wide": (8300, 1000), "rows5": (5, 203)}[form]
     K_pad = 32 * KB
     K = K_pad - (5 if KB > 1 else 0)
     say(f"gemm short K: KB={KB} M={M} N={N}")
@@ -250,7 +252,7 @@ def test_gemm_short_k(orc, KB, form):
     raw = synth.quantize_q8_0(rng.normal(0, 0.02, (N, K)).astype(np.float32), K_pad)
     x = rng.standard_normal((M, K)).astype(np.float32)
     qs, ds = _quant_gpu(x, K_pad)
-    rows = np.arange(M) if form == "small" else np.unique(np.concatenate(
+    rows = np.arange(M) if form != "wide" else np.unique(np.concatenate(
         [rng.choice(M, 200, replace=False), np.arange(M - 44, M)]))
     rq, rd = orc.quantize_q8_1(x[rows], K_pad)
     ref = orc.mul_mat_q8_0_q8_1(raw, K_pad, N, rq, rd)
